@@ -1,0 +1,114 @@
+// Shared state and helpers of libgen9blas (not installed). Everything here has hidden visibility.
+//
+// Roles (reference: lib/src/internal.h, lib/src/core.c, lib/kcl.c):
+// - error state: the text of the last error and the gen9blas_status of the current call;
+// - one-time init: device selection, the HIP stream, profiling events;
+// - operand resolution: device memory is used in place, host memory is staged through growing device work buffers;
+// - synchronization: one wait per call (or none in no-wait mode), then copies of staged results back to the host.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+#include "gen9blas.h"
+#include "gen9blas_hip.h"
+
+#define G9_HIDDEN __attribute__((visibility("hidden")))
+
+namespace g9 {
+
+// ---- error state (reference: lib/src/internal.h:28-35, lib/src/core.c:385-392) ----
+G9_HIDDEN extern char errbuf[1200];
+G9_HIDDEN extern int gst;            // status of the current call
+G9_HIDDEN extern int last_zc;        // zero-copy bits of the last level 3 call
+G9_HIDDEN extern double last_ms;     // gen9blas_last_time_ms
+G9_HIDDEN int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+G9_HIDDEN int hip_fail(hipError_t e, const char *what, const char *file, int line);
+#define G9_FAIL(code, ...) return ::g9::fail((code), __VA_ARGS__)
+#define G9_HIP(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) return ::g9::hip_fail(e_, #x, __FILE__, __LINE__); } while (0)
+#define G9_TRY(x) do { int r_ = (x); if (r_) return r_; } while (0)
+
+// ---- runtime ----
+G9_HIDDEN extern hipStream_t stream;
+G9_HIDDEN extern int device;
+G9_HIDDEN extern int profile;        // GEN9BLAS_PROFILE set: time the main kernels with events
+G9_HIDDEN extern int nowait;         // gen9blas_set_nowait
+G9_HIDDEN extern int num_cus;
+// Start of every entry point: reset the status, make sure the device is open and current. 0 or an error.
+G9_HIDDEN int begin();
+G9_HIDDEN double now_s();
+
+// ---- operands ----
+enum Slot { SLOT_A = 0, SLOT_B, SLOT_C, SLOT_P, SLOT_Q, NSLOTS };
+// Device scratch owned by the library, grown on demand and kept between calls (the reference's work buffers,
+// reference: lib/src/core.c:272-277). Growing waits for queued work first.
+G9_HIDDEN int scratch(int slot, size_t bytes, void **p);
+
+// A vector or matrix operand. Matrices are described as rows × cols elements with row stride ld; vectors as
+// rows = 1, cols = span (elements from the lowest address), ld = cols.
+struct Operand {
+    const void *host = nullptr;  // caller's pointer
+    void *dev = nullptr;         // pointer the kernels use
+    long long ld = 0;            // row stride (elements) the kernels must use; may differ from the caller's for staged matrices
+    long long caller_ld = 0;
+    long long rows = 0, cols = 0;
+    int es = 0;
+    bool zc = false;             // caller's memory used in place
+    bool written = false;        // kernels write it: copy back after the wait when staged
+};
+// Resolves op (host, rows, cols, ld, es set by the caller) for the kernels. Device memory is used in place; host
+// memory goes into the work buffer `slot`, with a row stride rounded up to 16 bytes when `repitch` (copy_in: with
+// the data; otherwise the buffer contents are undefined, as for outputs not read).
+G9_HIDDEN int resolve(Operand &op, int slot, bool copy_in, bool written, bool repitch);
+// 1 if p .. p+bytes lies in one device allocation.
+G9_HIDDEN int is_device(const void *p, size_t bytes);
+// End of a call: in no-wait mode with every operand in place, returns at once; otherwise waits for the stream and
+// copies staged written operands back.
+G9_HIDDEN int finish(Operand *ops, int n);
+// Waits for the stream (no copies). 0 or an error.
+G9_HIDDEN int wait_stream();
+
+// Kernel timing for GEN9BLAS_PROFILE=1: events around the main kernels of a call.
+G9_HIDDEN void prof_begin();
+G9_HIDDEN void prof_end();
+G9_HIDDEN void prof_collect(double t_call_start);
+
+// Scalars for kernels: double for FP64, float otherwise (reference: lib/src/core.c:356-359).
+inline int elem_size(int type) { return type == GEN9BLAS_S ? 4 : type == GEN9BLAS_D ? 8 : 2; }
+
+}  // namespace g9
+
+// ---- kernel launchers (one translation unit each) ----
+namespace g9 {
+struct GemmCall {
+    int type;                      // GEN9BLAS_H / HS / S / D
+    int tA, tB, M, N, K, count;
+    double alpha, beta;
+    const void *A; long long lda, sA;
+    const void *B; long long ldb, sB;
+    void *C; long long ldc, sC;
+};
+G9_HIDDEN int launch_gemm(const GemmCall &c);
+struct SkinnyCall {
+    int type;                      // GEN9BLAS_H / HS / S
+    int M, N, K;                   // C (M×N) = alpha·a·wᵀ + beta·C, a M×K, w N×K, both K-contiguous
+    double alpha, beta;
+    const void *a; long long sam;  // a[m][k] = a[m·sam + k]
+    const void *w; long long swn;  // w[n][k] = w[n·swn + k]
+    void *C; long long scm, scn;   // C[m][n] = C[m·scm + n·scn]
+};
+G9_HIDDEN int launch_skinny(const SkinnyCall &c);
+// Level 1/2: element i of a vector is at p[o + i·inc], o = (n-1)·(-inc) for inc < 0.
+G9_HIDDEN int launch_axpy(int es, int n, double a, const void *x, long long ox, long long ix, void *y, long long oy, long long iy);
+G9_HIDDEN int launch_scal(int es, int n, double a, void *x, long long ox, long long ix);
+G9_HIDDEN int launch_copy(int es, int n, const void *x, long long ox, long long ix, void *y, long long oy, long long iy);
+G9_HIDDEN int launch_rot(int es, int n, void *x, long long ox, long long ix, void *y, long long oy, long long iy,
+                         double h11, double h12, double h21, double h22, int swap);
+// mode 0: Σ x·y, 1: Σ|x|, 2: Σ x² (FP64). Result written to *dev_result (device double).
+G9_HIDDEN int launch_reduce(int es, int mode, int n, const void *x, long long ox, long long ix, const void *y, long long oy,
+                            long long iy, double *dev_result);
+G9_HIDDEN int launch_iamax(int es, int n, const void *x, long long ox, long long ix, long long *dev_result);
+G9_HIDDEN int launch_gemv(int es, int trans, int M, int N, double alpha, const void *A, long long lda, const void *x, long long ox,
+                          long long ix, double beta, void *y, long long oy, long long iy);
+G9_HIDDEN int launch_ger(int es, int M, int N, double alpha, const void *x, long long ox, long long ix, const void *y,
+                         long long oy, long long iy, void *A, long long lda);
+}  // namespace g9

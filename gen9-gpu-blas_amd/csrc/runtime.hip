@@ -1,0 +1,337 @@
+// HIP runtime glue of libgen9blas: init, errors, memory resolution, work buffers, waiting, profiling.
+//
+// Replaces two layers of the reference: its OpenCL-subset device runtime that built i915 command buffers
+// (reference: lib/kcl.c) and the glue above it (reference: lib/src/core.c). On MI355X the HIP runtime already does
+// command submission, so what remains is the contract of the glue:
+// - gen9blas_init runs once per process under pthread_once and a failure is final (reference: core.c:205-219);
+// - operands are resolved per call (reference: get_obj, core.c:328-340): device memory is used in place; host memory
+//   (pageable or pinned) is copied into growing device work buffers, with matrix rows re-pitched to 16 bytes so the
+//   vectorized kernels always apply, and written results are copied back after the one wait of the call
+//   (reference: to_host, core.c:363-367);
+// - errors map to gen9blas_status codes (reference: internal.h:28-35).
+#include "internal.h"
+#include <pthread.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+#include <map>
+#include <mutex>
+
+namespace g9 {
+
+char errbuf[1200];
+int gst;
+int last_zc;
+double last_ms;
+hipStream_t stream;
+int device = -1;
+int profile;
+int nowait;
+int num_cus;
+
+double now_s() {
+    struct timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return t.tv_sec + t.tv_nsec * 1e-9;
+}
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(errbuf, sizeof errbuf, fmt, ap);
+    va_end(ap);
+    gst = code;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what, const char *file, int line) {
+    const int code = e == hipErrorOutOfMemory ? GEN9BLAS_ERR_OUT_OF_MEMORY : GEN9BLAS_ERR;
+    const char *base = strrchr(file, '/');
+    return fail(code, "%s:%d: %s = %s", base ? base + 1 : file, line, what, hipGetErrorString(e));
+}
+
+// ---------------- init ----------------
+static pthread_once_t init_once = PTHREAD_ONCE_INIT;
+static int init_status = GEN9BLAS_ERR_NO_DEVICE;
+static char init_err[sizeof errbuf];
+static int arch;
+static hipEvent_t ev_start, ev_stop;
+static bool ev_used;
+
+static int init_impl() {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        G9_FAIL(GEN9BLAS_ERR_NO_DEVICE, "no HIP device (%s)", e != hipSuccess ? hipGetErrorString(e) : "count 0");
+    }
+    int d = 0;
+    const char *env = getenv("GEN9BLAS_DEVICE");
+    if (env) d = atoi(env);
+    else if (hipGetDevice(&d) != hipSuccess) d = 0;
+    if (d < 0 || d >= n) G9_FAIL(GEN9BLAS_ERR_NO_DEVICE, "GEN9BLAS_DEVICE=%d: %d devices", d, n);
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, d) != hipSuccess) G9_FAIL(GEN9BLAS_ERR_NO_DEVICE, "hipGetDeviceProperties(%d) failed", d);
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        G9_FAIL(GEN9BLAS_ERR_NO_DEVICE, "device %d is %s; this build has gfx950 kernels only", d, p.gcnArchName);
+    if (hipSetDevice(d) != hipSuccess) G9_FAIL(GEN9BLAS_ERR_NO_DEVICE, "hipSetDevice(%d) failed", d);
+    device = d;
+    arch = 950;
+    num_cus = p.multiProcessorCount;
+    // Default flags and default priority: the stream orders itself with the legacy null stream.
+    if (hipStreamCreate(&stream) != hipSuccess) G9_FAIL(GEN9BLAS_ERR_NO_DEVICE, "hipStreamCreate failed");
+    if (hipEventCreate(&ev_start) != hipSuccess || hipEventCreate(&ev_stop) != hipSuccess)
+        G9_FAIL(GEN9BLAS_ERR_NO_DEVICE, "hipEventCreate failed");
+    profile = getenv("GEN9BLAS_PROFILE") != nullptr;
+    errbuf[0] = 0;
+    return 0;
+}
+
+static void init_run() {
+    init_status = init_impl();
+    if (init_status) snprintf(init_err, sizeof init_err, "%s", errbuf[0] ? errbuf : "GPU initialization failed");
+}
+
+int begin() {
+    gst = 0;
+    pthread_once(&init_once, init_run);
+    if (init_status) {
+        snprintf(errbuf, sizeof errbuf, "%s", init_err);
+        gst = GEN9BLAS_ERR_NO_DEVICE;
+        return gst;
+    }
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess || cur != device) G9_HIP(hipSetDevice(device));
+    return 0;
+}
+
+// ---------------- work buffers ----------------
+static void *sbuf[NSLOTS];
+static size_t ssize[NSLOTS];
+
+int scratch(int slot, size_t bytes, void **p) {
+    if (bytes == 0) bytes = 256;
+    if (ssize[slot] < bytes) {
+        if (sbuf[slot]) {
+            G9_HIP(hipStreamSynchronize(stream));
+            G9_HIP(hipFree(sbuf[slot]));
+            sbuf[slot] = nullptr;
+            ssize[slot] = 0;
+        }
+        size_t nb = (bytes + (1u << 21) - 1) & ~(size_t)((1u << 21) - 1);
+        hipError_t e = hipMalloc(&sbuf[slot], nb);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            sbuf[slot] = nullptr;
+            G9_FAIL(GEN9BLAS_ERR_OUT_OF_MEMORY, "hipMalloc(%zu) for a work buffer: %s", nb, hipGetErrorString(e));
+        }
+        ssize[slot] = nb;
+    }
+    *p = sbuf[slot];
+    return 0;
+}
+
+// ---------------- operand resolution ----------------
+int is_device(const void *p, size_t bytes) {
+    if (!p) return 0;
+    hipPointerAttribute_t a;
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();   // plain host memory: the query fails, clear the error
+        return 0;
+    }
+    if (a.type != hipMemoryTypeDevice && a.type != hipMemoryTypeManaged && a.type != hipMemoryTypeUnified) return 0;
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) != hipSuccess) {
+        (void)hipGetLastError();
+        return 1;   // device memory whose extent the runtime does not report: trust the caller
+    }
+    return (uintptr_t)p + bytes <= (uintptr_t)base + size;
+}
+
+int resolve(Operand &op, int slot, bool copy_in, bool written, bool repitch) {
+    const size_t es = op.es;
+    const size_t span = ((size_t)(op.rows - 1) * (size_t)op.caller_ld + (size_t)op.cols) * es;
+    op.written = written;
+    if (is_device(op.host, span)) {
+        op.dev = const_cast<void *>(op.host);
+        op.ld = op.caller_ld;
+        op.zc = true;
+        return 0;
+    }
+    op.zc = false;
+    if (repitch && op.rows > 1) {
+        const size_t pitch = ((size_t)op.cols * es + 15) / 16 * 16;
+        op.ld = (long long)(pitch / es);
+        G9_TRY(scratch(slot, pitch * (size_t)op.rows, &op.dev));
+        if (copy_in)
+            G9_HIP(hipMemcpy2DAsync(op.dev, pitch, op.host, (size_t)op.caller_ld * es, (size_t)op.cols * es,
+                                    (size_t)op.rows, hipMemcpyHostToDevice, stream));
+    } else {
+        op.ld = op.caller_ld;
+        G9_TRY(scratch(slot, span, &op.dev));
+        if (copy_in) G9_HIP(hipMemcpyAsync(op.dev, op.host, span, hipMemcpyHostToDevice, stream));
+    }
+    return 0;
+}
+
+int wait_stream() {
+    G9_HIP(hipStreamSynchronize(stream));
+    G9_HIP(hipGetLastError());
+    return 0;
+}
+
+int finish(Operand *ops, int n) {
+    bool all_zc = true;
+    for (int i = 0; i < n; i++) all_zc &= ops[i].zc || !ops[i].host;
+    if (nowait && all_zc) {
+        G9_HIP(hipGetLastError());   // launch errors are reported at once; kernel errors at gen9blas_flush
+        return 0;
+    }
+    for (int i = 0; i < n; i++) {
+        const Operand &o = ops[i];
+        if (!o.written || o.zc || !o.host) continue;
+        const size_t es = o.es;
+        if (o.ld != o.caller_ld && o.rows > 1)
+            G9_HIP(hipMemcpy2DAsync(const_cast<void *>(o.host), (size_t)o.caller_ld * es, o.dev, (size_t)o.ld * es,
+                                    (size_t)o.cols * es, (size_t)o.rows, hipMemcpyDeviceToHost, stream));
+        else
+            G9_HIP(hipMemcpyAsync(const_cast<void *>(o.host), o.dev,
+                                  ((size_t)(o.rows - 1) * (size_t)o.caller_ld + (size_t)o.cols) * es,
+                                  hipMemcpyDeviceToHost, stream));
+    }
+    return wait_stream();
+}
+
+// ---------------- profiling ----------------
+void prof_begin() {
+    if (profile) {
+        (void)hipEventRecord(ev_start, stream);
+        ev_used = true;
+    }
+}
+void prof_end() {
+    if (profile && ev_used) (void)hipEventRecord(ev_stop, stream);
+}
+void prof_collect(double t_call_start) {
+    last_ms = (now_s() - t_call_start) * 1e3;
+    if (profile && ev_used && !nowait) {
+        float ms = 0;
+        if (hipEventSynchronize(ev_stop) == hipSuccess && hipEventElapsedTime(&ms, ev_start, ev_stop) == hipSuccess)
+            last_ms = ms;
+        else
+            (void)hipGetLastError();
+    }
+    ev_used = false;
+}
+
+// ---------------- pinned host memory registry (gen9blas_alloc / gen9blas_is_usm) ----------------
+static std::mutex alloc_mu;
+static std::map<uintptr_t, size_t> &blocks() {
+    static std::map<uintptr_t, size_t> m;
+    return m;
+}
+
+}  // namespace g9
+
+using namespace g9;
+
+extern "C" {
+
+int gen9blas_version(void) { return GEN9BLAS_VERSION; }
+
+int gen9blas_init(void) { return begin(); }
+
+int gen9blas_device_gen(void) { return begin() ? 0 : 9; }
+
+int gen9blas_device_arch(void) { return begin() ? 0 : arch; }
+
+int gen9blas_has(int f) {
+    if (begin()) return 0;
+    switch (f) {
+    case GEN9BLAS_FEAT_FP16:
+    case GEN9BLAS_FEAT_FP32:
+    case GEN9BLAS_FEAT_FP64: return 1;
+    default: return 0;   // the ML/packed-weight features of the reference are not part of this library
+    }
+}
+
+const char *gen9blas_error(void) { return errbuf; }
+int gen9blas_last_status(void) { return gst; }
+double gen9blas_last_time_ms(void) { return last_ms; }
+int gen9blas_last_zero_copy(void) { return last_zc; }
+
+void *gen9blas_alloc(size_t bytes) {
+    if (begin()) return nullptr;
+    void *p = nullptr;
+    hipError_t e = hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault);
+    if (e != hipSuccess || !p) {
+        (void)hipGetLastError();
+        fail(GEN9BLAS_ERR_OUT_OF_MEMORY, "hipHostMalloc(%zu): %s", bytes, hipGetErrorString(e));
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(alloc_mu);
+    blocks()[(uintptr_t)p] = bytes ? bytes : 1;
+    return p;
+}
+
+void gen9blas_free(void *p) {
+    if (!p) return;
+    {
+        std::lock_guard<std::mutex> lk(alloc_mu);
+        auto it = blocks().find((uintptr_t)p);
+        if (it == blocks().end()) return;
+        blocks().erase(it);
+    }
+    if (stream) (void)hipStreamSynchronize(stream);
+    (void)hipHostFree(p);
+}
+
+int gen9blas_is_usm(const void *p, size_t bytes) {
+    if (!p) return 0;
+    std::lock_guard<std::mutex> lk(alloc_mu);
+    auto &m = blocks();
+    auto it = m.upper_bound((uintptr_t)p);
+    if (it == m.begin()) return 0;
+    --it;
+    return (uintptr_t)p + bytes <= it->first + it->second;
+}
+
+void *gen9blas_hip_stream(void) { return begin() ? nullptr : (void *)stream; }
+
+void *gen9blas_device_alloc(size_t bytes) {
+    if (begin()) return nullptr;
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        fail(GEN9BLAS_ERR_OUT_OF_MEMORY, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+        return nullptr;
+    }
+    return p;
+}
+
+void gen9blas_device_free(void *p) {
+    if (!p || begin()) return;
+    (void)hipStreamSynchronize(stream);
+    (void)hipFree(p);
+}
+
+int gen9blas_memcpy(void *dst, const void *src, size_t bytes) {
+    G9_TRY(begin());
+    if (!bytes) return 0;
+    if (!dst || !src) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "gen9blas_memcpy: NULL pointer");
+    G9_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, stream));
+    return wait_stream();
+}
+
+void gen9blas_set_nowait(int on) { nowait = on != 0; }
+
+int gen9blas_flush(void) {
+    G9_TRY(begin());
+    return wait_stream();
+}
+
+}  // extern "C"

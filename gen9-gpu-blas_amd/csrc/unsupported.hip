@@ -1,0 +1,73 @@
+// Entry points of the reference ABI that this build declares and exports but does not compute yet: level 3 beyond
+// GEMM (SYMM/SYRK/SYR2K/TRMM/TRSM, reference: lib/src/level3.c), persistent packed B (reference: lib/src/packed.c) and
+// the level-2 symmetric/triangular/banded/packed functions (reference: lib/src/level12.c:267-519).
+// Each one validates its type and arguments the way the reference does, then returns GEN9BLAS_ERR_UNSUPPORTED with a
+// message, so a caller (the BLAS shim among them) falls back to its CPU path. Exporting them keeps the ABI whole:
+// loaders that bind every symbol of the header (the ctypes module, the Rust crate) work unchanged.
+#include "internal.h"
+
+using namespace g9;
+
+namespace {
+int check_type(int type) {
+    G9_TRY(begin());
+    if (type < 0 || type > 3) G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "type %d unavailable", type);
+    return 0;
+}
+int not_built(const char *f) { G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "%s is not implemented in this build", f); }
+}  // namespace
+
+struct gen9blas_packed_b {
+    int type;
+};
+
+extern "C" {
+
+gen9blas_packed_b *gen9blas_pack_b(int type, int transB, int K, int N, const void *B, int ldb) {
+    (void)transB; (void)B; (void)ldb;
+    if (check_type(type)) return nullptr;
+    if (K <= 0 || N <= 0) {
+        fail(GEN9BLAS_ERR_INVALID_ARG, "pack_b: K = %d, N = %d", K, N);
+        return nullptr;
+    }
+    not_built("gen9blas_pack_b");
+    return nullptr;
+}
+
+int gen9blas_gemm_pb(int transA, int M, double alpha, const void *A, int lda, const gen9blas_packed_b *Bp, double beta,
+                     void *C, int ldc) {
+    (void)transA; (void)M; (void)alpha; (void)A; (void)lda; (void)beta; (void)C; (void)ldc;
+    G9_TRY(begin());
+    if (!Bp) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "gemm_pb: NULL packed B");
+    return not_built("gen9blas_gemm_pb");
+}
+
+void gen9blas_packed_b_free(gen9blas_packed_b *Bp) { (void)Bp; }
+
+#define G9_UNBUILT(name, ...)                 \
+    int name(int type, __VA_ARGS__) {         \
+        G9_TRY(check_type(type));             \
+        return not_built(#name);              \
+    }
+
+G9_UNBUILT(gen9blas_symm, int, int, int, int, double, const void *, int, const void *, int, double, void *, int)
+G9_UNBUILT(gen9blas_syrk, int, int, int, int, double, const void *, int, double, void *, int)
+G9_UNBUILT(gen9blas_syr2k, int, int, int, int, double, const void *, int, const void *, int, double, void *, int)
+G9_UNBUILT(gen9blas_trmm, int, int, int, int, int, int, double, const void *, int, void *, int)
+G9_UNBUILT(gen9blas_trsm, int, int, int, int, int, int, double, const void *, int, void *, int)
+G9_UNBUILT(gen9blas_symv, int, int, double, const void *, int, const void *, int, double, void *, int)
+G9_UNBUILT(gen9blas_trmv, int, int, int, int, const void *, int, void *, int)
+G9_UNBUILT(gen9blas_trsv, int, int, int, int, const void *, int, void *, int)
+G9_UNBUILT(gen9blas_syr, int, int, double, const void *, int, void *, int)
+G9_UNBUILT(gen9blas_syr2, int, int, double, const void *, int, const void *, int, void *, int)
+G9_UNBUILT(gen9blas_gbmv, int, int, int, int, int, double, const void *, int, const void *, int, double, void *, int)
+G9_UNBUILT(gen9blas_sbmv, int, int, int, double, const void *, int, const void *, int, double, void *, int)
+G9_UNBUILT(gen9blas_tbmv, int, int, int, int, int, const void *, int, void *, int)
+G9_UNBUILT(gen9blas_tbsv, int, int, int, int, int, const void *, int, void *, int)
+G9_UNBUILT(gen9blas_spmv, int, int, double, const void *, const void *, int, double, void *, int)
+G9_UNBUILT(gen9blas_tpmv, int, int, int, int, const void *, void *, int)
+G9_UNBUILT(gen9blas_tpsv, int, int, int, int, const void *, void *, int)
+G9_UNBUILT(gen9blas_spr, int, int, double, const void *, int, void *)
+G9_UNBUILT(gen9blas_spr2, int, int, double, const void *, int, const void *, int, void *)
+
+}  // extern "C"

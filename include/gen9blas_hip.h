@@ -1,0 +1,32 @@
+// gen9blas MI355X additions: the HIP stream, device memory and asynchronous ("no-wait") calls.
+//
+// These entry points have no counterpart in the reference's BLAS header, except the no-wait pair, which mirrors
+// gen9blas_set_nowait / gen9blas_flush of the reference's ML header (reference: lib/gen9blas_ml.h:56-69) and is
+// extended here to every BLAS call whose operands are all device memory.
+#pragma once
+#include <stddef.h>
+#include "gen9blas.h"
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// gfx architecture number of the open device (950 for MI355X), 0 without a device.
+GEN9BLAS_API int gen9blas_device_arch(void);
+// The library's HIP stream (a hipStream_t). Every kernel of the library is launched on it. The stream synchronizes
+// with the legacy default stream, so work queued on the null stream by the caller is ordered before library calls.
+GEN9BLAS_API void *gen9blas_hip_stream(void);
+// Device memory (hipMalloc). Pointers into it are used in place by every entry point.
+GEN9BLAS_API void *gen9blas_device_alloc(size_t bytes);
+GEN9BLAS_API void gen9blas_device_free(void *p);
+// Copy between any two of host / pinned host / device memory, synchronous on the library stream.
+GEN9BLAS_API int gen9blas_memcpy(void *dst, const void *src, size_t bytes);
+// No-wait mode: while on, a call whose operands are all device memory queues its kernels and returns without waiting
+// (results written by the kernels are ready after gen9blas_flush). Calls that touch host memory, and calls that
+// return a value through a host pointer (dot, asum, nrm2, iamax), still wait.
+GEN9BLAS_API void gen9blas_set_nowait(int on);
+// Waits until all queued work of the library has finished; returns 0 or the error of a failed kernel.
+GEN9BLAS_API int gen9blas_flush(void);
+
+#ifdef __cplusplus
+}
+#endif

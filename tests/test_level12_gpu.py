@@ -1,0 +1,135 @@
+"""Level 1-2 parity on the GPU: axpy, scal, copy, swap, rot, dot, asum, nrm2, iamax, gemv (N and T), ger.
+
+Follows the reference's level 1-2 test (reference: lib/test_level12.py:27-97): lengths 1, 5, 255, 256, 1000, 100003;
+strides (1, 1), (1, 1) shifted, (3, −2), (−1, 1); GEMV on odd shapes, with beta, transposed views and submatrices.
+Error relative to the formula scale (e.g. |a·x| + |y| for axpy, |A|·|x| for gemv): FP32 ≤ 1e-6, FP16 ≤ 2e-3,
+FP64 ≤ 1e-13; reductions (FP64 on the GPU) ≤ 1e-6. The dot product is also compared with the oracle's FP64
+restatement (reference: lib/kernels/level12.cl:189-214): both are FP64 sums of exact products and agree to 1e-12.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = {np.float32: 1e-6, np.float16: 2e-3, np.float64: 1e-13}
+rng = np.random.default_rng(11)
+
+
+def check(name, W, ref, scale, tol):
+    e = float(np.max(np.abs(np.asarray(W, np.float64) - ref) / np.maximum(scale, 6.2e-5 if tol > 1e-5 else 1e-30)))
+    assert e <= tol, f"{name}: {e:.1e} > {tol:.0e}"
+
+
+def vector(n, dt, step=1, shift=0):
+    base = rng.uniform(-1, 1, n * abs(step) + shift + 3).astype(dt)
+    v = base[shift:shift + n * abs(step):abs(step)]
+    return v[::-1] if step < 0 else v
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float16, np.float64])
+@pytest.mark.parametrize("n", [1, 5, 255, 256, 1000, 100003])
+def test_level1(g9, orc, dt, n):
+    tol = TOL[dt]
+    for kx, ky, px in ((1, 1, 0), (1, 1, 1), (3, -2, 5), (-1, 1, 2)):
+        label = f"{np.dtype(dt).name} n={n} strides {kx},{ky} shift {px}"
+        x, y = vector(n, dt, kx, px), vector(n, dt, ky, 1)
+        X, Y = x.astype(np.float64), y.astype(np.float64)
+        g9.axpy(0.75, x, y)
+        check("axpy " + label, y, 0.75 * X + Y, 0.75 * abs(X) + abs(Y), tol)
+        y[:] = Y
+        g9.scal(-1.5, y)
+        check("scal " + label, y, -1.5 * Y, 1.5 * abs(Y), tol)
+        y[:] = Y
+        g9.copy(x, y)
+        check("copy " + label, y, X, 1, 0)
+        y[:] = Y
+        g9.swap(x, y)
+        check("swap " + label, np.concatenate([x, y]), np.concatenate([Y, X]), 1, 0)
+        x[:], y[:] = X, Y
+        g9.rot(x, y, 0.6, 0.8)
+        check("rot " + label, np.concatenate([x, y]), np.concatenate([0.6 * X + 0.8 * Y, 0.6 * Y - 0.8 * X]),
+              np.concatenate([abs(X) + abs(Y)] * 2), tol)
+        x[:], y[:] = X, Y
+        d = g9.dot(x, y)
+        check("dot " + label, d, X @ Y, abs(X) @ abs(Y), 1e-6)
+        assert abs(d - orc.dot(x, y)) <= 1e-12 * max(1.0, abs(X) @ abs(Y)), "dot vs oracle " + label
+        check("asum " + label, g9.asum(x), abs(X).sum(), abs(X).sum(), 1e-6)
+        check("nrm2 " + label, g9.nrm2(x), np.linalg.norm(X), np.linalg.norm(X), 1e-6)
+        assert g9.iamax(x) == int(np.argmax(abs(X))), "iamax " + label
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float16, np.float64])
+def test_level1_shared_pages(g9, dt):
+    v = rng.uniform(-1, 1, 3000).astype(dt)
+    V = v.astype(np.float64)
+    g9.axpy(2.0, v[:1000], v[1000:2000])
+    check("axpy shared pages", v[1000:2000], 2 * V[:1000] + V[1000:2000], 3, TOL[dt])
+    v[:] = V
+    check("dot x·x", g9.dot(v, v), V @ V, V @ V, 1e-6)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float16, np.float64])
+@pytest.mark.parametrize("M,N", [(1, 1), (7, 3), (64, 64), (257, 1031), (1000, 2), (3, 5000), (2048, 1536)])
+def test_gemv_ger(g9, orc, dt, M, N):
+    tol = TOL[dt]
+    A = rng.uniform(-1, 1, (M, N)).astype(dt)
+    Ad = A.astype(np.float64)
+    x, xt = vector(N, dt), vector(M, dt, -2, 3)
+    y0, yt0 = vector(M, dt, 2), vector(N, dt)
+    Y0, YT0 = y0.astype(np.float64), yt0.astype(np.float64)
+    y = g9.gemv(A, x, alpha=1.5)
+    check(f"gemv N {M}x{N}", y, 1.5 * Ad @ x.astype(np.float64), 1.5 * abs(Ad) @ abs(x.astype(np.float64)), tol)
+    g9.gemv(A, x, alpha=0.5, beta=-2.0, y=y0)
+    check(f"gemv N beta {M}x{N}", y0, 0.5 * Ad @ x.astype(np.float64) - 2 * Y0,
+          0.5 * abs(Ad) @ abs(x.astype(np.float64)) + 2 * abs(Y0), tol)
+    g9.gemv(A, xt, alpha=0.5, beta=1.0, y=yt0, trans=True)
+    Xt = xt.astype(np.float64)
+    check(f"gemv T {M}x{N}", yt0, 0.5 * Ad.T @ Xt + YT0, 0.5 * abs(Ad.T) @ abs(Xt) + abs(YT0), tol)
+    xv = vector(M, dt)
+    Xv = xv.astype(np.float64)
+    yv = g9.gemv(A.T, xv)
+    check(f"gemv A.T {M}x{N}", yv, Ad.T @ Xv, abs(Ad.T) @ abs(Xv), tol)
+    xg, yg = vector(M, dt, 1, 1), vector(N, dt, -3, 0)
+    Xg, Yg = xg.astype(np.float64), yg.astype(np.float64)
+    A2 = A.copy()
+    g9.ger(-0.5, xg, yg, A2)
+    check(f"ger {M}x{N}", A2, Ad - 0.5 * np.outer(Xg, Yg), abs(Ad) + 0.5 * np.outer(abs(Xg), abs(Yg)), tol)
+    # the oracle's restatement of the reference GEMV meets the same bound
+    if M * N <= 1 << 20:
+        R = orc.gemv(A, x, alpha=1.5)
+        check(f"oracle gemv N {M}x{N}", R, 1.5 * Ad @ x.astype(np.float64), 1.5 * abs(Ad) @ abs(x.astype(np.float64)), tol)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float16, np.float64])
+def test_gemv_submatrix(g9, dt):
+    B = rng.uniform(-1, 1, (300, 400)).astype(dt)
+    Bd = B.astype(np.float64)
+    y = g9.gemv(B[10:200, 5:305], B[0, :300])
+    check("gemv submatrix", y, Bd[10:200, 5:305] @ Bd[0, :300], abs(Bd[10:200, 5:305]) @ abs(Bd[0, :300]), TOL[dt])
+
+
+def test_level2_config_device(g9, orc, torch_dev):
+    """BASELINE level 1/2 config at full size on device buffers: SAXPY, SDOT (2^26), SGEMV N/T (16384²)."""
+    torch = torch_dev
+    n = 1 << 26
+    x = orc.uniform(n, np.float32, orc.SEED_X)
+    y = orc.uniform(n, np.float32, orc.SEED_Y)
+    xd, yd = torch.from_numpy(x).cuda(), torch.from_numpy(y).cuda()
+    d = g9.dot(xd, yd)
+    ref = float(np.dot(x.astype(np.float64), y.astype(np.float64)))
+    assert abs(d - ref) <= 1e-12 * float(np.abs(x).astype(np.float64) @ np.abs(y).astype(np.float64))
+    g9.axpy(0.5, xd, yd)
+    got = yd.cpu().numpy()
+    exp = np.float32(0.5) * x + y   # single rounding of a·x + y differs from fma by ≤ 1 ulp
+    assert np.max(np.abs(got.astype(np.float64) - exp) / (0.5 * np.abs(x) + np.abs(y) + 1e-30)) <= 1e-6
+    m = 16384
+    A = orc.uniform((m, m), np.float32, orc.SEED_A)
+    xv = orc.uniform(m, np.float32, orc.SEED_X)
+    Ad, xvd = torch.from_numpy(A).cuda(), torch.from_numpy(xv).cuda()
+    for trans in (False, True):
+        yv = g9.gemv(Ad, xvd, trans=trans).cpu().numpy()
+        rows = np.random.default_rng(8).integers(0, m, 64)
+        Asub = (A.T if trans else A)[rows].astype(np.float64)
+        ref = Asub @ xv.astype(np.float64)
+        scale = np.abs(Asub) @ np.abs(xv.astype(np.float64))
+        assert float(np.max(np.abs(yv[rows] - ref) / scale)) <= 1e-6, f"sgemv trans={trans}"

@@ -1,0 +1,92 @@
+"""Skinny GEMM parity on the GPU (C = A·Wᵀ and the other layouts with min(M, N) ≤ 16).
+
+Follows the reference's skinny test (reference: lib/test_skinny.py:38-63): the same shapes, both weight layouts,
+transposed views, the role swap for small N, alpha/beta with C as a slice of a larger array and nothing written outside
+it, host and device memory. Bound: max|C − ref| / max|ref| ≤ 4e-3 (FP16) and 2e-6 (FP32) against float64
+(lib/test_skinny.py:19, 29-35); the oracle's restatement of the reference skinny kernel meets the same bound.
+The 4096² decode shape of the benchmark is checked at M = 1, 2, 4, 8, 16 and with rotated weight copies.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = {np.float16: 4e-3, np.float32: 2e-6}
+SHAPES = [(1, 1000, 777), (3, 517, 1029), (4, 2048, 128), (5, 64, 9), (8, 333, 4096), (9, 1500, 1500),
+          (16, 4096, 1000), (1, 8, 3), (2, 7, 2000)]
+
+
+def _err(W, ref):
+    return float(np.max(np.abs(np.asarray(W, np.float64) - ref)) / max(1e-30, np.max(np.abs(ref))))
+
+
+def _dev(torch, x):
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+@pytest.mark.parametrize("dt", [np.float16, np.float32])
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_skinny_reference_cases(g9, orc, torch_dev, dt, M, N, K):
+    rng = np.random.default_rng(7)
+    fn = g9.hgemm if dt == np.float16 else g9.sgemm
+    for tA in (False, True):
+        for tB in (False, True):
+            a = rng.uniform(-1, 1, (K, M) if tA else (M, K)).astype(dt)
+            b = rng.uniform(-1, 1, (N, K) if tB else (K, N)).astype(dt)
+            A, B = (a.T if tA else a), (b.T if tB else b)
+            ref = A.astype(np.float64) @ B.astype(np.float64)
+            tag = f"{np.dtype(dt).name} M={M} N={N} K={K} tA={tA} tB={tB}"
+            assert _err(fn(A, B), ref) <= TOL[dt], tag
+            assert _err(fn(B.T, A.T), ref.T) <= TOL[dt], tag + " (small N)"
+            Ad = _dev(torch_dev, a)
+            Bd = _dev(torch_dev, b)
+            Wd = fn(Ad.t() if tA else Ad, Bd.t() if tB else Bd)
+            assert _err(Wd.cpu().numpy(), ref) <= TOL[dt], tag + " device"
+    # alpha, beta, C as a slice (row stride), nothing outside the slice changes
+    A = rng.uniform(-1, 1, (M, K)).astype(dt)
+    W = rng.uniform(-1, 1, (N, K)).astype(dt)
+    big = rng.uniform(-1, 1, (M + 2, N + 5)).astype(dt)
+    C = big[1:M + 1, 2:N + 2]
+    C0 = C.astype(np.float64)
+    D0 = big.copy()
+    fn(A, W.T, alpha=0.75, beta=-1.5, C=C)
+    ref = 0.75 * A.astype(np.float64) @ W.astype(np.float64).T - 1.5 * C0
+    assert _err(C, ref) <= TOL[dt]
+    mask = np.ones(big.shape, bool)
+    mask[1:M + 1, 2:N + 2] = False
+    assert np.array_equal(big[mask], D0[mask]), "write outside the C slice"
+    # the oracle's restatement of the reference skinny kernel meets the same bound
+    if M * N * K <= 4e6:
+        R = orc.skinny(A, W, 0.75, -1.5, C0.astype(dt), tB=True)
+        assert _err(R, ref) <= TOL[dt]
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
+def test_skinny_decode_4096(g9, orc, torch_dev, M):
+    """Benchmark shape: W 4096×4096 fp16 ~ N(0, 0.02), A M×4096 ~ N(0, 1), C = A·Wᵀ, rotated weight copies."""
+    torch = torch_dev
+    K = N = 4096
+    A = orc.normal((M, K), np.float16, orc.SEED_A)
+    Ad = _dev(torch, A)
+    for i in range(3):
+        W = orc.normal((N, K), np.float16, orc.SEED_W0 + i, 0.02)
+        Wd = _dev(torch, W)
+        C = g9.hgemm(Ad, Wd.t()).cpu().numpy()
+        ref = A.astype(np.float64) @ W.astype(np.float64).T
+        assert _err(C, ref) <= TOL[np.float16], f"M={M} copy {i}"
+        # the reference metric (north_star bound for FP16 accumulation in FP32: ≤ 1e-4 relative to Σ|a·w|)
+        scale = np.abs(A.astype(np.float64)) @ np.abs(W.astype(np.float64)).T
+        assert float(np.max(np.abs(C - ref) / scale)) <= 1e-3, f"M={M} copy {i}: reference metric"
+
+
+def test_skinny_oracle_parity_small(g9, orc):
+    """GPU skinny vs the oracle's restatement on a small A·Wᵀ (both FP32-accumulated: they agree to FP16 rounding)."""
+    rng = np.random.default_rng(3)
+    for M in (1, 3, 16):
+        A = rng.uniform(-1, 1, (M, 640)).astype(np.float16)
+        W = rng.uniform(-1, 1, (300, 640)).astype(np.float16)
+        G = g9.hgemm(A, W.T)
+        R = orc.skinny(A, W, tB=True)
+        d = np.abs(G.astype(np.float64) - R.astype(np.float64))
+        ulp = np.abs(R.astype(np.float64)) * 2.0 ** -10 + 2.0 ** -24
+        assert (d <= 2 * ulp).all(), f"M={M}: GPU and oracle differ by more than 2 FP16 ulp"
