@@ -120,15 +120,14 @@ def main():
     # ---------------- measured HBM bandwidth: streaming read of 1 GiB (> 256 MB MALL) ----------------
     nh = 1 << 28
     big = torch.empty(nh, dtype=torch.float32, device=dev).uniform_(-1, 1)
-    out = d()
+    out_d = torch.zeros(1, dtype=torch.float64, device=dev)   # device result: no host wait per call
+    out_p = ctypes.cast(ctypes.c_void_p(out_d.data_ptr()), ctypes.POINTER(ctypes.c_double))
 
     def rd():
-        rc = L.gen9blas_asum(1, nh, p(big.data_ptr()), 1, ctypes.byref(out))
+        rc = L.gen9blas_asum(1, nh, p(big.data_ptr()), 1, out_p)
         if rc:
             raise RuntimeError(L.gen9blas_error().decode())
-    g9.set_nowait(False)
     ms = timed(rd, k=10, w=2)
-    g9.set_nowait(True)
     hbm = 4.0 * nh / (ms * 1e-3) / 1e9
     res["hbm_read_1GiB"] = {"kernel": "gen9blas_asum FP32 2^28 (pure streaming read)", "ms": round(ms, 4),
                             "GBs": round(hbm, 1), "frac_of_datasheet": round(hbm / PEAK_HBM_GBS, 4)}
@@ -179,16 +178,13 @@ def main():
                 raise RuntimeError(L.gen9blas_error().decode())
         ms = timed(ax)
         res["saxpy_2^26"] = {"ms": round(ms, 4), "GBs": round(12.0 * n / (ms * 1e-3) / 1e9, 1)}
-        g9.set_nowait(False)
-
         def dt_():
-            rc = L.gen9blas_dot(1, n, p(xd.data_ptr()), 1, p(yd.data_ptr()), 1, ctypes.byref(out))
+            rc = L.gen9blas_dot(1, n, p(xd.data_ptr()), 1, p(yd.data_ptr()), 1, out_p)
             if rc:
                 raise RuntimeError(L.gen9blas_error().decode())
         ms = timed(dt_)
         res["sdot_2^26"] = {"ms": round(ms, 4), "GBs": round(8.0 * n / (ms * 1e-3) / 1e9, 1),
-                            "note": "includes the per-call wait for the FP64 result"}
-        g9.set_nowait(True)
+                            "note": "FP64 result written to device memory"}
         del xd, yd
         m = 16384
         Ad = to_dev(np.random.default_rng(1).uniform(-1, 1, (m, m)).astype(np.float32))
@@ -209,6 +205,27 @@ def main():
         del Ad
 
     g9.set_nowait(False)
+
+    # ---------------- calibration: AMD's libraries through torch.matmul (hipBLASLt / rocBLAS), not this library ----
+    if not args.quick:
+        cal = {}
+        for name, tdt in (("fp16", torch.float16), ("fp32", torch.float32), ("fp64", torch.float64)):
+            a = torch.randn(4096, 4096, dtype=tdt, device=dev)
+            b = torch.randn(4096, 4096, dtype=tdt, device=dev)
+            for _ in range(3):
+                torch.matmul(a, b)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                torch.matmul(a, b)
+            e1.record()
+            e1.synchronize()
+            ms = e0.elapsed_time(e1) / 10
+            cal[name] = round(2.0 * 4096 ** 3 / (ms * 1e-3) / 1e12, 1)
+            del a, b
+        res["calibration_torch_matmul_n4096_tflops"] = cal
+        log("calibration", cal)
 
     # ---------------- CPU baseline: the reference's CPU path on the host cores ----------------
     cpu = None

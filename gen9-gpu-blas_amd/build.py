@@ -21,13 +21,13 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 LIB = os.path.join(HERE, "libgen9blas.so")
 BLAS_LIB = os.path.join(HERE, "libgen9blas_blas.so")
 
-HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-I" + INCLUDE, "-I" + CSRC,
+HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC", "-fvisibility=hidden", "-I" + INCLUDE, "-I" + CSRC,
              # packed FP32 VALU forms are kept out of the generated code
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wall", "-Wno-unused-function"]
 HIP_SOURCES = ["runtime.hip", "gemm.hip", "gemm_kernels.hip", "skinny.hip", "level12.hip", "level12_kernels.hip",
                "unsupported.hip"]
-HEADERS = ["internal.h", "skinny_kernel.h"]
+HEADERS = ["internal.h", "skinny_kernel.h", "gemm_kernel.h", "wave.h"]
 
 
 def _run(cmd):

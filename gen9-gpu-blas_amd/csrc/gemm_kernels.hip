@@ -1,366 +1,54 @@
-// MFMA GEMM kernels for gfx950: C = alpha·op(A)·op(B) + beta·C in FP16 (FP32 accumulation), FP32 and FP64.
-//
-// Semantics follow the reference's main kernels and epilogues (reference: lib/kernels/hgemm.cl:838-898 hgemm_v /
-// hgemm_kc_v, lib/kernels/sgemm.cl:192-230 sgemm_v + gen9blas_epilog_fb, lib/kernels/dgemm_core.cl:61-94 dgemm_v,
-// lib/kernels/hgemm.cl:558-564 gen9blas_epilog_b): every C element is the sum over k of A·B products, then
-// alpha·sum + beta·C (C not read when beta = 0), rounded once to the element type. The design is MI355X-native:
-// - no packing pass and no separate epilogue kernel: the kernel reads op(A) and op(B) in any of the four transpose
-//   layouts straight from memory and applies alpha/beta in registers before its only store of C;
-// - block tiles are staged through double-buffered LDS with one barrier per k-step; the next k-step's global loads
-//   are in flight while the current one runs on the matrix cores;
-// - LDS rows hold 128 bytes of k (64 FP16 / 32 FP32 / 16 FP64) plus 16 bytes of padding, so the fragment reads of
-//   16 consecutive rows hit 16 distinct 4-bank groups;
-// - an operand stored with its m (or n) index contiguous is transposed in registers, V×V elements per thread
-//   (V = 16 bytes / element size), so LDS always holds k-contiguous rows and every fragment read is 16 bytes;
-// - accumulation is on MFMA: v_mfma_f32_32x32x16_f16, v_mfma_f32_32x32x2_f32, v_mfma_f64_16x16x4_f64. Operands are
-//   swapped (the MFMA "A" input is the B tile) so each lane ends up with 4 consecutive n of one row of C, which gives
-//   vector stores of C;
-// - the k index inside a block tile is permuted per lane group: lane group g of an MFMA consumes the k-run
-//   [g·BK/G, (g+1)·BK/G). A and B use the same permutation, so every product A[m][k]·B[k][n] is summed exactly once;
-// - workgroup → tile mapping: consecutive dispatch slots go to different XCDs, so tile indices are re-mapped to give
-//   each XCD a contiguous range, and tiles are ordered in groups of GM tile rows so an XCD's L2 shares A and B panels.
-#include "internal.h"
+// Host side of the MFMA GEMM: tile configuration per type and dispatch over the transpose layouts.
+// The kernel template and its design notes are in gemm_kernel.h.
+#include "gemm_kernel.h"
 
 namespace g9 {
 
-typedef _Float16 f16;
-typedef f16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef double f64x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-
-// ---------------- MFMA traits ----------------
-// D is MI × MI; G = 64 / MI lane groups; E elements of one operand per lane per instruction. Accumulator r of lane l
-// holds D[row(r, l)][l % MI]. In the 32×32 layouts rows come in runs of 4 consecutive values (r = 4q .. 4q+3); in
-// the FP64 16×16 layout accumulator r of lane group g holds row 4r + g.
-// SWAP: the B tile is the MFMA's first operand, so D rows are n (consecutive n per lane → vector stores of C).
-// BLOCKED: each block tile (BK values of k) is summed into a fresh accumulator that is then added to the running
-// one, so the FP32 rounding error grows with K/BK + BK instead of K.
-template <class T> struct Mma;
-template <> struct Mma<f16> {
-    static constexpr int MI = 32, G = 2, E = 8, NACC = 16;
-    static constexpr bool SWAP = true, BLOCKED = false;
-    using Acc = f32x16;
-    using Sum = float;
-    static __device__ __forceinline__ Acc mma(u32x4 a, u32x4 b, Acc c, int) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-    }
-    static __device__ __forceinline__ int row(int r, int l) { return 8 * (r >> 2) + 4 * (l >> 5) + (r & 3); }
-};
-template <> struct Mma<float> {
-    static constexpr int MI = 32, G = 2, E = 1, NACC = 16;
-    static constexpr bool SWAP = true, BLOCKED = true;
-    using Acc = f32x16;
-    using Sum = float;
-    // ss selects the element of the 16-byte group (4 FP32 values = 4 consecutive k-steps). Elements are copied to
-    // scalars before __builtin_bit_cast (hipcc evaluates a bit_cast of a vector element as element 0).
-    static __device__ __forceinline__ Acc mma(u32x4 a, u32x4 b, Acc c, int ss) {
-        const unsigned as = a[ss], bs = b[ss];
-        return __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, as), __builtin_bit_cast(float, bs), c, 0, 0, 0);
-    }
-    static __device__ __forceinline__ int row(int r, int l) { return 8 * (r >> 2) + 4 * (l >> 5) + (r & 3); }
-};
-template <> struct Mma<double> {
-    static constexpr int MI = 16, G = 4, E = 1, NACC = 4;
-    static constexpr bool SWAP = false, BLOCKED = false;
-    using Acc = f64x4;
-    using Sum = double;
-    static __device__ __forceinline__ Acc mma(u32x4 a, u32x4 b, Acc c, int ss) {
-        const unsigned a0 = a[2 * ss], a1 = a[2 * ss + 1], b0 = b[2 * ss], b1 = b[2 * ss + 1];
-        const u32x2 pa = {a0, a1}, pb = {b0, b1};
-        return __builtin_amdgcn_mfma_f64_16x16x4f64(__builtin_bit_cast(double, pa), __builtin_bit_cast(double, pb), c, 0, 0, 0);
-    }
-    static __device__ __forceinline__ int row(int r, int l) { return 4 * r + (l >> 4); }
-};
-
-template <class S> struct GemmParams {
-    const void *A, *B;
-    void *C;
-    long long lda, ldb, ldc, sA, sB, sC;
-    int M, N, K, tiles_m, tiles_n, vec_c;
-    S alpha, beta;
-};
-
-// 16 bytes (V elements) of row r, columns c .. c+V-1 of a row-major matrix X (R valid rows, Cc valid columns, row
-// stride ld); zero outside the valid region. VEC: X and ld are 16-byte aligned, so whole chunks load as one vector.
-template <class T, bool VEC>
-__device__ __forceinline__ u32x4 load16(const T *__restrict__ X, long long ld, int r, int c, int R, int Cc) {
-    constexpr int V = 16 / sizeof(T);
-    if (VEC && r < R && c + V <= Cc) return *reinterpret_cast<const u32x4 *>(X + (long long)r * ld + c);
-    union { u32x4 v; T e[V]; } u;
-#pragma unroll
-    for (int e = 0; e < V; e++) u.e[e] = (r < R && c + e < Cc) ? X[(long long)r * ld + c + e] : T(0);
-    return u.v;
-}
-
-// Transpose of a V×V block held as V rows of 16 bytes: out[j] element i = in[i] element j.
-template <class T> __device__ __forceinline__ void transpose(const u32x4 *in, u32x4 *out);
-template <> __device__ __forceinline__ void transpose<f16>(const u32x4 *in, u32x4 *out) {
-#pragma unroll
-    for (int j = 0; j < 8; j++)
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            const unsigned lo = in[2 * w][j >> 1], hi = in[2 * w + 1][j >> 1];
-            out[j][w] = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-        }
-}
-template <> __device__ __forceinline__ void transpose<float>(const u32x4 *in, u32x4 *out) {
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) out[j][i] = in[i][j];
-}
-template <> __device__ __forceinline__ void transpose<double>(const u32x4 *in, u32x4 *out) {
-    out[0] = u32x4{in[0][0], in[0][1], in[1][0], in[1][1]};
-    out[1] = u32x4{in[0][2], in[0][3], in[1][2], in[1][3]};
-}
-
-// Global → register → LDS staging of one operand tile: RT rows (m or n) × BK (k), 128 bytes of k per row.
-// KC: the operand is stored k-contiguous (element (mn, k) at X[mn·ld + k]); otherwise mn-contiguous
-// (element (mn, k) at X[k·ld + mn]) and transposed in registers on the way to LDS.
-constexpr int ROWB = 144;   // LDS bytes per tile row: 128 of data + 16 of padding
-template <class T, int RT, int NT, bool KC, bool VEC>
-struct Stage {
-    static constexpr int V = 16 / (int)sizeof(T);
-    static constexpr int N16 = RT * 8 / NT;   // 16-byte chunks per thread
-    static_assert(RT * 8 % NT == 0, "tile rows × 8 chunks must divide over the threads");
-    static_assert(KC || N16 % V == 0, "transposed staging needs whole V×V blocks per thread");
-    u32x4 r[N16];
-
-    __device__ __forceinline__ void load(const T *__restrict__ X, long long ld, int MN, int K, int mn0, int k0, int tid) {
-        if constexpr (KC) {
-#pragma unroll
-            for (int i = 0; i < N16; i++) {
-                const int id = i * NT + tid;
-                r[i] = load16<T, VEC>(X, ld, mn0 + (id >> 3), k0 + (id & 7) * V, MN, K);
-            }
-        } else {
-#pragma unroll
-            for (int b = 0; b < N16 / V; b++) {
-                const int id = b * NT + tid, lo = id & 31;
-                const int mb = (lo & 3) + 4 * (id >> 5), kb = lo >> 2;
-#pragma unroll
-                for (int i = 0; i < V; i++) r[b * V + i] = load16<T, VEC>(X, ld, k0 + kb * V + i, mn0 + mb * V, K, MN);
-            }
-        }
-    }
-    __device__ __forceinline__ void store(unsigned char *rows, int tid) const {
-        if constexpr (KC) {
-#pragma unroll
-            for (int i = 0; i < N16; i++) {
-                const int id = i * NT + tid;
-                *reinterpret_cast<u32x4 *>(rows + (id >> 3) * ROWB + (id & 7) * 16) = r[i];
-            }
-        } else {
-#pragma unroll
-            for (int b = 0; b < N16 / V; b++) {
-                const int id = b * NT + tid, lo = id & 31;
-                const int mb = (lo & 3) + 4 * (id >> 5), kb = lo >> 2;
-                u32x4 t[V];
-                transpose<T>(r + b * V, t);
-#pragma unroll
-                for (int j = 0; j < V; j++) *reinterpret_cast<u32x4 *>(rows + (mb * V + j) * ROWB + kb * 16) = t[j];
-            }
-        }
-    }
-};
-
-__device__ __forceinline__ float fma_s(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
-__device__ __forceinline__ double fma_s(double a, double b, double c) { return __builtin_fma(a, b, c); }
-template <class T, class S> __device__ __forceinline__ void store4(T *c, const S *v, S alpha, S beta, bool vec, int valid);
-
-template <class T, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool VEC>
-__global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename Mma<T>::Sum> p) {
-    using MM = Mma<T>;
-    using S = typename MM::Sum;
-    constexpr int NT = WM * WN * 64;
-    constexpr int BK = 128 / (int)sizeof(T);
-    constexpr int MI = MM::MI, G = MM::G;
-    constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / MI, TN = WTN / MI;
-    constexpr int KRB = BK / G * (int)sizeof(T);   // bytes of k per lane group and row
-    constexpr int QG = KRB / 16;                    // 16-byte groups per lane group and row
-    constexpr int SPG = 16 / ((int)sizeof(T) * MM::E);   // MFMA steps per 16-byte group
-    static_assert(TM * MI == WTM && TN * MI == WTN, "wave tile must be a multiple of the MFMA tile");
-    __shared__ __attribute__((aligned(16))) unsigned char lds[2][(BM + BN) * ROWB];
-
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int wm = wid % WM, wn = wid / WM;
-    const int g = lane / MI, lr = lane % MI;
-
-    // tile of this workgroup
-    int bid = blockIdx.x;
-    const int nt = p.tiles_m * p.tiles_n, nt8 = nt & ~7;
-    if (bid < nt8) bid = (bid & 7) * (nt8 >> 3) + (bid >> 3);
-    constexpr int GM = 4;
-    const int group = bid / (GM * p.tiles_n), first_m = group * GM;
-    const int gsz = min(p.tiles_m - first_m, GM);
-    const int in_group = bid % (GM * p.tiles_n);
-    const int m0 = (first_m + in_group % gsz) * BM, n0 = (in_group / gsz) * BN;
-
-    const long long z = blockIdx.y;
-    const T *A = reinterpret_cast<const T *>(p.A) + z * p.sA;
-    const T *B = reinterpret_cast<const T *>(p.B) + z * p.sB;
-    T *C = reinterpret_cast<T *>(p.C) + z * p.sC;
-
-    Stage<T, BM, NT, AK, VEC> sa;
-    Stage<T, BN, NT, BKC, VEC> sb;
-    constexpr int TI = MM::SWAP ? TN : TM, TJ = MM::SWAP ? TM : TN;   // acc[i][j]: D tile of (first, second) operand
-    typename MM::Acc acc[TI][TJ];
-#pragma unroll
-    for (int i = 0; i < TI; i++)
-#pragma unroll
-        for (int j = 0; j < TJ; j++)
-#pragma unroll
-            for (int r = 0; r < MM::NACC; r++) acc[i][j][r] = 0;
-
-    const int nk = (p.K + BK - 1) / BK;
-    sa.load(A, p.lda, p.M, p.K, m0, 0, tid);
-    sb.load(B, p.ldb, p.N, p.K, n0, 0, tid);
-    sa.store(lds[0], tid);
-    sb.store(lds[0] + BM * ROWB, tid);
-    __syncthreads();
-
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) {
-            sa.load(A, p.lda, p.M, p.K, m0, (kt + 1) * BK, tid);
-            sb.load(B, p.ldb, p.N, p.K, n0, (kt + 1) * BK, tid);
-        }
-        const unsigned char *As = lds[cur] + (wm * WTM + lr) * ROWB + g * KRB;
-        const unsigned char *Bs = lds[cur] + BM * ROWB + (wn * WTN + lr) * ROWB + g * KRB;
-        typename MM::Acc part[MM::BLOCKED ? TI : 1][MM::BLOCKED ? TJ : 1];
-        if constexpr (MM::BLOCKED) {
-#pragma unroll
-            for (int i = 0; i < TI; i++)
-#pragma unroll
-                for (int j = 0; j < TJ; j++)
-#pragma unroll
-                    for (int r = 0; r < MM::NACC; r++) part[i][j][r] = 0;
-        }
-#pragma unroll
-        for (int q = 0; q < QG; q++) {
-            u32x4 ra[TM], rb[TN];
-#pragma unroll
-            for (int i = 0; i < TM; i++) ra[i] = *reinterpret_cast<const u32x4 *>(As + i * MI * ROWB + q * 16);
-#pragma unroll
-            for (int i = 0; i < TN; i++) rb[i] = *reinterpret_cast<const u32x4 *>(Bs + i * MI * ROWB + q * 16);
-#pragma unroll
-            for (int ss = 0; ss < SPG; ss++)
-#pragma unroll
-                for (int i = 0; i < TI; i++)
-#pragma unroll
-                    for (int j = 0; j < TJ; j++) {
-                        const u32x4 x = MM::SWAP ? rb[i] : ra[i], y = MM::SWAP ? ra[j] : rb[j];
-                        if constexpr (MM::BLOCKED) part[i][j] = MM::mma(x, y, part[i][j], ss);
-                        else acc[i][j] = MM::mma(x, y, acc[i][j], ss);
-                    }
-        }
-        if constexpr (MM::BLOCKED) {
-#pragma unroll
-            for (int i = 0; i < TI; i++)
-#pragma unroll
-                for (int j = 0; j < TJ; j++) acc[i][j] += part[i][j];
-        }
-        if (kt + 1 < nk) {
-            sa.store(lds[cur ^ 1], tid);
-            sb.store(lds[cur ^ 1] + BM * ROWB, tid);
-        }
-        __syncthreads();
-    }
-
-    if constexpr (MM::SWAP) {
-        // lane holds D[n][m] with m = column, runs of 4 consecutive n: vector stores along a row of C
-#pragma unroll
-        for (int i = 0; i < TI; i++)
-#pragma unroll
-            for (int j = 0; j < TJ; j++) {
-                const int m = m0 + wm * WTM + j * MI + lr;
-                if (m >= p.M) continue;
-#pragma unroll
-                for (int q = 0; q < MM::NACC / 4; q++) {
-                    const int n = n0 + wn * WTN + i * MI + MM::row(4 * q, lane);
-                    if (n >= p.N) continue;
-                    const S v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-                    store4<T, S>(C + (long long)m * p.ldc + n, v, p.alpha, p.beta, p.vec_c, p.N - n);
-                }
-            }
-    } else {
-        // lane holds D[m][n] with n = column: the lanes of a group store consecutive n of one row
-#pragma unroll
-        for (int i = 0; i < TI; i++)
-#pragma unroll
-            for (int j = 0; j < TJ; j++) {
-                const int n = n0 + wn * WTN + j * MI + lr;
-                if (n >= p.N) continue;
-#pragma unroll
-                for (int r = 0; r < MM::NACC; r++) {
-                    const int m = m0 + wm * WTM + i * MI + MM::row(r, lane);
-                    if (m >= p.M) continue;
-                    T *c = C + (long long)m * p.ldc + n;
-                    S v = p.alpha * acc[i][j][r];
-                    if (p.beta != S(0)) v = fma_s(p.beta, (S)*c, v);
-                    *c = (T)v;
-                }
-            }
-    }
-}
-
-// C[0..3] = alpha·v + beta·C (C not read when beta = 0), rounded once to T; `valid` elements are inside C.
-template <class T, class S>
-__device__ __forceinline__ void store4(T *c, const S *v, S alpha, S beta, bool vec, int valid) {
-    if (vec && valid >= 4) {
-        if constexpr (sizeof(T) == 2) {
-            u32x2 old = beta != S(0) ? *reinterpret_cast<const u32x2 *>(c) : u32x2{0, 0};
-            union { u32x2 w; T e[4]; } o, n;
-            o.w = old;
-#pragma unroll
-            for (int e = 0; e < 4; e++) n.e[e] = (T)(beta != S(0) ? __builtin_fmaf(beta, (S)o.e[e], alpha * v[e]) : alpha * v[e]);
-            *reinterpret_cast<u32x2 *>(c) = n.w;
-        } else if constexpr (sizeof(T) == 4) {
-            f32x4 o = beta != S(0) ? *reinterpret_cast<const f32x4 *>(c) : f32x4{0, 0, 0, 0};
-            f32x4 n;
-#pragma unroll
-            for (int e = 0; e < 4; e++) n[e] = beta != S(0) ? __builtin_fmaf(beta, o[e], alpha * v[e]) : alpha * v[e];
-            *reinterpret_cast<f32x4 *>(c) = n;
-        } else {
-            f64x4 o = beta != S(0) ? *reinterpret_cast<const f64x4 *>(c) : f64x4{0, 0, 0, 0};
-            f64x4 n;
-#pragma unroll
-            for (int e = 0; e < 4; e++) n[e] = beta != S(0) ? __builtin_fma(beta, o[e], alpha * v[e]) : alpha * v[e];
-            *reinterpret_cast<f64x4 *>(c) = n;
-        }
-        return;
-    }
-#pragma unroll
-    for (int e = 0; e < 4; e++)
-        if (e < valid) {
-            S r = alpha * v[e];
-            if (beta != S(0)) r = fma_s(beta, (S)c[e], r);
-            c[e] = (T)r;
-        }
-}
-
 // ---------------- host side ----------------
-template <class T> struct Cfg;
-template <> struct Cfg<f16> { static constexpr int BM = 256, BN = 256, WM = 2, WN = 2; };
-template <> struct Cfg<float> { static constexpr int BM = 128, BN = 128, WM = 2, WN = 2; };
-template <> struct Cfg<double> { static constexpr int BM = 128, BN = 128, WM = 2, WN = 2; };
+// Tile configurations, per element type and layout, from a sweep on MI355X at n = 4096 (every variant checked against
+// a float64 reference). Big: the steady-state configuration. Small: 128-row tiles for products whose big tiles
+// would leave most of the 256 CUs idle.
+//   FP16 256×256, 8 waves (4×2): NN 794, NT 950 TFLOP/s. FP32 256×128 (NN 117) / 128×128 (NT 127).
+//   FP64 256×128, 8 waves (4×2): 70.6 TFLOP/s.
+struct TileCfg { int BM, BN, WM, WN; };
+// Layouts whose staging needs more registers than a wave has at 2 waves per SIMD (transposed A, unaligned
+// operands) keep FP16 at 4 waves (512 registers per wave), which compiles without spills.
+template <class T, bool AK, bool BKC, bool VEC> struct Cfg;
+template <bool AK, bool BKC, bool VEC> struct Cfg<f16, AK, BKC, VEC> {
+    static constexpr TileCfg big = (AK && VEC) ? TileCfg{256, 256, 4, 2} : TileCfg{256, 256, 2, 2};
+    static constexpr TileCfg small{128, 128, 2, 2};
+};
+template <bool AK, bool BKC, bool VEC> struct Cfg<float, AK, BKC, VEC> {
+    static constexpr TileCfg big = (AK && BKC) ? TileCfg{128, 128, 2, 2} : TileCfg{256, 128, 2, 2};
+    static constexpr TileCfg small{128, 128, 2, 2};
+};
+template <bool AK, bool BKC, bool VEC> struct Cfg<double, AK, BKC, VEC> {
+    static constexpr TileCfg big{256, 128, 4, 2}, small{64, 128, 2, 2};
+};
 
-template <class T, bool AK, bool BKC, bool VEC>
-static int launch_t(const GemmParams<typename Mma<T>::Sum> &p, int count) {
-    using CF = Cfg<T>;
-    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)count), block(CF::WM * CF::WN * 64);
-    hipLaunchKernelGGL((gemm_kernel<T, CF::BM, CF::BN, CF::WM, CF::WN, AK, BKC, VEC>), grid, block, 0, stream, p);
+template <class T, TileCfg C, bool AK, bool BKC, bool VEC>
+static int launch_t(GemmParams<typename Mma<T>::Sum> p, int count) {
+    p.tiles_m = (p.M + C.BM - 1) / C.BM;
+    p.tiles_n = (p.N + C.BN - 1) / C.BN;
+    if ((long long)p.tiles_m * p.tiles_n > 0x7fffffffLL || count > 65535)
+        G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "gemm grid too large (%d × %d tiles, batch %d)", p.tiles_m, p.tiles_n, count);
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)count), block(C.WM * C.WN * 64);
+    hipLaunchKernelGGL((gemm_kernel<T, C.BM, C.BN, C.WM, C.WN, AK, BKC, VEC, true>), grid, block, 0, stream, p);
     G9_HIP(hipGetLastError());
     return 0;
+}
+
+template <class T, bool AK, bool BKC, bool VEC>
+static int launch_layout(const GemmParams<typename Mma<T>::Sum> &p, int count) {
+    using CF = Cfg<T, AK, BKC, VEC>;
+    const long long big_tiles = (long long)((p.M + CF::big.BM - 1) / CF::big.BM) * ((p.N + CF::big.BN - 1) / CF::big.BN) * count;
+    if (big_tiles * 2 < num_cus) return launch_t<T, CF::small, AK, BKC, VEC>(p, count);
+    return launch_t<T, CF::big, AK, BKC, VEC>(p, count);
 }
 
 template <class T>
 static int launch_typed(const GemmCall &c) {
     using S = typename Mma<T>::Sum;
-    using CF = Cfg<T>;
     GemmParams<S> p;
     p.A = c.A; p.B = c.B; p.C = c.C;
     p.lda = c.lda; p.ldb = c.ldb; p.ldc = c.ldc;
@@ -368,26 +56,23 @@ static int launch_typed(const GemmCall &c) {
     p.M = c.M; p.N = c.N; p.K = c.K;
     p.alpha = (S)c.alpha;
     p.beta = (S)c.beta;
-    p.tiles_m = (c.M + CF::BM - 1) / CF::BM;
-    p.tiles_n = (c.N + CF::BN - 1) / CF::BN;
+    p.tiles_m = p.tiles_n = 0;
     const long long es = sizeof(T);
     const long long cal = es * 4 < 16 ? es * 4 : 16;   // alignment of a 4-element group of C
     p.vec_c = ((uintptr_t)c.C % cal == 0) && (c.ldc * es) % cal == 0 && (c.count == 1 || (c.sC * es) % cal == 0);
     const bool vec = ((uintptr_t)c.A % 16 == 0) && ((uintptr_t)c.B % 16 == 0) && (c.lda * es) % 16 == 0 &&
                      (c.ldb * es) % 16 == 0 && (c.count == 1 || ((c.sA * es) % 16 == 0 && (c.sB * es) % 16 == 0));
-    if ((long long)p.tiles_m * p.tiles_n > 0x7fffffffLL || c.count > 65535)
-        G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "gemm grid too large (%d × %d tiles, batch %d)", p.tiles_m, p.tiles_n, c.count);
     const bool ak = !c.tA, bk = c.tB;   // k-contiguous A: not transposed; k-contiguous B: transposed (stored N×K)
     const int sel = (ak ? 4 : 0) | (bk ? 2 : 0) | (vec ? 1 : 0);
     switch (sel) {
-    case 0: return launch_t<T, false, false, false>(p, c.count);
-    case 1: return launch_t<T, false, false, true>(p, c.count);
-    case 2: return launch_t<T, false, true, false>(p, c.count);
-    case 3: return launch_t<T, false, true, true>(p, c.count);
-    case 4: return launch_t<T, true, false, false>(p, c.count);
-    case 5: return launch_t<T, true, false, true>(p, c.count);
-    case 6: return launch_t<T, true, true, false>(p, c.count);
-    default: return launch_t<T, true, true, true>(p, c.count);
+    case 0: return launch_layout<T, false, false, false>(p, c.count);
+    case 1: return launch_layout<T, false, false, true>(p, c.count);
+    case 2: return launch_layout<T, false, true, false>(p, c.count);
+    case 3: return launch_layout<T, false, true, true>(p, c.count);
+    case 4: return launch_layout<T, true, false, false>(p, c.count);
+    case 5: return launch_layout<T, true, false, true>(p, c.count);
+    case 6: return launch_layout<T, true, true, false>(p, c.count);
+    default: return launch_layout<T, true, true, true>(p, c.count);
     }
 }
 

@@ -57,8 +57,14 @@ static int two(int es, int n, const void *x, int incx, bool x_written, void *y, 
 }
 
 static int reduction(int type, int mode, int n, const void *x, int incx, const void *y, int incy, double *result) {
-    if (result) *result = 0;
-    L12_BEGIN(n, !incx || (mode == 0 && !incy));
+    const double t0_ = now_s();
+    int es;
+    const int ok = l12_es(type, &es);
+    // a host result is 0 until the sum is known, as in the reference (reference: lib/src/level12.c:172)
+    if (result && (ok == GEN9BLAS_ERR_NO_DEVICE || !is_device(result, sizeof(double)))) *result = 0;
+    G9_TRY(ok);
+    if (n <= 0) return 0;
+    if (!incx || (mode == 0 && !incy)) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "vector increment 0");
     if (!result) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "NULL result pointer");
     Operand o[2];
     vec(o[0], x, n, incx, es);
@@ -69,18 +75,25 @@ static int reduction(int type, int mode, int n, const void *x, int incx, const v
         G9_TRY(resolve(o[1], SLOT_B, true, false, false));
         no = 2;
     }
-    void *res;
-    G9_TRY(scratch(SLOT_Q, 64, &res));
+    // A result pointer in device memory receives the sum in place (no wait in no-wait mode); a host pointer is
+    // filled after the wait.
+    const bool dev_result = is_device(result, sizeof(double));
+    void *res = result;
+    if (!dev_result) G9_TRY(scratch(SLOT_Q, 64, &res));
     prof_begin();
     G9_TRY(launch_reduce(es, mode, n, o[0].dev, voff(n, incx), incx, mode == 0 ? o[1].dev : nullptr,
                          mode == 0 ? voff(n, incy) : 0, mode == 0 ? incy : 0, (double *)res));
     prof_end();
-    G9_HIP(hipMemcpyAsync(result, res, sizeof(double), hipMemcpyDeviceToHost, stream));
-    const int saved = nowait;
-    nowait = 0;   // the result goes through a host pointer: always wait
-    const int r = finish(o, no);
-    nowait = saved;
-    G9_TRY(r);
+    if (dev_result) {
+        G9_TRY(finish(o, no));
+    } else {
+        G9_HIP(hipMemcpyAsync(result, res, sizeof(double), hipMemcpyDeviceToHost, stream));
+        const int saved = nowait;
+        nowait = 0;   // the result goes through a host pointer: always wait
+        const int r = finish(o, no);
+        nowait = saved;
+        G9_TRY(r);
+    }
     prof_collect(t0_);
     return 0;
 }

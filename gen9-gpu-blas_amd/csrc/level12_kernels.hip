@@ -7,6 +7,8 @@
 // beta = 0) (level12.cl:243-423). Vector element i lives at p[o + i·inc] with o = (n-1)·(-inc) for inc < 0, as in
 // BLAS. Contiguous, 16-byte-aligned operands move as 16-byte vectors; strided ones element by element.
 #include "internal.h"
+#include "wave.h"
+#include <type_traits>
 
 namespace g9 {
 namespace l12 {
@@ -64,11 +66,28 @@ __global__ void __launch_bounds__(NT) elem_kernel(int n, typename Comp<T>::R h11
         }
     };
     if (vec) {
+        // UNR chunks of 16 bytes per thread and iteration, all loads issued before the first store
+        constexpr int UNR = 4;
         const ll nv = n / V;
-        for (ll c = (ll)blockIdx.x * NT + threadIdx.x; c < nv; c += stride) {
+        ll c = (ll)blockIdx.x * NT + threadIdx.x;
+        for (; c + (UNR - 1) * stride < nv; c += UNR * stride) {
+            Vec<T> xv[UNR], yv[UNR];
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+                xv[u] = vload(x + (c + u * stride) * V);
+                if constexpr (OP == 0 || OP >= 3) yv[u] = vload(y + (c + u * stride) * V);
+            }
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+#pragma unroll
+                for (int e = 0; e < V; e++) one(xv[u].e[e], yv[u].e[e]);
+                if constexpr (OP == 1 || OP >= 3) vstore(x + (c + u * stride) * V, xv[u]);
+                if constexpr (OP == 0 || OP == 2 || OP >= 3) vstore(y + (c + u * stride) * V, yv[u]);
+            }
+        }
+        for (; c < nv; c += stride) {
             Vec<T> xv, yv;
-            if constexpr (OP != 2) xv = vload(x + c * V);
-            else xv = vload(x + c * V);
+            xv = vload(x + c * V);
             if constexpr (OP == 0 || OP >= 3) yv = vload(y + c * V);
 #pragma unroll
             for (int e = 0; e < V; e++) one(xv.e[e], yv.e[e]);
@@ -109,29 +128,43 @@ template <class T, int MODE>
 __global__ void __launch_bounds__(NT) reduce_kernel(int n, const T *x, ll ix, const T *y, ll iy, int vec, double *part) {
     constexpr int V = VW<T>;
     const ll stride = (ll)gridDim.x * NT;
-    double s = 0;
-    auto acc = [&](double a, double b) {
+    double s0 = 0, s1 = 0;   // two chains: FP64 fma latency does not serialize the stream
+    auto acc = [&](double &s, double a, double b) {
         if constexpr (MODE == 0) s = __builtin_fma(a, b, s);
         else if constexpr (MODE == 1) s += __builtin_fabs(a);
         else s = __builtin_fma(a, a, s);
     };
     ll done = 0;
     if (vec) {
+        constexpr int UNR = 4;   // 16-byte chunks per thread and iteration, all loads issued first
         const ll nv = n / V;
-        for (ll c = (ll)blockIdx.x * NT + threadIdx.x; c < nv; c += stride) {
+        ll c = (ll)blockIdx.x * NT + threadIdx.x;
+        for (; c + (UNR - 1) * stride < nv; c += UNR * stride) {
+            Vec<T> xv[UNR], yv[UNR];
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+                xv[u] = vload(x + (c + u * stride) * V);
+                if constexpr (MODE == 0) yv[u] = vload(y + (c + u * stride) * V);
+            }
+#pragma unroll
+            for (int u = 0; u < UNR; u++)
+#pragma unroll
+                for (int e = 0; e < V; e++) acc(e & 1 ? s1 : s0, (double)xv[u].e[e], MODE == 0 ? (double)yv[u].e[e] : 0.0);
+        }
+        for (; c < nv; c += stride) {
             const Vec<T> xv = vload(x + c * V);
             Vec<T> yv;
             if constexpr (MODE == 0) yv = vload(y + c * V);
 #pragma unroll
-            for (int e = 0; e < V; e++) acc((double)xv.e[e], MODE == 0 ? (double)yv.e[e] : 0.0);
+            for (int e = 0; e < V; e++) acc(s0, (double)xv.e[e], MODE == 0 ? (double)yv.e[e] : 0.0);
         }
         done = nv * V;
         ix = 1;
         iy = 1;
     }
     for (ll i = done + (ll)blockIdx.x * NT + threadIdx.x; i < n; i += stride)
-        acc((double)x[i * ix], MODE == 0 ? (double)y[i * iy] : 0.0);
-    const double t = block_sum(s);
+        acc(s0, (double)x[i * ix], MODE == 0 ? (double)y[i * iy] : 0.0);
+    const double t = block_sum(s0 + s1);
     if (threadIdx.x == 0) part[blockIdx.x] = t;
 }
 
@@ -228,23 +261,9 @@ __global__ void __launch_bounds__(NT) gemv_n_kernel(int M, int N, typename Comp<
             for (int r = 0; r < RWN; r++) s[r] = fma_r((R)ar[r][jt], xj, s[r]);
         }
     }
-    // butterfly over RWN = 4 values: two halving exchanges, then plain sums
+    // butterfly over the RWN row sums: two halving exchanges, then plain sums
     int base = 0;
-#pragma unroll
-    for (int st = 0; st < 6; st++) {
-        const int d = 32 >> st, h = RWN >> (st + 1);
-        const bool up = (lane & d) != 0;
-        if (h >= 1) {
-#pragma unroll
-            for (int i = 0; i < h; i++) {
-                const R keep = up ? s[i + h] : s[i], send = up ? s[i] : s[i + h];
-                s[i] = keep + __shfl_xor(send, d);
-            }
-            if (up) base += h;
-        } else {
-            s[0] += __shfl_xor(s[0], d);
-        }
-    }
+    butterfly<0, RWN>(s, lane, base);
     if ((lane & (64 / RWN - 1)) == 0) {
         const int row = r0 + base;
         if (row < M) {

@@ -1,27 +1,29 @@
 // Launcher of the skinny GEMM kernel (C = alpha·a·wᵀ + beta·C, a M×K with M ≤ 16, w N×K, both K-contiguous).
 // Kernel selection replaces the reference's skinny_k1 / skinny_r4 / skinny_r8 choice (reference: lib/src/gemm.c:225-245)
-// with one template over the M tile; the weight-row count RW and the K split KS per M tile are chosen so that
-// every configuration keeps thousands of waves in flight over a 4096×4096 weight matrix.
+// with one template over the M tile. Per M tile, the weight rows per workgroup (RW), the waves splitting K (KS) and
+// the chunks prefetched per lane (NC) are the fastest of a sweep over 155 configurations on MI355X for
+// C = A·Wᵀ with W 4096×4096 FP16 rotated over 32 copies (1 GiB, beyond the 256 MB MALL).
 #include "skinny_kernel.h"
 
 namespace g9 {
 
-template <class T, int MT, int RW, int KS>
+template <class T, int MT, int RW, int KS, int NC>
 static int launch_cfg(const sk::Params &p, bool vec) {
     const dim3 grid((unsigned)((p.N + RW - 1) / RW), (unsigned)((p.M + MT - 1) / MT)), block(KS * 64);
-    if (vec) hipLaunchKernelGGL((sk::skinny_kernel<T, MT, RW, KS, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((sk::skinny_kernel<T, MT, RW, KS, false>), grid, block, 0, stream, p);
+    if (vec) hipLaunchKernelGGL((sk::skinny_kernel<T, MT, RW, KS, NC, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((sk::skinny_kernel<T, MT, RW, KS, NC, false>), grid, block, 0, stream, p);
     G9_HIP(hipGetLastError());
     return 0;
 }
 
 template <class T>
 static int launch_typed(const sk::Params &p, bool vec) {
-    if (p.M <= 1) return launch_cfg<T, 1, 8, 4>(p, vec);
-    if (p.M <= 2) return launch_cfg<T, 2, 8, 4>(p, vec);
-    if (p.M <= 4) return launch_cfg<T, 4, 8, 4>(p, vec);
-    if (p.M <= 8) return launch_cfg<T, 8, 4, 4>(p, vec);
-    return launch_cfg<T, 16, 4, 4>(p, vec);   // M > 16 (forced threshold): tiles of 16 rows, w re-read per tile
+    //                                       MT  RW  KS  NC
+    if (p.M <= 1) return launch_cfg<T, 1, 1, 4, 2>(p, vec);
+    if (p.M <= 2) return launch_cfg<T, 2, 2, 4, 1>(p, vec);
+    if (p.M <= 4) return launch_cfg<T, 4, 4, 8, 1>(p, vec);
+    if (p.M <= 8) return launch_cfg<T, 8, 4, 4, 1>(p, vec);
+    return launch_cfg<T, 16, 8, 4, 1>(p, vec);   // M > 16 (forced threshold): tiles of 16 rows, w re-read per tile
 }
 
 int launch_skinny(const SkinnyCall &c) {
@@ -34,7 +36,7 @@ int launch_skinny(const SkinnyCall &c) {
     const int es = c.type == GEN9BLAS_S ? 4 : 2;
     const bool vec = ((uintptr_t)c.a % 16 == 0) && ((uintptr_t)c.w % 16 == 0) && (c.sam * es) % 16 == 0 &&
                      (c.swn * es) % 16 == 0;
-    if ((long long)(c.N + 7) / 8 > 0x7fffffffLL || (c.M + 15) / 16 > 65535)
+    if ((long long)c.N > 0x7fffffffLL || (c.M + 15) / 16 > 65535)
         G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "skinny grid too large (M %d, N %d)", c.M, c.N);
     if (c.type == GEN9BLAS_S) return launch_typed<float>(p, vec);
     return launch_typed<sk::f16>(p, vec);

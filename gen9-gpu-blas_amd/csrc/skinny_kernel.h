@@ -13,6 +13,7 @@
 //   exchange per value instead of six; then the KS waves combine through LDS.
 #pragma once
 #include "internal.h"
+#include "wave.h"
 
 namespace g9 {
 namespace sk {
@@ -58,7 +59,7 @@ template <class T, bool VEC> __device__ __forceinline__ u32x4 ld16(const T *p) {
     return u.v;
 }
 
-template <class T, int MT, int RW, int KS, bool VEC>
+template <class T, int MT, int RW, int KS, int NC, bool VEC>
 __global__ void __launch_bounds__(KS * 64) skinny_kernel(Params p) {
     constexpr int V = 16 / (int)sizeof(T);
     constexpr int NV = RW * MT;
@@ -76,20 +77,31 @@ __global__ void __launch_bounds__(KS * 64) skinny_kernel(Params p) {
 #pragma unroll
     for (int i = 0; i < NV; i++) v[i] = 0.f;
 
+    // Super-steps of NC chunks per lane: every weight load of a super-step is issued before its first product, so
+    // a wave keeps NC·RW 16-byte loads per lane in flight. Chunk j of lane l in wave wv covers
+    // k = k0 + ((j·KS + wv)·64 + l)·V .. +V-1 (a wave reads 1 KiB contiguous per row and chunk).
     const int K = p.K, kvec = K - K % V;
-    constexpr int STEP = KS * 64 * V;
-    int k = (wv * 64 + lane) * V;
-#pragma unroll 2
-    for (; k < kvec; k += STEP) {
-        u32x4 wq[RW], aq[MT];
+    constexpr int SUPER = NC * KS * 64 * V;
+    const u32x4 zero = {0, 0, 0, 0};
+    for (int k0 = 0; k0 < kvec; k0 += SUPER) {
+        u32x4 wq[NC][RW];
 #pragma unroll
-        for (int r = 0; r < RW; r++) wq[r] = ld16<T, VEC>(wr[r] + k);
+        for (int j = 0; j < NC; j++) {
+            const int k = k0 + ((j * KS + wv) * 64 + lane) * V;
 #pragma unroll
-        for (int m = 0; m < MT; m++) aq[m] = ld16<T, VEC>(ar[m] + k);
+            for (int r = 0; r < RW; r++) wq[j][r] = k < kvec ? ld16<T, VEC>(wr[r] + k) : zero;
+        }
 #pragma unroll
-        for (int r = 0; r < RW; r++)
+        for (int j = 0; j < NC; j++) {
+            const int k = k0 + ((j * KS + wv) * 64 + lane) * V;
+            u32x4 aq[MT];
 #pragma unroll
-            for (int m = 0; m < MT; m++) v[r * MT + m] = dot16<T>(wq[r], aq[m], v[r * MT + m]);
+            for (int m = 0; m < MT; m++) aq[m] = k < kvec ? ld16<T, VEC>(ar[m] + k) : zero;
+#pragma unroll
+            for (int r = 0; r < RW; r++)
+#pragma unroll
+                for (int m = 0; m < MT; m++) v[r * MT + m] = dot16<T>(wq[j][r], aq[m], v[r * MT + m]);
+        }
     }
     // K tail (K % V elements): one element per lane
     for (int kt = kvec + wv * 64 + lane; kt < K; kt += KS * 64) {
@@ -103,24 +115,9 @@ __global__ void __launch_bounds__(KS * 64) skinny_kernel(Params p) {
 
     // transposing butterfly across the wave
     int base = 0;
-#pragma unroll
-    for (int s = 0; s < 6; s++) {
-        const int d = 32 >> s, h = NV >> (s + 1);
-        const bool up = (lane & d) != 0;
-        if (h >= 1) {
-#pragma unroll
-            for (int i = 0; i < h; i++) {
-                const float keep = up ? v[i + h] : v[i], send = up ? v[i] : v[i + h];
-                v[i] = keep + __shfl_xor(send, d);
-            }
-            if (up) base += h;
-        } else {
-            v[0] += __shfl_xor(v[0], d);
-        }
-    }
-    constexpr int NF = NV >= 64 ? NV / 64 : 1;               // sums per lane
-    constexpr int DUP = NV >= 64 ? 1 : 64 / NV;               // lanes holding the same sum
-    const bool writer = (lane & (DUP - 1)) == 0;
+    butterfly<0, NV>(v, lane, base);
+    constexpr int NF = Butterfly<NV>::per_lane;
+    const bool writer = (lane & (Butterfly<NV>::dup - 1)) == 0;
 
     T *C = reinterpret_cast<T *>(p.C);
     auto emit = [&](int idx, float s) {

@@ -133,3 +133,28 @@ def test_level2_config_device(g9, orc, torch_dev):
         ref = Asub @ xv.astype(np.float64)
         scale = np.abs(Asub) @ np.abs(xv.astype(np.float64))
         assert float(np.max(np.abs(yv[rows] - ref) / scale)) <= 1e-6, f"sgemv trans={trans}"
+
+
+def test_reduction_device_result(g9, orc, torch_dev):
+    """dot / asum / nrm2 with the result pointer in device memory (written in place, no host wait), also in
+    no-wait mode; must equal the host-result call bit for bit."""
+    import ctypes
+    torch = torch_dev
+    x = rng.uniform(-1, 1, 300001).astype(np.float32)
+    y = rng.uniform(-1, 1, 300001).astype(np.float32)
+    xd, yd = torch.from_numpy(x).cuda(), torch.from_numpy(y).cuda()
+    out = torch.zeros(3, dtype=torch.float64, device="cuda")
+    L = g9._lib
+
+    def p(addr):   # device address as the double* the signature declares
+        return ctypes.cast(ctypes.c_void_p(addr), ctypes.POINTER(ctypes.c_double))
+    for nowait in (False, True):
+        g9.set_nowait(nowait)
+        assert L.gen9blas_dot(1, x.size, xd.data_ptr(), 1, yd.data_ptr(), 1, p(out.data_ptr())) == 0
+        assert L.gen9blas_asum(1, x.size, xd.data_ptr(), 1, p(out.data_ptr() + 8)) == 0
+        assert L.gen9blas_nrm2(1, x.size, xd.data_ptr(), 1, p(out.data_ptr() + 16)) == 0
+        g9.flush()
+        g9.set_nowait(False)
+        got = out.cpu().numpy()
+        assert got[0] == g9.dot(xd, yd) and got[1] == g9.asum(xd) and got[2] == g9.nrm2(xd)
+        assert abs(got[0] - orc.dot(x, y)) <= 1e-12 * float(np.abs(x) @ np.abs(y))
