@@ -30,14 +30,23 @@ template <class T> __device__ __forceinline__ Vec<T> vload(const T *p) {
     v.u = *reinterpret_cast<const u32x4 *>(p);
     return v;
 }
+// Streamed operands are read once: nontemporal loads keep them from displacing reusable lines in L2 and MALL (about
+// +10 % HBM rate on gfx950 for a single pass). Stores stay ordinary, nontemporal stores measured slower.
+template <class T> __device__ __forceinline__ Vec<T> vload_nt(const T *p) {
+    Vec<T> v;
+    v.u = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return v;
+}
 template <class T> __device__ __forceinline__ void vstore(T *p, const Vec<T> &v) { *reinterpret_cast<u32x4 *>(p) = v.u; }
 __device__ __forceinline__ float fma_r(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 __device__ __forceinline__ double fma_r(double a, double b, double c) { return __builtin_fma(a, b, c); }
 
 constexpr int NT = 256;
-static unsigned stream_grid(ll chunks) {
+// Grid of a streaming kernel: one 16-byte chunk per thread and grid-stride step, at most `per_cu` blocks per CU
+// (4 for kernels with two input streams, 8 for a single read stream: the best HBM rate in a sweep on gfx950).
+static unsigned stream_grid(ll chunks, int per_cu = 4) {
     ll g = (chunks + NT - 1) / NT;
-    const ll cap = (ll)(num_cus > 0 ? num_cus : 256) * 16;
+    const ll cap = (ll)(num_cus > 0 ? num_cus : 256) * per_cu;
     return (unsigned)(g < 1 ? 1 : g > cap ? cap : g);
 }
 
@@ -66,29 +75,11 @@ __global__ void __launch_bounds__(NT) elem_kernel(int n, typename Comp<T>::R h11
         }
     };
     if (vec) {
-        // UNR chunks of 16 bytes per thread and iteration, all loads issued before the first store
-        constexpr int UNR = 4;
         const ll nv = n / V;
-        ll c = (ll)blockIdx.x * NT + threadIdx.x;
-        for (; c + (UNR - 1) * stride < nv; c += UNR * stride) {
-            Vec<T> xv[UNR], yv[UNR];
-#pragma unroll
-            for (int u = 0; u < UNR; u++) {
-                xv[u] = vload(x + (c + u * stride) * V);
-                if constexpr (OP == 0 || OP >= 3) yv[u] = vload(y + (c + u * stride) * V);
-            }
-#pragma unroll
-            for (int u = 0; u < UNR; u++) {
-#pragma unroll
-                for (int e = 0; e < V; e++) one(xv[u].e[e], yv[u].e[e]);
-                if constexpr (OP == 1 || OP >= 3) vstore(x + (c + u * stride) * V, xv[u]);
-                if constexpr (OP == 0 || OP == 2 || OP >= 3) vstore(y + (c + u * stride) * V, yv[u]);
-            }
-        }
-        for (; c < nv; c += stride) {
+        for (ll c = (ll)blockIdx.x * NT + threadIdx.x; c < nv; c += stride) {
             Vec<T> xv, yv;
-            xv = vload(x + c * V);
-            if constexpr (OP == 0 || OP >= 3) yv = vload(y + c * V);
+            xv = vload_nt(x + c * V);
+            if constexpr (OP == 0 || OP >= 3) yv = vload_nt(y + c * V);
 #pragma unroll
             for (int e = 0; e < V; e++) one(xv.e[e], yv.e[e]);
             if constexpr (OP == 1 || OP >= 3) vstore(x + c * V, xv);
@@ -124,6 +115,9 @@ __device__ __forceinline__ double block_sum(double s) {
     return t;   // valid in thread 0
 }
 
+// Two kernels: every block writes its FP64 partial, then reduce_final adds the partials in index order, so the
+// result does not depend on block scheduling. (Finishing in the last block instead needs a device-scope fence per
+// block, which writes back and invalidates the L2 of the XCD: about 35 % of the HBM rate at 1 GiB on gfx950.)
 template <class T, int MODE>
 __global__ void __launch_bounds__(NT) reduce_kernel(int n, const T *x, ll ix, const T *y, ll iy, int vec, double *part) {
     constexpr int V = VW<T>;
@@ -134,44 +128,40 @@ __global__ void __launch_bounds__(NT) reduce_kernel(int n, const T *x, ll ix, co
         else if constexpr (MODE == 1) s += __builtin_fabs(a);
         else s = __builtin_fma(a, a, s);
     };
-    ll done = 0;
+    ll tail = 0;
     if (vec) {
-        constexpr int UNR = 4;   // 16-byte chunks per thread and iteration, all loads issued first
         const ll nv = n / V;
-        ll c = (ll)blockIdx.x * NT + threadIdx.x;
-        for (; c + (UNR - 1) * stride < nv; c += UNR * stride) {
-            Vec<T> xv[UNR], yv[UNR];
-#pragma unroll
-            for (int u = 0; u < UNR; u++) {
-                xv[u] = vload(x + (c + u * stride) * V);
-                if constexpr (MODE == 0) yv[u] = vload(y + (c + u * stride) * V);
-            }
-#pragma unroll
-            for (int u = 0; u < UNR; u++)
-#pragma unroll
-                for (int e = 0; e < V; e++) acc(e & 1 ? s1 : s0, (double)xv[u].e[e], MODE == 0 ? (double)yv[u].e[e] : 0.0);
-        }
-        for (; c < nv; c += stride) {
-            const Vec<T> xv = vload(x + c * V);
+        for (ll c = (ll)blockIdx.x * NT + threadIdx.x; c < nv; c += stride) {
+            const Vec<T> xv = vload_nt(x + c * V);
             Vec<T> yv;
-            if constexpr (MODE == 0) yv = vload(y + c * V);
+            if constexpr (MODE == 0) yv = vload_nt(y + c * V);
 #pragma unroll
-            for (int e = 0; e < V; e++) acc(s0, (double)xv.e[e], MODE == 0 ? (double)yv.e[e] : 0.0);
+            for (int e = 0; e < V; e++) acc(e & 1 ? s1 : s0, (double)xv.e[e], MODE == 0 ? (double)yv.e[e] : 0.0);
         }
-        done = nv * V;
+        tail = nv * V;
         ix = 1;
         iy = 1;
     }
-    for (ll i = done + (ll)blockIdx.x * NT + threadIdx.x; i < n; i += stride)
+    for (ll i = tail + (ll)blockIdx.x * NT + threadIdx.x; i < n; i += stride)
         acc(s0, (double)x[i * ix], MODE == 0 ? (double)y[i * iy] : 0.0);
     const double t = block_sum(s0 + s1);
     if (threadIdx.x == 0) part[blockIdx.x] = t;
 }
 
-// Sum of the partials in a fixed order (deterministic), sqrt for nrm2.
+// Sum of np ≤ FIN·NT partials (more are handled by the plain loop): all loads are issued before the first add, so
+// the kernel costs about one memory latency.
+constexpr int FIN = 8;
 __global__ void __launch_bounds__(NT) reduce_final(int np, const double *part, int mode, double *out) {
+    double v[FIN];
+#pragma unroll
+    for (int j = 0; j < FIN; j++) {
+        const int i = threadIdx.x + j * NT;
+        v[j] = i < np ? part[i] : 0.0;
+    }
     double s = 0;
-    for (int i = threadIdx.x; i < np; i += NT) s += part[i];
+#pragma unroll
+    for (int j = 0; j < FIN; j++) s += v[j];
+    for (int i = threadIdx.x + FIN * NT; i < np; i += NT) s += part[i];
     const double t = block_sum(s);
     if (threadIdx.x == 0) *out = mode == 2 ? __builtin_sqrt(t) : t;
 }
@@ -386,7 +376,7 @@ int launch_reduce(int es, int mode, int n, const void *x, ll ox, ll ix, const vo
         using T = std::remove_pointer_t<decltype(tag)>;
         const T *xp = (const T *)x + ox, *yp = y ? (const T *)y + oy : xp;
         const bool vec = ix == 1 && (mode != 0 || iy == 1) && al16(xp) && (mode != 0 || al16(yp));
-        const unsigned g = stream_grid(vec ? (n + VW<T> - 1) / VW<T> : n);
+        const unsigned g = stream_grid(vec ? (n + VW<T> - 1) / VW<T> : n, mode == 0 ? 4 : 8);
         void *pp;
         G9_TRY(scratch(SLOT_P, g * sizeof(double), &pp));
         double *part = (double *)pp;

@@ -50,7 +50,9 @@ template <> __device__ __forceinline__ float dot16<float>(u32x4 w, u32x4 a, floa
     return acc;
 }
 
-template <class T, bool VEC> __device__ __forceinline__ u32x4 ld16(const T *p) {
+// NTL: nontemporal load, for the weights (read once per call, they should not evict the small operand from L2).
+template <class T, bool VEC, bool NTL = false> __device__ __forceinline__ u32x4 ld16(const T *p) {
+    if constexpr (VEC && NTL) return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
     if constexpr (VEC) return *reinterpret_cast<const u32x4 *>(p);
     constexpr int V = 16 / sizeof(T);
     union { u32x4 v; T e[V]; } u;
@@ -89,7 +91,7 @@ __global__ void __launch_bounds__(KS * 64) skinny_kernel(Params p) {
         for (int j = 0; j < NC; j++) {
             const int k = k0 + ((j * KS + wv) * 64 + lane) * V;
 #pragma unroll
-            for (int r = 0; r < RW; r++) wq[j][r] = k < kvec ? ld16<T, VEC>(wr[r] + k) : zero;
+            for (int r = 0; r < RW; r++) wq[j][r] = k < kvec ? ld16<T, VEC, true>(wr[r] + k) : zero;
         }
 #pragma unroll
         for (int j = 0; j < NC; j++) {
