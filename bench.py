@@ -1,18 +1,20 @@
 """Benchmark of the gen9blas hot path on one MI355X: SGEMM/HGEMM/DGEMM TFLOPS at n = 4096, skinny 4096² FP16 µs/call
 and HBM GB/s, level 1/2 GB/s, each as a fraction of its roofline, with the reference's CPU path timed beside it.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu] [--case NAME ...]
 
 Prints ONE JSON line. `value` is HGEMM (GEN9BLAS_H) TFLOP/s at n = 4096 (NN, alpha = 1, beta = 0, inputs resident in
-HBM); every other configuration of BASELINE.json is in `results`. A step is one library call on one configuration;
+HBM); every other configuration of BASELINE.json is in `results`. A step is one library call on one configuration,
 timed with HIP events recorded on the library's own stream (the stream its kernels run on) around K back-to-back calls
-after W warm-up calls, in no-wait mode (device operands, no host synchronization per call).
-Inputs: np.random.default_rng seeds A = 1, B = 2, C = 3, W copies 100..131, x = 20, y = 21 (synthetic, BASELINE §8d).
+after W warm-up calls, in no-wait mode (device operands, no host synchronization per call). `--case` runs only the
+named cases (for profiling runs; the JSON line then carries only what was measured).
+Inputs: np.random.default_rng seeds A = 1, B = 2, C = 3, W copies 100..131, x = 20, y = 21 (synthetic data).
 """
 import argparse
 import ctypes
 import json
 import os
+import re
 import sys
 import time
 
@@ -23,10 +25,33 @@ sys.path.insert(0, os.path.join(ROOT, "gen9-gpu-blas_amd"))
 
 PEAK_TFLOPS = {"H": 2516.6, "HS": 2516.6, "S": 157.3, "D": 78.6}   # MI355X dense MFMA (datasheet)
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per launch of the headline kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs scaled by a copy kernel
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "hgemm_n4096_hbm_traffic.md")
+
+GEMM_CASES = {
+    "hgemm_n4096": ("H", 4096), "hgemm_accurate_n4096": ("HS", 4096),
+    "hgemm_n1024": ("H", 1024), "hgemm_accurate_n1024": ("HS", 1024),
+    "hgemm_n2048": ("H", 2048), "hgemm_accurate_n2048": ("HS", 2048),
+    "sgemm_n1024": ("S", 1024), "sgemm_n4096": ("S", 4096),
+    "dgemm_n1024": ("D", 1024), "dgemm_n4096": ("D", 4096),
+    "sgemm_odd_3000x11008x4096_tB_beta05": ("S", None),
+}
+QUICK = ("hgemm_n4096", "hgemm_accurate_n4096", "hbm_read_1GiB", "skinny")
+OTHER_CASES = ("hbm_read_1GiB", "skinny", "saxpy_2^26", "sdot_2^26", "sgemv_16384", "copy_256MiB", "calibration")
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def traffic_from_summary():
+    """HBM bytes per launch recorded in the committed PMC summary (line `traffic_bytes_per_launch: N`), or None."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read(), re.M)
+        return float(m.group(1)) if m else None
+    except OSError:
+        return None
 
 
 def main():
@@ -34,13 +59,15 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--quick", action="store_true", help="HGEMM n=4096 and skinny only, no CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="HGEMM n=4096, HBM read and skinny only, no CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--case", action="append", default=[], choices=list(GEMM_CASES) + list(OTHER_CASES))
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the GPU boxes of this build have one GPU and the library is single-device "
               "(multi-GPU sharding is design-only). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    cases = set(args.case) or set(QUICK if args.quick else list(GEMM_CASES) + list(OTHER_CASES))
 
     import torch
     import gen9blas as g9
@@ -49,10 +76,14 @@ def main():
     stream = torch.cuda.ExternalStream(g9.hip_stream())
     steps, warm = args.steps, args.warmup
     dev = torch.device("cuda:0")
-    p, i, d = ctypes.c_void_p, ctypes.c_int, ctypes.c_double
+    p, d = ctypes.c_void_p, ctypes.c_double
 
     def to_dev(x):
         return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+    def check(rc):
+        if rc:
+            raise RuntimeError(L.gen9blas_error().decode())
 
     def timed(fn, k=steps, w=warm):
         """ms per call: HIP events on the library stream around k back-to-back calls after w warm-ups."""
@@ -89,125 +120,106 @@ def main():
         del A, B, C
         args_ = (typ, 0, tB, M, N, K, d(1.0), p(Ad.data_ptr()), K, p(Bd.data_ptr()), K if tB else N, d(beta),
                  p(Cd.data_ptr()), N)
-
-        def fn():
-            rc = L.gen9blas_gemm(*args_)
-            if rc:
-                raise RuntimeError(L.gen9blas_error().decode())
-        ms = timed(fn)
+        ms = timed(lambda: check(L.gen9blas_gemm(*args_)))
         tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
         del Ad, Bd, Cd
         return {"M": M, "N": N, "K": K, "ms": round(ms, 4), "tflops": round(tf, 2),
                 "frac_of_peak": round(tf / PEAK_TFLOPS[kind], 4)}
 
-    log("HGEMM n=4096 ...")
-    res["hgemm_n4096"] = gemm_case("H", 4096)
-    log(res["hgemm_n4096"])
-    res["hgemm_accurate_n4096"] = gemm_case("HS", 4096)
-    if not args.quick:
-        for n in (1024, 2048):
-            res[f"hgemm_n{n}"] = gemm_case("H", n)
-            res[f"hgemm_accurate_n{n}"] = gemm_case("HS", n)
-        log("SGEMM / DGEMM ...")
-        res["sgemm_n1024"] = gemm_case("S", 1024)
-        res["sgemm_n4096"] = gemm_case("S", 4096)
-        res["dgemm_n1024"] = gemm_case("D", 1024)
-        res["dgemm_n4096"] = gemm_case("D", 4096)
-        res["sgemm_odd_3000x11008x4096_tB_beta05"] = gemm_case("S", M=3000, N=11008, K=4096, tB=1, beta=0.5)
-        for k, v in res.items():
-            log(k, v)
+    for name, (kind, n) in GEMM_CASES.items():
+        if name not in cases:
+            continue
+        if n:
+            res[name] = gemm_case(kind, n)
+        else:
+            res[name] = gemm_case(kind, M=3000, N=11008, K=4096, tB=1, beta=0.5)
+        log(name, res[name])
 
     # ---------------- measured HBM bandwidth: streaming read of 1 GiB (> 256 MB MALL) ----------------
-    nh = 1 << 28
-    big = torch.empty(nh, dtype=torch.float32, device=dev).uniform_(-1, 1)
     out_d = torch.zeros(1, dtype=torch.float64, device=dev)   # device result: no host wait per call
     out_p = ctypes.cast(ctypes.c_void_p(out_d.data_ptr()), ctypes.POINTER(ctypes.c_double))
+    hbm = None
+    if "hbm_read_1GiB" in cases:
+        nh = 1 << 28
+        big = torch.empty(nh, dtype=torch.float32, device=dev).uniform_(-1, 1)
+        ms = timed(lambda: check(L.gen9blas_asum(1, nh, p(big.data_ptr()), 1, out_p)), k=10, w=2)
+        hbm = 4.0 * nh / (ms * 1e-3) / 1e9
+        res["hbm_read_1GiB"] = {"kernel": "gen9blas_asum FP32 2^28 (pure streaming read)", "ms": round(ms, 4),
+                                "GBs": round(hbm, 1), "frac_of_datasheet": round(hbm / PEAK_HBM_GBS, 4)}
+        log("hbm_read_1GiB", res["hbm_read_1GiB"])
+        del big
 
-    def rd():
-        rc = L.gen9blas_asum(1, nh, p(big.data_ptr()), 1, out_p)
-        if rc:
-            raise RuntimeError(L.gen9blas_error().decode())
-    ms = timed(rd, k=10, w=2)
-    hbm = 4.0 * nh / (ms * 1e-3) / 1e9
-    res["hbm_read_1GiB"] = {"kernel": "gen9blas_asum FP32 2^28 (pure streaming read)", "ms": round(ms, 4),
-                            "GBs": round(hbm, 1), "frac_of_datasheet": round(hbm / PEAK_HBM_GBS, 4)}
-    log(res["hbm_read_1GiB"])
-    del big
+    def hbm_fracs(r):
+        if hbm:
+            r["frac_of_measured_hbm"] = round(r["GBs"] / hbm, 4)
+        r["frac_of_datasheet_hbm"] = round(r["GBs"] / PEAK_HBM_GBS, 4)
+        return r
 
-    # ---------------- skinny C = A·Wᵀ, W 4096² fp16, 32 rotated copies ----------------
-    log("skinny ...")
-    K = N = 4096
-    ncopy = 32
-    Wd = torch.empty((ncopy, N, K), dtype=torch.float16, device=dev)
-    for c in range(ncopy):
-        w = np.random.default_rng(100 + c).standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
-        Wd[c].copy_(torch.from_numpy(w.astype(np.float16)))
-    sk = {}
-    for M in (1, 2, 4, 8, 16):
-        Ah = np.random.default_rng(1).standard_normal((M, K), dtype=np.float32).astype(np.float16)
-        Ad = to_dev(Ah)
-        Cd = torch.empty((M, N), dtype=torch.float16, device=dev)
+    # ---------------- skinny C = A·Wᵀ, W 4096² fp16, 32 rotated copies (1 GiB) ----------------
+    if "skinny" in cases:
+        K = N = 4096
+        ncopy = 32
+        Wd = torch.empty((ncopy, N, K), dtype=torch.float16, device=dev)
+        for c in range(ncopy):
+            w = np.random.default_rng(100 + c).standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+            Wd[c].copy_(torch.from_numpy(w.astype(np.float16)))
+        sk = {}
         wp = [Wd[c].data_ptr() for c in range(ncopy)]
-        state = {"j": 0}
+        for M in (1, 2, 4, 8, 16):
+            Ad = to_dev(np.random.default_rng(1).standard_normal((M, K), dtype=np.float32).astype(np.float16))
+            Cd = torch.empty((M, N), dtype=torch.float16, device=dev)
+            state = {"j": 0}
 
-        def fn():
-            j = state["j"]
-            state["j"] = (j + 1) % ncopy
-            rc = L.gen9blas_gemm(0, 0, 1, M, N, K, d(1.0), p(Ad.data_ptr()), K, p(wp[j]), K, d(0.0), p(Cd.data_ptr()), N)
-            if rc:
-                raise RuntimeError(L.gen9blas_error().decode())
-        ms = timed(fn, k=max(steps, 32) * 2, w=max(warm, 32))
-        byts = 2.0 * N * K + 2.0 * M * K + 2.0 * M * N
-        gbs = byts / (ms * 1e-3) / 1e9
-        sk[f"M{M}"] = {"us_per_call": round(ms * 1e3, 2), "GBs": round(gbs, 1), "frac_of_measured_hbm": round(gbs / hbm, 4),
-                       "frac_of_datasheet_hbm": round(gbs / PEAK_HBM_GBS, 4)}
-        log(M, sk[f"M{M}"])
-    res["skinny_fp16_4096x4096"] = sk
-    del Wd
+            def fn():
+                j = state["j"]
+                state["j"] = (j + 1) % ncopy
+                check(L.gen9blas_gemm(0, 0, 1, M, N, K, d(1.0), p(Ad.data_ptr()), K, p(wp[j]), K, d(0.0),
+                                      p(Cd.data_ptr()), N))
+            ms = timed(fn, k=max(steps, 32) * 2, w=max(warm, 32))
+            byts = 2.0 * N * K + 2.0 * M * K + 2.0 * M * N
+            sk[f"M{M}"] = hbm_fracs({"us_per_call": round(ms * 1e3, 2), "GBs": round(byts / (ms * 1e-3) / 1e9, 1)})
+            log("skinny", M, sk[f"M{M}"])
+        res["skinny_fp16_4096x4096"] = sk
+        del Wd
 
     # ---------------- level 1/2 ----------------
-    if not args.quick:
-        log("level 1/2 ...")
-        n = 1 << 26
+    n = 1 << 26
+    if cases & {"saxpy_2^26", "sdot_2^26", "copy_256MiB"}:
         xd = to_dev(np.random.default_rng(20).uniform(-1, 1, n).astype(np.float32))
         yd = to_dev(np.random.default_rng(21).uniform(-1, 1, n).astype(np.float32))
-
-        def ax():
-            rc = L.gen9blas_axpy(1, n, d(0.5), p(xd.data_ptr()), 1, p(yd.data_ptr()), 1)
-            if rc:
-                raise RuntimeError(L.gen9blas_error().decode())
-        ms = timed(ax)
-        res["saxpy_2^26"] = {"ms": round(ms, 4), "GBs": round(12.0 * n / (ms * 1e-3) / 1e9, 1)}
-        def dt_():
-            rc = L.gen9blas_dot(1, n, p(xd.data_ptr()), 1, p(yd.data_ptr()), 1, out_p)
-            if rc:
-                raise RuntimeError(L.gen9blas_error().decode())
-        ms = timed(dt_)
-        res["sdot_2^26"] = {"ms": round(ms, 4), "GBs": round(8.0 * n / (ms * 1e-3) / 1e9, 1),
-                            "note": "FP64 result written to device memory"}
+        if "saxpy_2^26" in cases:
+            ms = timed(lambda: check(L.gen9blas_axpy(1, n, d(0.5), p(xd.data_ptr()), 1, p(yd.data_ptr()), 1)))
+            res["saxpy_2^26"] = hbm_fracs({"ms": round(ms, 4), "GBs": round(12.0 * n / (ms * 1e-3) / 1e9, 1)})
+            log("saxpy_2^26", res["saxpy_2^26"])
+        if "sdot_2^26" in cases:
+            ms = timed(lambda: check(L.gen9blas_dot(1, n, p(xd.data_ptr()), 1, p(yd.data_ptr()), 1, out_p)))
+            res["sdot_2^26"] = hbm_fracs({"ms": round(ms, 4), "GBs": round(8.0 * n / (ms * 1e-3) / 1e9, 1),
+                                          "note": "FP64 result written to device memory"})
+            log("sdot_2^26", res["sdot_2^26"])
+        if "copy_256MiB" in cases:
+            # known-size copy (reads 256 MiB, writes 256 MiB): the reference point for the HBM byte counters
+            ms = timed(lambda: check(L.gen9blas_copy(1, n, p(xd.data_ptr()), 1, p(yd.data_ptr()), 1)))
+            res["copy_256MiB"] = hbm_fracs({"ms": round(ms, 4), "GBs": round(8.0 * n / (ms * 1e-3) / 1e9, 1)})
+            log("copy_256MiB", res["copy_256MiB"])
         del xd, yd
+    if "sgemv_16384" in cases:
         m = 16384
         Ad = to_dev(np.random.default_rng(1).uniform(-1, 1, (m, m)).astype(np.float32))
         xv = to_dev(np.random.default_rng(20).uniform(-1, 1, m).astype(np.float32))
         yv = torch.empty(m, dtype=torch.float32, device=dev)
         for tr in (0, 1):
-            def gv():
-                rc = L.gen9blas_gemv(1, tr, m, m, d(1.0), p(Ad.data_ptr()), m, p(xv.data_ptr()), 1, d(0.0),
-                                     p(yv.data_ptr()), 1)
-                if rc:
-                    raise RuntimeError(L.gen9blas_error().decode())
-            ms = timed(gv)
+            ms = timed(lambda: check(L.gen9blas_gemv(1, tr, m, m, d(1.0), p(Ad.data_ptr()), m, p(xv.data_ptr()), 1,
+                                                     d(0.0), p(yv.data_ptr()), 1)))
             byts = 4.0 * m * m + 8.0 * m
-            res[f"sgemv_{'T' if tr else 'N'}_16384"] = {"ms": round(ms, 4), "GBs": round(byts / (ms * 1e-3) / 1e9, 1)}
-        for k in ("saxpy_2^26", "sdot_2^26", "sgemv_N_16384", "sgemv_T_16384"):
-            res[k]["frac_of_measured_hbm"] = round(res[k]["GBs"] / hbm, 4)
+            k = f"sgemv_{'T' if tr else 'N'}_16384"
+            res[k] = hbm_fracs({"ms": round(ms, 4), "GBs": round(byts / (ms * 1e-3) / 1e9, 1)})
             log(k, res[k])
         del Ad
 
     g9.set_nowait(False)
 
     # ---------------- calibration: AMD's libraries through torch.matmul (hipBLASLt / rocBLAS), not this library ----
-    if not args.quick:
+    if "calibration" in cases:
         cal = {}
         for name, tdt in (("fp16", torch.float16), ("fp32", torch.float32), ("fp64", torch.float64)):
             a = torch.randn(4096, 4096, dtype=tdt, device=dev)
@@ -229,19 +241,21 @@ def main():
 
     # ---------------- CPU baseline: the reference's CPU path on the host cores ----------------
     cpu = None
-    if not args.quick and not args.no_cpu:
+    if not args.quick and not args.no_cpu and not args.case:
         cpu = cpu_baseline()
 
-    h = res["hgemm_n4096"]
+    h = res.get("hgemm_n4096")
     line = {
         "metric": "SGEMM/HGEMM/DGEMM TFLOPS @n=4096; skinny 4096² fp16 µs/call + HBM GB/s",
-        "value": h["tflops"], "unit": "TFLOPS", "n_gpus": 1, "steps": steps, "warmup": warm,
-        "ms_per_step": h["ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "value": h["tflops"] if h else None, "unit": "TFLOPS", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": h["ms"] if h else None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp16", "data": "synthetic",
         "config": {"workload": "HGEMM FP16 (GEN9BLAS_H) n=4096 NN alpha=1 beta=0, A,B ~ N(0,1) fp16, HBM-resident",
                    "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": h["tflops"], "peak": PEAK_TFLOPS["H"], "unit": "TFLOP/s",
-                     "frac": h["frac_of_peak"], "traffic": None},
+        "roofline": {"bound": "mfma", "achieved": h["tflops"] if h else None, "peak": PEAK_TFLOPS["H"],
+                     "unit": "TFLOP/s", "frac": h["frac_of_peak"] if h else None, "traffic": traffic_from_summary(),
+                     "traffic_unit": "bytes per launch (HBM, FETCH_SIZE + WRITE_SIZE scaled by a known-size copy)",
+                     "algorithmic_bytes": 3 * 2 * 4096 * 4096},
         "cpu_baseline": cpu,
         "results": res,
     }

@@ -59,8 +59,9 @@ def build(force=False, jobs=None, verbose=True):
         for out in ex.map(_run, todo):
             if out.strip() and verbose:
                 print(out, file=sys.stderr)
-    if force or todo or _stale(LIB, objs):
-        _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-soname,libgen9blas.so", "-o", LIB + ".tmp"] + objs)
+    if force or todo or _stale(LIB, objs + [os.path.join(CSRC, "exports.map")]):
+        _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-soname,libgen9blas.so",
+              "-Wl,--version-script=" + os.path.join(CSRC, "exports.map"), "-o", LIB + ".tmp"] + objs)
         os.replace(LIB + ".tmp", LIB)
     _build_blas(force)
     return LIB

@@ -1,0 +1,78 @@
+"""Status codes and error reporting on a GPU, following the reference's error test (reference: lib/test_errors.py:33-61).
+
+init succeeds once per process; has(unknown) = 0; device_gen is 9; a wrong type gives UNSUPPORTED; a bad leading
+dimension or a zero increment gives INVALID_ARG; gemm_pb(NULL) gives INVALID_ARG; pack_b with a bad type or K = 0
+returns NULL and sets last_status; an impossible pinned allocation returns NULL with OUT_OF_MEMORY. Also: a
+non-positive dimension is a no-op returning 0 (reference: lib/src/gemm.c:10), and gen9blas_error() holds a message
+after every failure.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+OK, DECLINED, ERR, UNSUPPORTED, INVALID, OOM, NO_DEVICE = 0, 1, -1, -2, -3, -4, -5
+
+
+@pytest.fixture(scope="module")
+def L(g9):
+    L = g9._lib
+    i, d, p = ctypes.c_int, ctypes.c_double, ctypes.c_void_p
+    L.gen9blas_gemv.argtypes = [i, i, i, i, d, p, i, p, i, d, p, i]
+    L.gen9blas_axpy.argtypes = [i, i, d, p, i, p, i]
+    L.gen9blas_gemm_pb.argtypes = [i, i, d, p, i, p, d, p, i]
+    L.gen9blas_pack_b.argtypes = [i, i, i, i, p, i]
+    L.gen9blas_pack_b.restype = p
+    return L
+
+
+def test_library_state(L):
+    assert L.gen9blas_version() // 100 == 2
+    assert L.gen9blas_init() == OK
+    assert L.gen9blas_init() == OK
+    assert L.gen9blas_has(999) == 0
+    assert L.gen9blas_has(0) == 1 and L.gen9blas_has(1) == 1 and L.gen9blas_has(2) == 1
+    assert L.gen9blas_device_gen() in (8, 9)
+    assert L.gen9blas_device_arch() == 950
+
+
+def test_status_codes(L):
+    a = np.ones((8, 8), np.float32)
+    b = np.ones((8, 8), np.float32)
+    c = np.zeros((8, 8), np.float32)
+    pa, pb, pc = a.ctypes.data, b.ctypes.data, c.ctypes.data
+    assert L.gen9blas_gemm(1, 0, 0, 8, 8, 8, 1.0, pa, 8, pb, 8, 0.0, pc, 8) == OK
+    assert L.gen9blas_last_status() == OK
+    assert np.all(c == 8.0)
+    assert L.gen9blas_gemm(7, 0, 0, 8, 8, 8, 1.0, pa, 8, pb, 8, 0.0, pc, 8) == UNSUPPORTED
+    assert L.gen9blas_last_status() == UNSUPPORTED and L.gen9blas_error()
+    c[:] = -1
+    for M, N, K in ((0, 8, 8), (8, -1, 8), (8, 8, 0)):
+        assert L.gen9blas_gemm(1, 0, 0, M, N, K, 1.0, pa, 8, pb, 8, 0.0, pc, 8) == OK
+    assert np.all(c == -1), "a call with a non-positive dimension wrote C"
+    assert L.gen9blas_gemm(1, 0, 0, 8, 8, 8, 1.0, pa, 4, pb, 8, 0.0, pc, 8) == INVALID   # lda < K
+    x = np.ones(8, np.float32)
+    y = np.zeros(8, np.float32)
+    assert L.gen9blas_gemv(1, 0, 8, 8, 1.0, pa, 4, x.ctypes.data, 1, 0.0, y.ctypes.data, 1) == INVALID
+    assert L.gen9blas_axpy(1, 8, 1.0, x.ctypes.data, 0, y.ctypes.data, 1) == INVALID
+    assert b"increment" in L.gen9blas_error()
+    assert L.gen9blas_gemm_pb(0, 8, 1.0, pa, 8, None, 0.0, pc, 8) == INVALID
+    assert L.gen9blas_pack_b(7, 0, 8, 8, pb, 8) is None
+    assert L.gen9blas_last_status() == UNSUPPORTED
+    assert L.gen9blas_pack_b(1, 0, 0, 8, pb, 8) is None
+    assert L.gen9blas_last_status() == INVALID
+    assert L.gen9blas_alloc(1 << 44) is None
+    assert L.gen9blas_last_status() == OOM
+    assert L.gen9blas_gemm(1, 0, 0, 8, 8, 8, 1.0, pa, 8, pb, 8, 0.0, pc, 8) == OK   # errors are not sticky
+
+
+def test_functions_outside_this_build_report_unsupported(L):
+    """Entry points of the reference ABI that this build exports without computing them return UNSUPPORTED (so the
+    BLAS shim falls back to the CPU), after the same type check as the reference."""
+    a = np.eye(8, dtype=np.float32)
+    d = ctypes.c_double
+    assert L.gen9blas_symm(1, 0, 0, 8, 8, d(1.0), a.ctypes.data, 8, a.ctypes.data, 8, d(0.0), a.ctypes.data, 8) == UNSUPPORTED
+    assert L.gen9blas_symm(9, 0, 0, 8, 8, d(1.0), a.ctypes.data, 8, a.ctypes.data, 8, d(0.0), a.ctypes.data, 8) == UNSUPPORTED
+    assert b"type 9" in L.gen9blas_error()
