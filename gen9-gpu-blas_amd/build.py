@@ -68,18 +68,24 @@ def build(force=False, jobs=None, verbose=True):
 
 
 def _build_blas(force):
+    """libgen9blas_blas.so: the BLAS / CBLAS shim (blas_shim/blas_shim.c) plus its generated forwarding stubs."""
+    src = os.path.join(HERE, "blas_shim", "blas_shim.c")
     gen = os.path.join(HERE, "blas_shim", "gen_forward.py")
-    src = os.path.join(HERE, "blas_shim", "cblas.c")
-    if not os.path.exists(src):
-        return
-    fwd = os.path.join(BUILD, "cblas_forward.S")
-    if force or _stale(fwd, [gen, src]):
-        out = subprocess.run([sys.executable, gen, src], capture_output=True, text=True, check=True).stdout
-        with open(fwd, "w") as f:
+    hdr = [os.path.join(INCLUDE, h) for h in ("gen9blas.h", "gen9blas_hip.h")]
+    obj = os.path.join(BUILD, "blas_shim.o")
+    fwd_c, fwd_o = os.path.join(BUILD, "blas_forward.c"), os.path.join(BUILD, "blas_forward.o")
+    cflags = ["gcc", "-O2", "-fPIC", "-std=gnu11", "-Wall", "-fvisibility=hidden", "-I" + INCLUDE]
+    if force or _stale(obj, [src] + hdr):
+        _run(cflags + ["-c", src, "-o", obj])
+    if force or _stale(fwd_c, [obj, gen]):
+        out = subprocess.run([sys.executable, gen, obj], capture_output=True, text=True, check=True).stdout
+        with open(fwd_c, "w") as f:
             f.write(out)
-    if force or _stale(BLAS_LIB, [src, fwd, LIB, os.path.join(INCLUDE, "gen9blas.h")]):
-        _run(["gcc", "-O2", "-fPIC", "-shared", "-std=gnu11", "-Wall", "-fvisibility=hidden", "-I" + INCLUDE, src, fwd,
-              "-o", BLAS_LIB + ".tmp", "-L" + HERE, "-lgen9blas", "-Wl,-rpath,$ORIGIN", "-ldl", "-lpthread"])
+    if force or _stale(fwd_o, [fwd_c]):
+        _run(cflags + ["-c", fwd_c, "-o", fwd_o])
+    if force or _stale(BLAS_LIB, [obj, fwd_o, LIB]):
+        _run(["gcc", "-shared", "-fPIC", "-Wl,-soname,libgen9blas_blas.so", "-o", BLAS_LIB + ".tmp", obj, fwd_o,
+              "-L" + HERE, "-lgen9blas", "-Wl,-rpath,$ORIGIN", "-ldl", "-lpthread"])
         os.replace(BLAS_LIB + ".tmp", BLAS_LIB)
 
 

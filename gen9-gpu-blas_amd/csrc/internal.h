@@ -56,8 +56,10 @@ struct Operand {
     bool written = false;        // kernels write it: copy back after the wait when staged
 };
 // Resolves op (host, rows, cols, ld, es set by the caller) for the kernels. Device memory is used in place; host
-// memory goes into the work buffer `slot`, with a row stride rounded up to 16 bytes when `repitch` (copy_in: with
-// the data; otherwise the buffer contents are undefined, as for outputs not read).
+// memory goes into the work buffer `slot` as one copy of the caller's span with the caller's row stride, or, when
+// `repitch` and row gaps make up more than half of the span, packed with a row stride rounded up to 16 bytes
+// (copy_in: with the data; otherwise the buffer contents are undefined, as for outputs not read, except the gaps of
+// a written operand, which are copied in so the copy back preserves them).
 G9_HIDDEN int resolve(Operand &op, int slot, bool copy_in, bool written, bool repitch);
 // 1 if p .. p+bytes lies in one device allocation.
 G9_HIDDEN int is_device(const void *p, size_t bytes);

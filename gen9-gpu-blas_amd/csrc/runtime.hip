@@ -162,18 +162,24 @@ int resolve(Operand &op, int slot, bool copy_in, bool written, bool repitch) {
         return 0;
     }
     op.zc = false;
-    if (repitch && op.rows > 1) {
+    // Host memory moves in one 1D copy of the caller's span with the caller's leading dimension: from pageable
+    // memory a 2D copy goes row by row (about 20 µs per row). Only a matrix whose row gaps make up more than half of
+    // its span is packed by a 2D copy instead.
+    const size_t dense = (size_t)op.rows * (size_t)op.cols * es;
+    if (repitch && op.rows > 1 && span > 2 * dense) {
         const size_t pitch = ((size_t)op.cols * es + 15) / 16 * 16;
         op.ld = (long long)(pitch / es);
         G9_TRY(scratch(slot, pitch * (size_t)op.rows, &op.dev));
         if (copy_in)
             G9_HIP(hipMemcpy2DAsync(op.dev, pitch, op.host, (size_t)op.caller_ld * es, (size_t)op.cols * es,
                                     (size_t)op.rows, hipMemcpyHostToDevice, stream));
-    } else {
-        op.ld = op.caller_ld;
-        G9_TRY(scratch(slot, span, &op.dev));
-        if (copy_in) G9_HIP(hipMemcpyAsync(op.dev, op.host, span, hipMemcpyHostToDevice, stream));
+        return 0;
     }
+    op.ld = op.caller_ld;
+    G9_TRY(scratch(slot, span, &op.dev));
+    // the copy back rewrites the whole span: gap elements of a written operand must hold the caller's values
+    if (written && span > dense) copy_in = true;
+    if (copy_in) G9_HIP(hipMemcpyAsync(op.dev, op.host, span, hipMemcpyHostToDevice, stream));
     return 0;
 }
 
@@ -247,6 +253,7 @@ int gen9blas_init(void) { return begin(); }
 int gen9blas_device_gen(void) { return begin() ? 0 : 9; }
 
 int gen9blas_device_arch(void) { return begin() ? 0 : arch; }
+int gen9blas_is_device(const void *p, size_t bytes) { return begin() ? 0 : is_device(p, bytes ? bytes : 1); }
 
 int gen9blas_has(int f) {
     if (begin()) return 0;

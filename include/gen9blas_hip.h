@@ -18,6 +18,9 @@ GEN9BLAS_API void *gen9blas_hip_stream(void);
 // Device memory (hipMalloc). Pointers into it are used in place by every entry point.
 GEN9BLAS_API void *gen9blas_device_alloc(size_t bytes);
 GEN9BLAS_API void gen9blas_device_free(void *p);
+// 1 when [p, p+bytes) lies in one HIP device (or managed) allocation, which kernels use in place; 0 for host memory,
+// NULL, or without a device. The BLAS shim uses it to keep device operands off the CPU BLAS.
+GEN9BLAS_API int gen9blas_is_device(const void *p, size_t bytes);
 // Copy between any two of host / pinned host / device memory, synchronous on the library stream.
 GEN9BLAS_API int gen9blas_memcpy(void *dst, const void *src, size_t bytes);
 // No-wait mode: while on, a call whose operands are all device memory queues its kernels and returns without waiting

@@ -1,0 +1,122 @@
+"""libgen9blas_blas.so (the BLAS / CBLAS shim) without a GPU: every call must reach the CPU BLAS with BLAS results.
+
+Checks the reference BLAS layer's contract (reference: lib/src/cblas.c:1-562, lib/test_blas.py, lib/test_blas_d.py)
+on the CPU side: the library loads and finds a CPU BLAS, it exports its own S/D entry points plus a forwarding stub
+for every other BLAS/CBLAS symbol of that CPU BLAS, row- and column-major CBLAS calls and Fortran calls give the
+float64 closed-form results (bounds 1e-5 FP32 / 1e-12 FP64 as in the reference's tests), and forwarded functions
+(here ssymm, dsymm) work. Without a device the routing sends everything to the CPU, so these run anywhere.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import blas_shim_util as U
+
+rng = np.random.default_rng(5)
+TOL = {"s": 1e-5, "d": 1e-12}
+DT = {"s": np.float32, "d": np.float64}
+
+
+@pytest.fixture(scope="module")
+def L():
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU is present: the GPU module covers the shim there")
+    if not os.path.exists(U.SHIM):
+        pytest.fail("libgen9blas_blas.so is not built: run python gen9-gpu-blas_amd/build.py")
+    return U.load()
+
+
+def test_exports(L):
+    out = subprocess.run(["nm", "-D", "--defined-only", U.SHIM], capture_output=True, text=True, check=True).stdout
+    syms = {l.split()[-1] for l in out.splitlines() if l.strip()}
+    assert U.OWN <= syms
+    blas = {s for s in syms if s.startswith("cblas_") or s.endswith("_")}
+    assert len(blas) == len(syms), f"non-BLAS exports: {sorted(syms - blas)[:10]}"
+    for s in ("cblas_zgemm", "cblas_csyrk", "dtrsm_", "cblas_sgbmv", "xerbla_", "cblas_dtrsv", "zdotc_"):
+        assert s in syms, s
+    assert len(syms) > 300
+
+
+@pytest.mark.parametrize("P", ["s", "d"])
+@pytest.mark.parametrize("order", [U.ROW, U.COL])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_cblas_gemm(L, P, order, ta, tb):
+    dt = DT[P]
+    M, N, K = 37, 29, 45
+    opA = rng.uniform(-1, 1, (M, K)).astype(dt)
+    opB = rng.uniform(-1, 1, (K, N)).astype(dt)
+    C0 = rng.uniform(-1, 1, (M, N)).astype(dt)
+    A = opA.T.copy() if ta else opA
+    B = opB.T.copy() if tb else opB
+    if order == U.COL:   # column-major storage of the same matrices
+        Af, Bf, C = np.asfortranarray(A), np.asfortranarray(B), np.asfortranarray(C0.copy())
+        lda, ldb, ldc = A.shape[0], B.shape[0], M
+    else:
+        Af, Bf, C = A, B, C0.copy()
+        lda, ldb, ldc = A.shape[1], B.shape[1], N
+    getattr(L, f"cblas_{P}gemm")(order, U.T if ta else U.NT, U.T if tb else U.NT, M, N, K, 1.5, U.ptr(Af), lda,
+                                 U.ptr(Bf), ldb, -0.5, U.ptr(C), ldc)
+    ref = 1.5 * opA.astype(np.float64) @ opB + -0.5 * C0
+    scale = 1.5 * np.abs(opA.astype(np.float64)) @ np.abs(opB) + 0.5 * np.abs(C0)
+    assert U.ref_error(C, ref, scale) <= TOL[P]
+
+
+@pytest.mark.parametrize("P", ["s", "d"])
+def test_fortran_gemm(L, P):
+    dt = DT[P]
+    M, N, K = 20, 33, 17
+    A = np.asfortranarray(rng.uniform(-1, 1, (K, M)).astype(dt))    # op(A) = Aᵀ
+    B = np.asfortranarray(rng.uniform(-1, 1, (K, N)).astype(dt))
+    C = np.asfortranarray(np.zeros((M, N), dt))
+    U.fortran_gemm(L, P, "t", "N", M, N, K, 2.0, A, K, B, K, 0.0, C, M)
+    ref = 2.0 * A.T.astype(np.float64) @ B
+    assert U.ref_error(C, ref, 2.0 * np.abs(A.T.astype(np.float64)) @ np.abs(B)) <= TOL[P]
+
+
+@pytest.mark.parametrize("P", ["s", "d"])
+def test_gemv_ger_level1(L, P):
+    dt = DT[P]
+    M, N = 50, 70
+    A = rng.uniform(-1, 1, (M, N)).astype(dt)
+    x, y = rng.uniform(-1, 1, N).astype(dt), rng.uniform(-1, 1, M).astype(dt)
+    y0 = y.copy()
+    getattr(L, f"cblas_{P}gemv")(U.ROW, U.NT, M, N, 1.0, U.ptr(A), N, U.ptr(x), 1, 0.5, U.ptr(y), 1)
+    ref = A.astype(np.float64) @ x + 0.5 * y0
+    assert U.ref_error(y, ref, np.abs(A.astype(np.float64)) @ np.abs(x) + 0.5 * np.abs(y0)) <= TOL[P]
+    A2 = A.copy()
+    getattr(L, f"cblas_{P}ger")(U.COL, N, M, -1.0, U.ptr(x), 1, U.ptr(y0), 1, U.ptr(A2), N)   # Aᵀ col-major = A
+    assert U.ref_error(A2, A - np.outer(y0, x), np.abs(A) + np.abs(np.outer(y0, x))) <= TOL[P]
+    v, w = rng.uniform(-1, 1, 1000).astype(dt), rng.uniform(-1, 1, 1000).astype(dt)
+    V, W = v.astype(np.float64), w.astype(np.float64)
+    assert abs(getattr(L, f"cblas_{P}dot")(1000, U.ptr(v), 1, U.ptr(w), 1) - V @ W) <= TOL[P] * (abs(V) @ abs(W))
+    assert abs(getattr(L, f"cblas_{P}asum")(1000, U.ptr(v), 1) - abs(V).sum()) <= TOL[P] * abs(V).sum()
+    assert abs(getattr(L, f"cblas_{P}nrm2")(1000, U.ptr(v), 1) - np.linalg.norm(V)) <= TOL[P] * np.linalg.norm(V)
+    assert getattr(L, f"cblas_i{P}amax")(1000, U.ptr(v), 1) == int(np.argmax(abs(V)))
+    getattr(L, f"cblas_{P}axpy")(1000, 0.25, U.ptr(v), 1, U.ptr(w), 1)
+    assert U.ref_error(w, 0.25 * V + W, 0.25 * abs(V) + abs(W)) <= TOL[P]
+    getattr(L, f"cblas_{P}scal")(500, -2.0, U.ptr(v), 2)
+    assert np.array_equal(v[::2], (-2.0 * V[::2]).astype(dt)) and np.array_equal(v[1::2], V[1::2].astype(dt))
+
+
+def test_mixed_precision_dots(L):
+    """On the CPU these are the CPU BLAS's own (SciPy's OpenBLAS sums dsdot in FP32: 1e-6, not FP64 accuracy)."""
+    v, w = rng.uniform(-1, 1, 999).astype(np.float32), rng.uniform(-1, 1, 999).astype(np.float32)
+    exact = v.astype(np.float64) @ w.astype(np.float64)
+    scale = np.abs(v).astype(np.float64) @ np.abs(w)
+    assert abs(L.cblas_dsdot(999, U.ptr(v), 1, U.ptr(w), 1) - exact) <= 1e-5 * scale
+    assert abs(L.cblas_sdsdot(999, 0.5, U.ptr(v), 1, U.ptr(w), 1) - (0.5 + exact)) <= 1e-5 * scale
+
+
+@pytest.mark.parametrize("P", ["s", "d"])
+def test_forwarded_symm(L, P):
+    """A function the shim forwards to the CPU BLAS by a tail jump (not routed): results as BLAS."""
+    dt = DT[P]
+    A = rng.uniform(-1, 1, (30, 30)).astype(dt)
+    S = np.tril(A) + np.tril(A, -1).T            # the lower triangle defines the symmetric matrix
+    B = rng.uniform(-1, 1, (30, 20)).astype(dt)
+    C = np.zeros((30, 20), dt)
+    getattr(L, f"cblas_{P}symm")(U.ROW, 141, 122, 30, 20, 1.0, U.ptr(A), 30, U.ptr(B), 20, 0.0, U.ptr(C), 20)
+    assert U.ref_error(C, S.astype(np.float64) @ B, np.abs(S.astype(np.float64)) @ np.abs(B)) <= TOL[P]

@@ -1,0 +1,107 @@
+"""libgen9blas_blas.so on a GPU (GEN9BLAS_BLAS=auto): where each call runs, and its results.
+
+Routing (GEN9BLAS_BLAS_INFO=1 names the side of every routed call): host-memory level 3 above the flop threshold
+(1e9) and any call of 2^16 elements or more with device operands run on the GPU; smaller level 3 and host-memory
+level 1-2 stay on the CPU BLAS. Results
+against float64 closed forms under the reference's BLAS-test bounds (reference: lib/test_blas.py, lib/test_blas_d.py:
+1e-5 FP32, 1e-12 FP64), the mixed dots under FP64 accuracy (the GPU accumulates in FP64).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import blas_shim_util as U
+
+pytestmark = pytest.mark.gpu
+rng = np.random.default_rng(6)
+TOL = {"s": 1e-5, "d": 1e-12}
+DT = {"s": np.float32, "d": np.float64}
+
+
+@pytest.fixture(scope="module")
+def L(g9):
+    os.environ["GEN9BLAS_BLAS_INFO"] = "1"   # read at the shim's first routed call
+    os.environ.pop("GEN9BLAS_BLAS", None)
+    os.environ.pop("GEN9BLAS_BLAS_L3_MIN", None)
+    return U.load()
+
+
+def routes(capfd):
+    return [l.split("-> ")[1] for l in capfd.readouterr().err.splitlines() if l.startswith("gen9blas_blas:") and "->" in l]
+
+
+@pytest.mark.parametrize("P", ["s", "d"])
+@pytest.mark.parametrize("order", [U.ROW, U.COL])
+def test_gemm_host_routes_by_size(L, capfd, P, order):
+    dt = DT[P]
+    for n, side in ((96, "CPU"), (512, "CPU"), (1024, "GPU")):
+        A, B = rng.uniform(-1, 1, (n, n)).astype(dt), rng.uniform(-1, 1, (n, n)).astype(dt)
+        C0 = rng.uniform(-1, 1, (n, n)).astype(dt)
+        C = C0.copy()
+        capfd.readouterr()
+        # column-major call on the same buffers computes Cᵀ = Aᵀ·Bᵀ... in row-major terms: C = B·A for these arrays
+        getattr(L, f"cblas_{P}gemm")(order, U.NT, U.T, n, n, n, 1.0, U.ptr(A), n, U.ptr(B), n, 0.5, U.ptr(C), n)
+        assert routes(capfd) == [side], (n, side)
+        Ad, Bd = A.astype(np.float64), B.astype(np.float64)
+        if order == U.ROW:
+            ref, scale = Ad @ Bd.T, np.abs(Ad) @ np.abs(Bd.T)
+        else:
+            ref, scale = (Ad.T @ Bd).T, (np.abs(Ad.T) @ np.abs(Bd)).T
+        assert U.ref_error(C, ref + 0.5 * C0, scale + 0.5 * np.abs(C0)) <= TOL[P]
+
+
+@pytest.mark.parametrize("P", ["s", "d"])
+def test_fortran_gemm_on_gpu(L, capfd, P):
+    dt = DT[P]
+    M, N, K = 1000, 1100, 900   # 2e9 flops: above the host-memory threshold
+    A = np.asfortranarray(rng.uniform(-1, 1, (M, K)).astype(dt))
+    B = np.asfortranarray(rng.uniform(-1, 1, (N, K)).astype(dt))    # op(B) = Bᵀ
+    C = np.asfortranarray(np.zeros((M, N), dt))
+    capfd.readouterr()
+    U.fortran_gemm(L, P, "N", "T", M, N, K, 1.0, A, M, B, N, 0.0, C, M)
+    assert routes(capfd) == ["GPU"]
+    Ad, Bd = A.astype(np.float64), B.astype(np.float64)
+    assert U.ref_error(C, Ad @ Bd.T, np.abs(Ad) @ np.abs(Bd.T)) <= TOL[P]
+
+
+@pytest.mark.parametrize("P", ["s", "d"])
+def test_level12_host_stays_on_cpu_device_goes_to_gpu(L, capfd, torch_dev, P):
+    torch = torch_dev
+    dt = DT[P]
+    n = 1 << 20
+    x, y = rng.uniform(-1, 1, n).astype(dt), rng.uniform(-1, 1, n).astype(dt)
+    X, Y = x.astype(np.float64), y.astype(np.float64)
+    capfd.readouterr()
+    got = getattr(L, f"cblas_{P}dot")(n, U.ptr(x), 1, U.ptr(y), 1)
+    assert routes(capfd) == ["CPU"]
+    assert abs(got - X @ Y) <= TOL[P] * (abs(X) @ abs(Y))
+    xd, yd = torch.from_numpy(x).cuda(), torch.from_numpy(y).cuda()
+    got = getattr(L, f"cblas_{P}dot")(n, U.ptr(xd), 1, U.ptr(yd), 1)
+    getattr(L, f"cblas_{P}axpy")(n, 0.5, U.ptr(xd), 1, U.ptr(yd), 1)
+    assert routes(capfd) == ["GPU", "GPU"]
+    # FP64 accumulation on the GPU, then (sdot) one rounding of the result to float
+    assert abs(got - X @ Y) <= 1e-12 * (abs(X) @ abs(Y)) + (6e-8 * abs(X @ Y) if P == "s" else 0)
+    assert U.ref_error(yd.cpu().numpy(), 0.5 * X + Y, 0.5 * abs(X) + abs(Y)) <= TOL[P]
+    M, N = 1000, 3000
+    A = rng.uniform(-1, 1, (M, N)).astype(dt)
+    v = rng.uniform(-1, 1, M).astype(dt)
+    Ad, vd = torch.from_numpy(A).cuda(), torch.from_numpy(v).cuda()
+    out = torch.zeros(N, dtype=Ad.dtype, device="cuda")
+    # column-major view of the row-major A is Aᵀ (N×M, lda = N): y = Aᵀ·v
+    getattr(L, f"cblas_{P}gemv")(U.COL, U.NT, N, M, 1.0, U.ptr(Ad), N, U.ptr(vd), 1, 0.0, U.ptr(out), 1)
+    assert routes(capfd) == ["GPU"]
+    Af = A.astype(np.float64)
+    assert U.ref_error(out.cpu().numpy(), Af.T @ v, np.abs(Af.T) @ np.abs(v.astype(np.float64))) <= TOL[P]
+
+
+def test_mixed_dots_fp64_on_device(L, capfd, torch_dev):
+    torch = torch_dev
+    v, w = rng.uniform(-1, 1, 100003).astype(np.float32), rng.uniform(-1, 1, 100003).astype(np.float32)
+    exact = v.astype(np.float64) @ w.astype(np.float64)
+    vd, wd = torch.from_numpy(v).cuda(), torch.from_numpy(w).cuda()
+    capfd.readouterr()
+    assert abs(L.cblas_dsdot(v.size, U.ptr(vd), 1, U.ptr(wd), 1) - exact) <= 1e-12 * (np.abs(v) @ np.abs(w))
+    got = L.cblas_sdsdot(v.size, 0.25, U.ptr(vd), 1, U.ptr(wd), 1)   # FP64 sum, one rounding to float
+    assert abs(got - (0.25 + exact)) <= 6e-8 * abs(0.25 + exact)
+    assert routes(capfd) == ["GPU", "GPU"]
