@@ -37,7 +37,8 @@ GEMM_CASES = {
     "sgemm_odd_3000x11008x4096_tB_beta05": ("S", None),
 }
 QUICK = ("hgemm_n4096", "hgemm_accurate_n4096", "hbm_read_1GiB", "skinny")
-OTHER_CASES = ("hbm_read_1GiB", "skinny", "saxpy_2^26", "sdot_2^26", "sgemv_16384", "copy_256MiB", "calibration")
+OTHER_CASES = ("hgemm_n4096_host", "hbm_read_1GiB", "skinny", "saxpy_2^26", "sdot_2^26", "sgemv_16384", "copy_256MiB",
+               "calibration")
 
 
 def log(*a):
@@ -134,6 +135,28 @@ def main():
         else:
             res[name] = gemm_case(kind, M=3000, N=11008, K=4096, tB=1, beta=0.5)
         log(name, res[name])
+
+    # ---------------- the same HGEMM on host (pageable NumPy) buffers: PCIe-inclusive whole call, not `value` ------
+    if "hgemm_n4096_host" in cases:
+        n = 4096
+        A = np.random.default_rng(1).standard_normal((n, n), dtype=np.float32).astype(np.float16)
+        B = np.random.default_rng(2).standard_normal((n, n), dtype=np.float32).astype(np.float16)
+        C = np.empty((n, n), np.float16)
+        call = lambda: check(L.gen9blas_gemm(0, 0, 0, n, n, n, d(1.0), p(A.ctypes.data), n, p(B.ctypes.data), n,
+                                             d(0.0), p(C.ctypes.data), n))
+        g9.set_nowait(False)   # host operands: every call copies in, computes, copies back and waits
+        call()
+        ts = []
+        for _ in range(max(3, steps // 4)):
+            t = time.perf_counter()
+            call()
+            ts.append(time.perf_counter() - t)
+        g9.set_nowait(True)
+        ms = float(np.median(ts)) * 1e3
+        res["hgemm_n4096_host"] = {"ms": round(ms, 3), "tflops": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 2),
+                                   "note": "whole call on pageable host buffers: 2 x 32 MiB in, 32 MiB out over PCIe"}
+        log("hgemm_n4096_host", res["hgemm_n4096_host"])
+        del A, B, C
 
     # ---------------- measured HBM bandwidth: streaming read of 1 GiB (> 256 MB MALL) ----------------
     out_d = torch.zeros(1, dtype=torch.float64, device=dev)   # device result: no host wait per call

@@ -195,3 +195,37 @@ def test_gemm_exact_small_integers(g9, torch_dev):
                     B = np.ascontiguousarray(b.T).T if tb else b
                     W = g9.gemm(A, B)
                     assert np.array_equal(W.astype(np.int64), ref), f"{dt} {M}x{N}x{K} tA={ta} tB={tb}"
+
+
+def test_banded_launch(tmp_path):
+    """GEN9BLAS_MAX_LAUNCH_MS splits a long product into row bands, each its own launch (reference:
+    lib/src/gemm.c:119-164): results equal the unbanded call's. The variable is read once per process, so the banded
+    call runs in a child process (one extra GPU process, sequential)."""
+    import os
+    import subprocess
+    import sys
+    script = tmp_path / "banded.py"
+    script.write_text(
+        "import sys, numpy as np\n"
+        f"sys.path.insert(0, {os.path.join(os.path.dirname(os.path.dirname(os.path.realpath(__file__))), 'gen9-gpu-blas_amd')!r})\n"
+        "import gen9blas as g\n"
+        "rng = np.random.default_rng(4)\n"
+        "for dt in (np.float32, np.float64, np.float16):\n"
+        "    a = rng.uniform(-1, 1, (1100, 700)).astype(dt); b = rng.uniform(-1, 1, (700, 900)).astype(dt)\n"
+        "    c0 = rng.uniform(-1, 1, (1100, 900)).astype(dt)\n"
+        "    c = g.gemm(a, b, 1.5, 0.5, c0.copy())\n"
+        "    np.save(sys.argv[1] + '_' + np.dtype(dt).name + '.npy', c)\n")
+    outs = {}
+    for band in ("", "0.0001"):
+        env = dict(os.environ)
+        env.pop("GEN9BLAS_MAX_LAUNCH_MS", None)
+        if band:
+            env["GEN9BLAS_MAX_LAUNCH_MS"] = band
+        prefix = str(tmp_path / ("banded" if band else "plain"))
+        r = subprocess.run([sys.executable, str(script), prefix], env=env, capture_output=True, text=True, timeout=100)
+        assert r.returncode == 0, r.stderr[-2000:]
+        outs[band] = prefix
+    for dt in ("float32", "float64", "float16"):
+        plain = np.load(outs[""] + "_" + dt + ".npy")
+        banded = np.load(outs["0.0001"] + "_" + dt + ".npy")
+        assert np.array_equal(plain, banded), dt   # bands compute the same per-element sums in the same order
