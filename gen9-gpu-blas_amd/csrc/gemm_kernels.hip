@@ -1,6 +1,10 @@
 // Host side of the MFMA GEMM: tile configuration per type and dispatch over the transpose layouts.
-// The kernel template and its design notes are in gemm_kernel.h.
+// The kernel templates and their design notes are in gemm_kernel.h (every shape and type) and hgemm_kernel.h
+// (FP16, whole tiles, direct global→LDS loads).
 #include "gemm_kernel.h"
+#include "hgemm_kernel.h"
+#include <stdlib.h>
+#include <string.h>
 
 namespace g9 {
 
@@ -46,6 +50,59 @@ static int launch_layout(const GemmParams<typename Mma<T>::Sum> &p, int count) {
     return launch_t<T, CF::big, AK, BKC, VEC>(p, count);
 }
 
+// ---------------- FP16 whole-tile kernel ----------------
+// Configurations from a sweep on MI355X with N(0,1) FP16 inputs (n = 4096: 256×256 with 8 waves, KB = 64, two
+// stages: NN 1052 TFLOP/s; n = 2048: 128×128, 4 waves, KB = 64, four stages: 662; n = 1024: 128×128, two stages).
+// Products with fewer big tiles than CUs take the 128×128 tile.
+template <int BM, int BN, int WM, int WN, int KB, int NS, bool AK, bool BKC>
+static int launch_hg(const hg::Params &p0, int count) {
+    hg::Params p = p0;
+    p.tiles_m = p.M / BM;
+    p.tiles_n = p.N / BN;
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)count), block(WM * WN * 64);
+    hipLaunchKernelGGL((hg::hgemm_kernel<BM, BN, WM, WN, KB, NS, AK, BKC>), grid, block, 0, stream, p);
+    G9_HIP(hipGetLastError());
+    return 0;
+}
+template <bool AK, bool BKC>
+static int launch_hg_layout(const hg::Params &p, int count) {
+    if ((long long)(p.M / 256) * (p.N / 256) * count >= num_cus && p.M % 256 == 0 && p.N % 256 == 0)
+        return launch_hg<256, 256, 2, 4, 64, 2, AK, BKC>(p, count);
+    if (p.K / 64 >= 32) return launch_hg<128, 128, 2, 2, 64, 4, AK, BKC>(p, count);
+    return launch_hg<128, 128, 2, 2, 64, 2, AK, BKC>(p, count);
+}
+// The whole-tile FP16 kernel applies when every operand is 16-byte aligned with 16-byte row strides, M and N are
+// multiples of 128, K of 64, and the grid fits. GEN9BLAS_HGEMM=generic forces the general kernel.
+static bool hgemm_tiles_apply(const GemmCall &c) {
+    static int generic = -1;
+    if (generic < 0) {
+        const char *e = getenv("GEN9BLAS_HGEMM");
+        generic = e && !strcmp(e, "generic");
+    }
+    if (generic || c.M % 128 || c.N % 128 || c.K % 64 || c.count > 65535) return false;
+    const long long es = 2;
+    return (uintptr_t)c.A % 16 == 0 && (uintptr_t)c.B % 16 == 0 && (uintptr_t)c.C % 16 == 0 && (c.lda * es) % 16 == 0 &&
+           (c.ldb * es) % 16 == 0 && (c.ldc * es) % 16 == 0 &&
+           (c.count == 1 || ((c.sA * es) % 16 == 0 && (c.sB * es) % 16 == 0 && (c.sC * es) % 16 == 0));
+}
+static int launch_hgemm_tiles(const GemmCall &c) {
+    hg::Params p;
+    p.A = reinterpret_cast<const hg::f16 *>(c.A);
+    p.B = reinterpret_cast<const hg::f16 *>(c.B);
+    p.C = reinterpret_cast<hg::f16 *>(c.C);
+    p.lda = c.lda; p.ldb = c.ldb; p.ldc = c.ldc;
+    p.sA = c.sA; p.sB = c.sB; p.sC = c.sC;
+    p.M = c.M; p.N = c.N; p.K = c.K;
+    p.tiles_m = p.tiles_n = 0;
+    p.alpha = (float)c.alpha;
+    p.beta = (float)c.beta;
+    const bool ak = !c.tA, bk = c.tB;
+    if (ak && bk) return launch_hg_layout<true, true>(p, c.count);
+    if (ak) return launch_hg_layout<true, false>(p, c.count);
+    if (bk) return launch_hg_layout<false, true>(p, c.count);
+    return launch_hg_layout<false, false>(p, c.count);
+}
+
 template <class T>
 static int launch_typed(const GemmCall &c) {
     using S = typename Mma<T>::Sum;
@@ -79,7 +136,7 @@ static int launch_typed(const GemmCall &c) {
 int launch_gemm(const GemmCall &c) {
     switch (c.type) {
     case GEN9BLAS_H:
-    case GEN9BLAS_HS: return launch_typed<f16>(c);
+    case GEN9BLAS_HS: return hgemm_tiles_apply(c) ? launch_hgemm_tiles(c) : launch_typed<f16>(c);
     case GEN9BLAS_S: return launch_typed<float>(c);
     case GEN9BLAS_D: return launch_typed<double>(c);
     }

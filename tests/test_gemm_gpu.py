@@ -197,6 +197,44 @@ def test_gemm_exact_small_integers(g9, torch_dev):
                     assert np.array_equal(W.astype(np.int64), ref), f"{dt} {M}x{N}x{K} tA={ta} tB={tb}"
 
 
+@pytest.mark.parametrize("M,N,K,count", [(256, 384, 320, 1), (128, 256, 2112, 1), (1024, 1024, 192, 16)])
+def test_hgemm_whole_tile_kernel(g9, torch_dev, M, N, K, count):
+    """Shapes served by the whole-tile FP16 kernel (M, N multiples of 128, K of 64, 16-byte aligned operands): 128×128
+    tiles with two and with four LDS stages, and 256×256 tiles over a batch of 16, in every transpose layout, through
+    the C ABI on device memory. Small-integer inputs make every result exact, so a misplaced 16-byte chunk, k row or
+    tile shows up bit-exactly; alpha/beta are then checked against float64 with the HGEMM bound."""
+    import ctypes
+    torch = torch_dev
+    rng = np.random.default_rng(21)
+    for ta in (0, 1):
+        for tb in (0, 1):
+            a = rng.integers(-2, 3, (count, M, K)).astype(np.float16)
+            b = rng.integers(-2, 3, (count, K, N)).astype(np.float16)
+            c0 = rng.uniform(-1, 1, (count, M, N)).astype(np.float16)
+            A = np.ascontiguousarray(a.transpose(0, 2, 1)) if ta else a      # stored K×M when transposed
+            B = np.ascontiguousarray(b.transpose(0, 2, 1)) if tb else b      # stored N×K when transposed
+            Ad, Bd = _to_dev(torch, A), _to_dev(torch, B)
+            ref = np.einsum("bmk,bkn->bmn", a.astype(np.int64), b.astype(np.int64))
+            assert np.abs(ref).max() <= 2048
+            for al, be in ((1.0, 0.0), (0.5, -1.5)):
+                Cd = _to_dev(torch, c0 if be else np.zeros_like(c0))
+                lda, ldb = (M if ta else K), (K if tb else N)
+                rc = g9._lib.gen9blas_gemm_batched(g9.GEN9BLAS_H, ta, tb, M, N, K, al, ctypes.c_void_p(Ad.data_ptr()),
+                                                   lda, M * K, ctypes.c_void_p(Bd.data_ptr()), ldb, K * N, be,
+                                                   ctypes.c_void_p(Cd.data_ptr()), N, M * N, count)
+                assert rc == 0, g9._lib.gen9blas_error()
+                torch.cuda.synchronize()
+                W = Cd.cpu().numpy()
+                tag = f"{M}x{N}x{K}x{count} tA={ta} tB={tb} alpha={al} beta={be}"
+                if be == 0.0:
+                    assert np.array_equal(W.astype(np.int64), ref), tag
+                else:
+                    r64 = al * ref + be * c0.astype(np.float64)
+                    scale = abs(al) * (np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64))) + abs(be) * np.abs(c0.astype(np.float64))
+                    e = np.abs(W.astype(np.float64) - r64) / scale
+                    assert e.max() <= 2e-3, f"{tag}: max e {e.max():.2e}"
+
+
 def test_banded_launch(tmp_path):
     """GEN9BLAS_MAX_LAUNCH_MS splits a long product into row bands, each its own launch (reference:
     lib/src/gemm.c:119-164): results equal the unbanded call's. The variable is read once per process, so the banded
