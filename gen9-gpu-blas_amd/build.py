@@ -27,7 +27,7 @@ HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC", "-fvisibilit
              "-Wall", "-Wno-unused-function"]
 HIP_SOURCES = ["runtime.hip", "gemm.hip", "gemm_kernels.hip", "skinny.hip", "level12.hip", "level12_kernels.hip",
                "unsupported.hip"]
-HEADERS = ["internal.h", "skinny_kernel.h", "gemm_kernel.h", "hgemm_kernel.h", "wave.h"]
+HEADERS = ["internal.h", "skinny_kernel.h", "gemm_kernel.h", "hgemm_kernel.h", "lds_dma.h", "wave.h"]
 
 
 def _run(cmd):

@@ -30,6 +30,7 @@
 //   one XCD's L2 serves the A and B panels its tiles share.
 #pragma once
 #include "internal.h"
+#include "lds_dma.h"
 
 namespace g9 {
 namespace hg {
@@ -40,7 +41,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
-#define G9_LDS __attribute__((address_space(3)))
 
 struct Params {
     const f16 *A, *B;
@@ -49,30 +49,6 @@ struct Params {
     int M, N, K, tiles_m, tiles_n;
     float alpha, beta;
 };
-
-// One global→LDS copy of 16 bytes per lane: lane L writes LDS bytes lds + 16·L .. +15 with the 16 bytes at
-// base + voff (global_load_lds_dwordx4, M0 = LDS address). Issued by inline assembly: the compiler does not track
-// these writes, so it adds no wait for them before unrelated LDS reads. The kernel waits for them itself
-// (s_waitcnt vmcnt and a barrier before the data is read). Nothing else in the kernels that use it touches M0.
-__device__ __forceinline__ void lds_dma16(const void *base, unsigned voff, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "s"(lds) : "memory");
-}
-
-// s_waitcnt fields (gfx9): vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8; a field at its maximum does not wait.
-template <int N> __device__ __forceinline__ void wait_vm() {   // at most N vector-memory loads of this wave in flight
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4)); }
-// At most s stages of LPS loads each still in flight, s in [0, MAXS].
-template <int MAXS, int LPS> __device__ __forceinline__ void wait_vm_stages(int s) {
-    if constexpr (MAXS > 0) {
-        if (s >= MAXS) { wait_vm<MAXS * LPS>(); return; }
-        wait_vm_stages<MAXS - 1, LPS>(s);
-    } else {
-        wait_vm<0>();
-    }
-}
 
 // Global → LDS loads of one operand tile: RT rows (m or n) × KB k, RT·KB·2 bytes, issued by NW waves.
 // KC: stored k-contiguous (element (mn, k) at X[mn·ld + k]); otherwise mn-contiguous (element (mn, k) at X[k·ld + mn]).

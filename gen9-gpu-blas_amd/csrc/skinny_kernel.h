@@ -13,6 +13,7 @@
 //   exchange per value instead of six; then the KS waves combine through LDS.
 #pragma once
 #include "internal.h"
+#include "lds_dma.h"
 #include "wave.h"
 
 namespace g9 {
@@ -145,6 +146,112 @@ __global__ void __launch_bounds__(KS * 64) skinny_kernel(Params p) {
 #pragma unroll
             for (int q = 0; q < KS; q++) s += part[q][t];
             emit(t, s);
+        }
+    }
+}
+
+// FP16 skinny kernel on the matrix cores, for 4 < M ≤ 16 (and M tiles beyond). The dot-product kernel above is
+// issue-bound there: it needs 4·M v_dot2 instructions per 16 bytes of w. Here one v_mfma_f32_16x16x32_f16 multiplies
+// 16 rows of w by 16 rows of a (rows of a beyond M are zero) over 32 k, so the instruction count no longer grows
+// with M and the kernel stays bound by the weight stream:
+// - a workgroup owns 16 rows of w (n0 .. n0+15) and one tile of MT rows of a; its KS waves split K in groups of
+//   GK = 256 k, round robin (wave wv takes groups wv, wv + KS, ...);
+// - each wave streams its groups through a private NS-stage LDS ring with global_load_lds_dwordx4: per group, 8
+//   copies of 1 KiB bring 16 rows × 512 bytes of w (one copy = 2 rows, contiguous in memory), and ⌈MT/2⌉ copies
+//   bring the MT rows of a. No barrier is needed until the end: a wave only reads what it loaded itself;
+// - chunk c (16 bytes, k = 8c .. 8c+7) of row r of a group sits at position c ^ r of the row, so the 16 lanes that
+//   read one chunk of 16 different rows hit distinct banks;
+// - the 16×16 FP32 partial tiles of the KS waves are summed through LDS, then alpha (and beta·C, C not read when
+//   beta = 0) is applied and rounded once to FP16, as in the dot-product kernel.
+// Requires K % 256 == 0 and 16-byte aligned rows of a and w (the launcher checks; other shapes take the kernel above).
+template <int MT, int KS, int NS>
+__global__ void __launch_bounds__(KS * 64) skinny_mfma_kernel(Params p) {
+    typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    constexpr int GK = 256, ROWB = GK * 2;                 // 512 bytes of a row per group
+    constexpr int NA = (MT + 1) / 2;                       // copies of a per group (2 rows each)
+    constexpr int WB = 16 * ROWB, AB = NA * 1024, SB = WB + AB;
+    constexpr int LPG = 8 + NA;                            // copies per group
+    static_assert((NS - 1) * LPG < 64, "copies in flight must fit vmcnt");
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[KS * NS * SB];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, r16 = lane & 15;
+    const int n0 = blockIdx.x * 16, m0 = blockIdx.y * MT;
+    const unsigned lbase = (unsigned)(uintptr_t)smem + wv * NS * SB;
+    const G9_LDS unsigned char *lds = (const G9_LDS unsigned char *)smem + wv * NS * SB;
+    const int G = p.K / GK;
+    const int ng = G > wv ? (G - wv + KS - 1) / KS : 0;
+
+    // copy i of w covers rows 2i, 2i+1 of the group; lane L: row 2i + L/32, position L % 32 = chunk (L % 32) ^ row.
+    // Rows past N (and of a past M) load the last valid row; their results are never stored (a: zeroed below).
+    const int rsub = lane >> 5, pos = lane & 31;
+    unsigned woff[8], aoff[NA];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int r = 2 * i + rsub, rr = min(n0 + r, p.N - 1) - n0;
+        woff[i] = (unsigned)((long long)rr * p.swn * 2 + ((pos ^ r) << 4));
+    }
+#pragma unroll
+    for (int i = 0; i < NA; i++) {
+        const int r = 2 * i + rsub, rr = min(m0 + r, p.M - 1) - m0;
+        aoff[i] = (unsigned)((long long)rr * p.sam * 2 + ((pos ^ r) << 4));
+    }
+    const char *wb = reinterpret_cast<const char *>(reinterpret_cast<const f16 *>(p.w) + (long long)n0 * p.swn);
+    const char *ab = reinterpret_cast<const char *>(reinterpret_cast<const f16 *>(p.a) + (long long)m0 * p.sam);
+    auto issue = [&](int j, int st) {   // group wv + KS·j into stage st
+        const long long kofs = (long long)(wv + KS * j) * ROWB;
+        const unsigned dst = lbase + st * SB;
+#pragma unroll
+        for (int i = 0; i < 8; i++) lds_dma16(wb + kofs, woff[i], dst + i * 1024);
+#pragma unroll
+        for (int i = 0; i < NA; i++) lds_dma16(ab + kofs, aoff[i], dst + WB + i * 1024);
+    };
+
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const bool mval = r16 < MT && m0 + r16 < p.M;
+    const int arow = r16 < MT ? r16 : 0;
+#pragma unroll
+    for (int s = 0; s < NS; s++)
+        if (s < ng) issue(s, s);
+    int st = 0;
+    for (int j = 0; j < ng; j++) {
+        wait_vm_stages<NS - 1, LPG>(min(NS - 1, ng - 1 - j));   // group j has landed
+        const G9_LDS unsigned char *sg = lds + st * SB;
+        u32x4 wf[8], af[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            wf[t] = *reinterpret_cast<const G9_LDS u32x4 *>(sg + r16 * ROWB + (((4 * t + g) ^ r16) << 4));
+            af[t] = *reinterpret_cast<const G9_LDS u32x4 *>(sg + WB + arow * ROWB + (((4 * t + g) ^ arow) << 4));
+        }
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const u32x4 av = mval ? af[t] : u32x4{0, 0, 0, 0};
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, wf[t]), __builtin_bit_cast(f16x8, av),
+                                                         acc, 0, 0, 0);
+        }
+        wait_lgkm0();   // the stage is refilled next: its reads must be done
+        if (j + NS < ng) issue(j + NS, st);
+        st = st + 1 == NS ? 0 : st + 1;
+    }
+
+    // lane holds D[n = 4g + i][m = r16]; sum the KS waves' tiles
+    __syncthreads();
+    float *part = reinterpret_cast<float *>(smem);   // [KS][16 n][16 m]
+#pragma unroll
+    for (int i = 0; i < 4; i++) part[(wv * 16 + 4 * g + i) * 16 + r16] = acc[i];
+    __syncthreads();
+    f16 *C = reinterpret_cast<f16 *>(p.C);
+    for (int idx = threadIdx.x; idx < 16 * MT; idx += KS * 64) {
+        const int n = idx / MT, m = idx % MT;
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < KS; q++) sum += part[(q * 16 + n) * 16 + m];
+        const int gm = m0 + m, gn = n0 + n;
+        if (gm < p.M && gn < p.N) {
+            f16 *c = C + (long long)gm * p.scm + (long long)gn * p.scn;
+            const float r = p.beta == 0.f ? p.alpha * sum : __builtin_fmaf(p.alpha, sum, p.beta * (float)*c);
+            *c = (f16)r;
         }
     }
 }

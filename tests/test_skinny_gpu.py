@@ -90,3 +90,33 @@ def test_skinny_oracle_parity_small(g9, orc):
         d = np.abs(G.astype(np.float64) - R.astype(np.float64))
         ulp = np.abs(R.astype(np.float64)) * 2.0 ** -10 + 2.0 ** -24
         assert (d <= 2 * ulp).all(), f"M={M}: GPU and oracle differ by more than 2 FP16 ulp"
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 100, 256), (8, 4099, 512), (12, 333, 768), (16, 64, 4096), (16, 3000, 2560)])
+def test_skinny_matrix_core_kernel(g9, torch_dev, M, N, K):
+    """FP16 shapes that take the matrix-core skinny kernel (4 < M ≤ 16, K a multiple of 256, aligned rows): fewer
+    K groups than waves, N not a multiple of 16, both M tiles, host and device memory. Small-integer inputs give exact
+    products and sums, so every result must be bit-exact; then alpha/beta on a C slice, and the role swap (small N)
+    that stores through swapped strides."""
+    rng = np.random.default_rng(31)
+    a = rng.integers(-3, 4, (M, K)).astype(np.float16)
+    w = rng.integers(-3, 4, (N, K)).astype(np.float16)
+    ref = a.astype(np.int64) @ w.astype(np.int64).T
+    assert np.abs(ref).max() <= 2048
+    assert np.array_equal(g9.hgemm(a, w.T).astype(np.int64), ref), "host"
+    Wd = g9.hgemm(_dev(torch_dev, a), _dev(torch_dev, w).t())
+    assert np.array_equal(Wd.cpu().numpy().astype(np.int64), ref), "device"
+    # role swap: C (N×M) = w·aᵀ takes the skinny path with a as the streamed operand and C written column-wise
+    assert np.array_equal(g9.hgemm(w, a.T).astype(np.int64), ref.T), "small N"
+    # alpha/beta into a slice of a larger array; nothing outside it changes
+    big = rng.uniform(-1, 1, (M + 3, N + 4)).astype(np.float16)
+    D0 = big.copy()
+    C = big[2:M + 2, 1:N + 1]
+    C0 = C.astype(np.float64)
+    g9.hgemm(a, w.T, alpha=0.5, beta=-2.0, C=C)
+    r64 = 0.5 * ref - 2.0 * C0
+    scale = 0.5 * (np.abs(a.astype(np.float64)) @ np.abs(w.astype(np.float64)).T) + 2.0 * np.abs(C0)
+    assert float(np.max(np.abs(C.astype(np.float64) - r64) / scale)) <= 2e-3
+    mask = np.ones(big.shape, bool)
+    mask[2:M + 2, 1:N + 1] = False
+    assert np.array_equal(big[mask], D0[mask]), "write outside the C slice"
