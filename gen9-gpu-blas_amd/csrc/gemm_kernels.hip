@@ -51,9 +51,9 @@ static int launch_layout(const GemmParams<typename Mma<T>::Sum> &p, int count) {
 }
 
 // ---------------- FP16 whole-tile kernel ----------------
-// Configurations from a sweep on MI355X with N(0,1) FP16 inputs (n = 4096: 256×256 with 8 waves, KB = 64, two
-// stages: NN 1052 TFLOP/s; n = 2048: 128×128, 4 waves, KB = 64, four stages: 662; n = 1024: 128×128, two stages).
-// Products with fewer big tiles than CUs take the 128×128 tile.
+// Configurations from sweeps on MI355X with N(0,1) FP16 inputs: n = 4096, 256×256 tiles, 8 waves (4×2), KB = 64,
+// two stages: 1130-1180 TFLOP/s (NN; hipBLASLt on the same inputs: 1180-1210); n = 2048 and 1024, 128×128 tiles,
+// 4 waves, KB = 32, four stages: 721 and 191. Products with fewer 256×256 tiles than CUs take the 128×128 tile.
 template <int BM, int BN, int WM, int WN, int KB, int NS, bool AK, bool BKC>
 static int launch_hg(const hg::Params &p0, int count) {
     hg::Params p = p0;
@@ -67,12 +67,11 @@ static int launch_hg(const hg::Params &p0, int count) {
 template <bool AK, bool BKC>
 static int launch_hg_layout(const hg::Params &p, int count) {
     if ((long long)(p.M / 256) * (p.N / 256) * count >= num_cus && p.M % 256 == 0 && p.N % 256 == 0)
-        return launch_hg<256, 256, 2, 4, 64, 2, AK, BKC>(p, count);
-    if (p.K / 64 >= 32) return launch_hg<128, 128, 2, 2, 64, 4, AK, BKC>(p, count);
-    return launch_hg<128, 128, 2, 2, 64, 2, AK, BKC>(p, count);
+        return launch_hg<256, 256, 4, 2, 64, 2, AK, BKC>(p, count);
+    return launch_hg<128, 128, 2, 2, 32, 4, AK, BKC>(p, count);
 }
 // The whole-tile FP16 kernel applies when every operand is 16-byte aligned with 16-byte row strides, M and N are
-// multiples of 128, K of 64, and the grid fits. GEN9BLAS_HGEMM=generic forces the general kernel.
+// multiples of 128, K of 64 (both tile configurations' k-steps divide it), and the grid fits. GEN9BLAS_HGEMM=generic forces the general kernel.
 static bool hgemm_tiles_apply(const GemmCall &c) {
     static int generic = -1;
     if (generic < 0) {

@@ -24,8 +24,8 @@
 //   long, and read with ds_read_b64_tr_b16, which transposes 16-lane groups: lane j of a group reads 4 consecutive
 //   mn of row kb + j/4, and lane i receives mn i of rows kb .. kb+3. Chunk c of row k sits at c ^ (4·(k & 3)), so
 //   the four rows of a group fall on distinct banks;
-// - operands are swapped in the MFMA (the B fragment is the first input), so each lane ends with 4 consecutive n
-//   of one row of C: 8-byte stores;
+// - operands are swapped in the MFMA (the B fragment is the first input), so each lane ends with runs of 4
+//   consecutive n of one row of C; v_permlane32_swap joins two runs, giving 16-byte stores;
 // - the workgroup → tile mapping gives each XCD a contiguous range of tiles, ordered in groups of 4 tile rows, so
 //   one XCD's L2 serves the A and B panels its tiles share.
 #pragma once
@@ -91,9 +91,14 @@ struct Loader {
     // Issues this wave's loads of the next k-step into the tile at LDS address `dst`, then advances.
     __device__ __forceinline__ void issue(unsigned dst, int wave) {
 #pragma unroll
-        for (int i = 0; i < NI; i++) lds_dma16(org + i * step_i, voff, dst + 1024 * (wave + NW * i));
+        for (int i = 0; i < NI; i++) one(i, dst, wave);
         org += step_k;
     }
+    // Instruction i of this wave's loads of the current k-step; advance() moves to the next k-step.
+    __device__ __forceinline__ void one(int i, unsigned dst, int wave) const {
+        lds_dma16(org + i * step_i, voff, dst + 1024 * (wave + NW * i));
+    }
+    __device__ __forceinline__ void advance(bool more) { if (more) org += step_k; }
 };
 
 // Fragment reads of one operand for a wave's TT MFMA tiles (32 rows of m or n each, starting at wave row w0).
@@ -190,71 +195,115 @@ __global__ void __launch_bounds__(WM *WN * 64) hgemm_kernel(Params p) {
 #pragma unroll
         for (int i = 0; i < TN; i++) rb[buf][i] = fb.read(stg + ABYTES, i, s);
     };
-    auto mfmas = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < TN; i++)
-#pragma unroll
-            for (int j = 0; j < TM; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, rb[buf][i]),
-                                                                   __builtin_bit_cast(f16x8, ra[buf][j]), acc[i][j], 0, 0, 0);
-    };
-    auto issue = [&](int stg) {
-        la.issue(lds_addr + stg * SBYTES, wave);
-        lb.issue(lds_addr + stg * SBYTES + ABYTES, wave);
-    };
-
     const int nk = p.K / KB;
-    // prologue: k-steps 0 .. NS-1 into stages 0 .. NS-1, then wait for k-step 0
+    // prologue: k-steps 0 .. NS-1 into stages 0 .. NS-1 (past the last k-step, the last one is loaded again into a
+    // stage nobody reads, so every k-step issues the same number of loads), then wait for k-step 0
 #pragma unroll
-    for (int s = 0; s < NS; s++)
-        if (s < nk) issue(s);
-    wait_vm_stages<NS - 1, LPS>(min(NS - 1, nk - 1));
+    for (int s = 0; s < NS; s++) {
+        la.issue(lds_addr + s * SBYTES, wave);
+        lb.issue(lds_addr + s * SBYTES + ABYTES, wave);
+        if (s + 1 >= nk) { la.org -= la.step_k; lb.org -= lb.step_k; }
+    }
+    wait_vm<(NS - 1) * LPS>();
     __syncthreads();
     read_frags(lds, 0, 0);
 
+    // One k-step: NSUB substeps of TM·TN MFMAs. The instruction order is pinned (sched_barrier between slots):
+    // slot t of a substep holds MFMA t followed by its share of the next substep's fragment reads (in the order the
+    // MFMAs use them); before the last
+    // substep, the wait for k-step kt+1 and the barrier; in the last substep, the reads of k-step kt+1's first
+    // substep and the loads of k-step kt+NS into the stage just released, spread over the MFMA slots.
+    constexpr int NMF = TM * TN;
+    constexpr int NRF = TM + TN;                 // fragments per substep
+    constexpr int NLD = LPS;                     // global→LDS copies per k-step
     int st = 0;   // stage holding k-step kt
     for (int kt = 0; kt < nk; kt++) {
         const G9_LDS unsigned char *cur = lds + st * SBYTES;
         const int nst = st + 1 == NS ? 0 : st + 1;
 #pragma unroll
-        for (int s = 0; s < NSUB; s++) {
-            if (s + 1 < NSUB) {
-                read_frags(cur, s + 1, (s + 1) & 1);
-            } else if (kt + 1 < nk) {
-                // Before the last substep: k-step kt+1 must be in LDS (this wave's loads: at most min(NS-2, nk-2-kt)
-                // later stages still in flight; the other waves': the barrier), and every wave must be done reading
-                // stage st (its fragments are in registers: lgkmcnt(0), then the barrier) before the stage is
-                // reloaded with k-step kt+NS.
-                wait_vm_stages<NS - 2, LPS>(min(NS - 2, nk - 2 - kt));
-                wait_lgkm0();
-                __syncthreads();
-                if (kt + NS < nk) issue(st);
-                read_frags(lds + nst * SBYTES, 0, 0);
+        for (int s = 0; s < NSUB - 1; s++) {
+            const int nb = (s + 1) & 1;
+#pragma unroll
+            for (int t = 0; t < NMF; t++) {
+                const int i = t / TM, j = t % TM;
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, rb[s & 1][i]),
+                                                                   __builtin_bit_cast(f16x8, ra[s & 1][j]), acc[i][j], 0, 0, 0);
+                constexpr int PER = (NRF + NMF - 1) / NMF;
+#pragma unroll
+                for (int q = t * PER; q < (t + 1) * PER && q < NRF; q++) {   // in order of first use
+                    if (q == 0) rb[nb][0] = fb.read(cur + ABYTES, 0, s + 1);
+                    else if (q <= TM) ra[nb][q - 1] = fa.read(cur, q - 1, s + 1);
+                    else rb[nb][q - TM] = fb.read(cur + ABYTES, q - TM, s + 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-            mfmas(s & 1);
+        }
+        // k-step kt+1 in LDS: this wave's loads (NS-2 later k-steps may stay in flight) and, after the barrier, every
+        // other wave's; all waves are done reading stage st (lgkmcnt(0) before the barrier) before it is reloaded.
+        wait_vm<(NS - 2) * LPS>();
+        wait_lgkm0();
+        __syncthreads();
+        {
+            constexpr int s = NSUB - 1;
+            const G9_LDS unsigned char *nxt = lds + nst * SBYTES;
+            const unsigned dsta = lds_addr + st * SBYTES, dstb = dsta + ABYTES;
+            constexpr int NIT = NRF + NLD, PER = (NIT + NMF - 1) / NMF;
+#pragma unroll
+            for (int t = 0; t < NMF; t++) {
+                const int i = t / TM, j = t % TM;
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, rb[s & 1][i]),
+                                                                   __builtin_bit_cast(f16x8, ra[s & 1][j]), acc[i][j], 0, 0, 0);
+#pragma unroll
+                for (int q = t * PER; q < (t + 1) * PER && q < NIT; q++) {
+                    if (q == 0) rb[0][0] = fb.read(nxt + ABYTES, 0, 0);
+                    else if (q <= TM) ra[0][q - 1] = fa.read(nxt, q - 1, 0);
+                    else if (q < NRF) rb[0][q - TM] = fb.read(nxt + ABYTES, q - TM, 0);
+                    else if (q - NRF < LA::NI) la.one(q - NRF, dsta, wave);
+                    else lb.one(q - NRF - LA::NI, dstb, wave);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            const bool more = kt + NS + 1 < nk;   // the next issue loads k-step kt+NS+1, if it exists
+            la.advance(more);
+            lb.advance(more);
         }
         st = nst;
     }
+    wait_vm<0>();   // the loads into stages nobody reads have landed before the wave ends
 
-    // lane holds D[n][m]: m = lane % 32 of MFMA tile j, n in runs of 4 (rows 8q + 4·(lane/32) .. +3 of tile i)
+    // Epilogue. Lane l holds D[n][m] for m = lane % 32 of MFMA tile j and n in runs of 4: rows 8q + 4·(l / 32) .. +3
+    // of tile i, q = 0..3. Each run becomes 4 FP16 values (alpha·acc + beta·C in FP32, rounded once); then lanes l and
+    // l+32 trade runs with v_permlane32_swap, so that each lane holds 8 consecutive n (16 bytes): lane l < 32 those of
+    // q = 2p, lane l + 32 those of q = 2p + 1, for p = 0, 1. Two 16-byte stores per MFMA tile and lane.
     const float alpha = p.alpha, beta = p.beta;
+    const int hi = lane >> 5;
 #pragma unroll
     for (int i = 0; i < TN; i++)
 #pragma unroll
         for (int j = 0; j < TM; j++) {
             const int m = m0 + wm * WTM + j * 32 + (lane & 31);
+            f16 *crow = C + (long long)m * p.ldc + n0 + wn * WTN + i * 32;
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int n = n0 + wn * WTN + i * 32 + 8 * q + 4 * (lane >> 5);
-                f16 *c = C + (long long)m * p.ldc + n;
-                union { u32x2 w; f16 e[4]; } o, v;
-                if (beta != 0.f) o.w = *reinterpret_cast<const u32x2 *>(c);
+            for (int pr = 0; pr < 2; pr++) {
+                unsigned w[2][2];   // [q - 2·pr][dword]: the lane's own run of q, 4 FP16 values
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float x = alpha * acc[i][j][4 * q + e];
-                    v.e[e] = (f16)(beta != 0.f ? __builtin_fmaf(beta, (float)o.e[e], x) : x);
+                for (int h = 0; h < 2; h++) {
+                    const int q = 2 * pr + h;
+                    union { u32x2 w; f16 e[4]; } o, v;
+                    if (beta != 0.f) o.w = *reinterpret_cast<const u32x2 *>(crow + 8 * q + 4 * hi);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float x = alpha * acc[i][j][4 * q + e];
+                        v.e[e] = (f16)(beta != 0.f ? __builtin_fmaf(beta, (float)o.e[e], x) : x);
+                    }
+                    w[h][0] = v.w[0];
+                    w[h][1] = v.w[1];
                 }
-                *reinterpret_cast<u32x2 *>(c) = v.w;
+                // swap lanes 32..63 of the q = 2pr run with lanes 0..31 of the q = 2pr+1 run
+                const auto s0 = __builtin_amdgcn_permlane32_swap(w[0][0], w[1][0], false, false);
+                const auto s1 = __builtin_amdgcn_permlane32_swap(w[0][1], w[1][1], false, false);
+                const u32x4 out = {s0[0], s1[0], s0[1], s1[1]};
+                *reinterpret_cast<u32x4 *>(crow + 8 * (2 * pr + hi)) = out;
             }
         }
 }
