@@ -82,6 +82,10 @@ template <class S> struct GemmParams {
     long long lda, ldb, ldc, sA, sB, sC;
     int M, N, K, tiles_m, tiles_n, vec_c;
     S alpha, beta;
+    // split K (count = 1 only): slice z = blockIdx.y covers k = z·kper .. +kper and writes its unscaled partial sums
+    // to P + z·M·N (row stride N, accumulator type S); a reduction kernel then forms alpha·Σ + beta·C
+    S *P;
+    int kper, vec_p;
 };
 
 // 16 bytes (V elements) of row r, columns c .. c+V-1 of a row-major matrix X (R valid rows, Cc valid columns, row
@@ -190,7 +194,7 @@ template <class T, class S> __device__ __forceinline__ void store4(T *c, const S
 // Instruction-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100, SG_DS_WRITE = 0x200;
 
-template <class T, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool VEC, bool SCHED = true>
+template <class T, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool VEC, bool SCHED = true, bool SPLIT = false>
 __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename Mma<T>::Sum> p) {
     using MM = Mma<T>;
     using S = typename MM::Sum;
@@ -219,9 +223,20 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
     const int m0 = (first_m + in_group % gsz) * BM, n0 = (in_group / gsz) * BN;
 
     const long long z = blockIdx.y;
-    const T *A = reinterpret_cast<const T *>(p.A) + z * p.sA;
-    const T *B = reinterpret_cast<const T *>(p.B) + z * p.sB;
-    T *C = reinterpret_cast<T *>(p.C) + z * p.sC;
+    const T *A = reinterpret_cast<const T *>(p.A);
+    const T *B = reinterpret_cast<const T *>(p.B);
+    T *C = reinterpret_cast<T *>(p.C);
+    int K = p.K;
+    if constexpr (SPLIT) {
+        const int k0 = (int)z * p.kper;
+        K = min(p.K - k0, p.kper);
+        A += AK ? k0 : (long long)k0 * p.lda;
+        B += BKC ? k0 : (long long)k0 * p.ldb;
+    } else {
+        A += z * p.sA;
+        B += z * p.sB;
+        C += z * p.sC;
+    }
 
     Stage<T, BM, NT, AK, VEC> sa;
     Stage<T, BN, NT, BKC, VEC> sb;
@@ -278,21 +293,21 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
         }
     };
 
-    const int nk = (p.K + BK - 1) / BK;
+    const int nk = (K + BK - 1) / BK;
     // Interior tiles with whole k-steps load without bounds tests: the steady-state loop is then one basic block,
     // whose instruction order is pinned below so the LDS reads, global loads and LDS writes of a k-step run between
     // its MFMAs.
-    const bool fast = VEC && m0 + BM <= p.M && n0 + BN <= p.N && p.K % BK == 0;
+    const bool fast = VEC && m0 + BM <= p.M && n0 + BN <= p.N && K % BK == 0;
     if (fast) {
-        sa.template load<false>(A, p.lda, p.M, p.K, m0, 0, tid);
-        sb.template load<false>(B, p.ldb, p.N, p.K, n0, 0, tid);
+        sa.template load<false>(A, p.lda, p.M, K, m0, 0, tid);
+        sb.template load<false>(B, p.ldb, p.N, K, n0, 0, tid);
         sa.store(lds[0], tid);
         sb.store(lds[0] + BM * ROWB, tid);
         __syncthreads();
         for (int kt = 0; kt + 1 < nk; kt++) {
             const int cur = kt & 1;
-            sa.template load<false>(A, p.lda, p.M, p.K, m0, (kt + 1) * BK, tid);
-            sb.template load<false>(B, p.ldb, p.N, p.K, n0, (kt + 1) * BK, tid);
+            sa.template load<false>(A, p.lda, p.M, K, m0, (kt + 1) * BK, tid);
+            sb.template load<false>(B, p.ldb, p.N, K, n0, (kt + 1) * BK, tid);
             compute(cur);
             sa.store(lds[cur ^ 1], tid);
             sb.store(lds[cur ^ 1] + BM * ROWB, tid);
@@ -323,8 +338,8 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
         compute((nk - 1) & 1);
     } else {
         auto load_tile = [&](int k0) {
-            sa.template load<true>(A, p.lda, p.M, p.K, m0, k0, tid);
-            sb.template load<true>(B, p.ldb, p.N, p.K, n0, k0, tid);
+            sa.template load<true>(A, p.lda, p.M, K, m0, k0, tid);
+            sb.template load<true>(B, p.ldb, p.N, K, n0, k0, tid);
         };
         load_tile(0);
         sa.store(lds[0], tid);
@@ -355,7 +370,10 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
                     const int n = n0 + wn * WTN + i * MI + MM::row(4 * q, lane);
                     if (n >= p.N) continue;
                     const S v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-                    store4<T, S>(C + (long long)m * p.ldc + n, v, p.alpha, p.beta, p.vec_c, p.N - n);
+                    if constexpr (SPLIT)
+                        store4<S, S>(p.P + z * p.M * (long long)p.N + (long long)m * p.N + n, v, S(1), S(0), p.vec_p, p.N - n);
+                    else
+                        store4<T, S>(C + (long long)m * p.ldc + n, v, p.alpha, p.beta, p.vec_c, p.N - n);
                 }
             }
     } else {
@@ -370,6 +388,10 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
                 for (int r = 0; r < MM::NACC; r++) {
                     const int m = m0 + wm * WTM + i * MI + MM::row(r, lane);
                     if (m >= p.M) continue;
+                    if constexpr (SPLIT) {
+                        p.P[z * p.M * (long long)p.N + (long long)m * p.N + n] = acc[i][j][r];
+                        continue;
+                    }
                     T *c = C + (long long)m * p.ldc + n;
                     S v = p.alpha * acc[i][j][r];
                     if (p.beta != S(0)) v = fma_s(p.beta, (S)*c, v);
@@ -412,6 +434,36 @@ __device__ __forceinline__ void store4(T *c, const S *v, S alpha, S beta, bool v
             if (beta != S(0)) r = fma_s(beta, (S)c[e], r);
             c[e] = (T)r;
         }
+}
+
+// Split-K finish: C = alpha·(P[0] + ... + P[splits-1]) + beta·C (C not read when beta = 0), summed in slice order
+// and rounded once to T. One thread per 4 consecutive elements of a row (N % 4 == 0 and aligned C), else per element.
+template <class T, class S, bool VEC4>
+__global__ void __launch_bounds__(256) splitk_reduce(const S *__restrict__ P, T *C, long long ldc, int M, int N, int splits,
+                                                     S alpha, S beta) {
+    const long long mn = (long long)M * N;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    if constexpr (VEC4) {
+        for (long long g = blockIdx.x * (long long)blockDim.x + threadIdx.x; g < mn / 4; g += stride) {
+            const long long e = 4 * g;
+            const int m = (int)(e / N), n = (int)(e % N);
+            S v[4] = {0, 0, 0, 0};
+            for (int sp = 0; sp < splits; sp++)
+#pragma unroll
+                for (int t = 0; t < 4; t++) v[t] += P[sp * mn + e + t];
+            store4<T, S>(C + (long long)m * ldc + n, v, alpha, beta, true, 4);
+        }
+    } else {
+        for (long long e = blockIdx.x * (long long)blockDim.x + threadIdx.x; e < mn; e += stride) {
+            const int m = (int)(e / N), n = (int)(e % N);
+            S v = 0;
+            for (int sp = 0; sp < splits; sp++) v += P[sp * mn + e];
+            S r = alpha * v;
+            T *c = C + (long long)m * ldc + n;
+            if (beta != S(0)) r = fma_s(beta, (S)*c, r);
+            *c = (T)r;
+        }
+    }
 }
 
 }  // namespace g9

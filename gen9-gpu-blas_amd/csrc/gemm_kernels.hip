@@ -5,6 +5,7 @@
 #include "hgemm_kernel.h"
 #include <stdlib.h>
 #include <string.h>
+#include <algorithm>
 
 namespace g9 {
 
@@ -30,13 +31,55 @@ template <bool AK, bool BKC, bool VEC> struct Cfg<double, AK, BKC, VEC> {
     static constexpr TileCfg big{256, 128, 4, 2}, small{64, 128, 2, 2};
 };
 
+// Split-K slices for a single product of `tiles` tiles: doubled while the slices still leave at most one workgroup
+// per CU and each slice keeps at least 4 k-steps, up to 8. GEN9BLAS_SPLITK=n forces n slices (0 or 1: none).
+// Splitting changes only the FP32 (FP64) summation order: each slice sums its k-range, the slices are then added in
+// order, and alpha/beta and the rounding to the element type are applied once.
+static int splitk_slices(long long tiles, int K, int BK, int count) {
+    static int forced = -2;
+    if (forced == -2) {
+        const char *e = getenv("GEN9BLAS_SPLITK");
+        forced = e ? atoi(e) : -1;
+    }
+    if (count != 1) return 1;
+    if (forced >= 0) return forced < 1 ? 1 : forced > 64 ? 64 : forced;
+    int s = 1;
+    while (s < 8 && tiles * s * 2 <= num_cus && K / (s * 2) >= 4 * BK) s *= 2;
+    return s;
+}
+
 template <class T, TileCfg C, bool AK, bool BKC, bool VEC>
 static int launch_t(GemmParams<typename Mma<T>::Sum> p, int count) {
+    using S = typename Mma<T>::Sum;
+    constexpr int BK = 128 / (int)sizeof(T);
     p.tiles_m = (p.M + C.BM - 1) / C.BM;
     p.tiles_n = (p.N + C.BN - 1) / C.BN;
     if ((long long)p.tiles_m * p.tiles_n > 0x7fffffffLL || count > 65535)
         G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "gemm grid too large (%d × %d tiles, batch %d)", p.tiles_m, p.tiles_n, count);
-    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)count), block(C.WM * C.WN * 64);
+    const long long tiles = (long long)p.tiles_m * p.tiles_n;
+    const int split = splitk_slices(tiles, p.K, BK, count);
+    const dim3 block(C.WM * C.WN * 64);
+    if (split > 1) {
+        p.kper = ((p.K + split - 1) / split + BK - 1) / BK * BK;
+        const int ns = (p.K + p.kper - 1) / p.kper;
+        void *P;
+        G9_TRY(scratch(SLOT_P, (size_t)ns * p.M * p.N * sizeof(S), &P));
+        p.P = reinterpret_cast<S *>(P);
+        p.vec_p = p.N % 4 == 0;
+        hipLaunchKernelGGL((gemm_kernel<T, C.BM, C.BN, C.WM, C.WN, AK, BKC, VEC, true, true>), dim3((unsigned)tiles, (unsigned)ns),
+                           block, 0, stream, p);
+        G9_HIP(hipGetLastError());
+        const long long mn = (long long)p.M * p.N;
+        const bool v4 = p.vec_c && p.N % 4 == 0;
+        const long long work = v4 ? mn / 4 : mn;
+        const unsigned blocks = (unsigned)std::min<long long>((work + 255) / 256, (long long)num_cus * 8);
+        T *Cp = reinterpret_cast<T *>(p.C);
+        if (v4) hipLaunchKernelGGL((splitk_reduce<T, S, true>), dim3(blocks), dim3(256), 0, stream, p.P, Cp, p.ldc, p.M, p.N, ns, p.alpha, p.beta);
+        else hipLaunchKernelGGL((splitk_reduce<T, S, false>), dim3(blocks), dim3(256), 0, stream, p.P, Cp, p.ldc, p.M, p.N, ns, p.alpha, p.beta);
+        G9_HIP(hipGetLastError());
+        return 0;
+    }
+    const dim3 grid((unsigned)tiles, (unsigned)count);
     hipLaunchKernelGGL((gemm_kernel<T, C.BM, C.BN, C.WM, C.WN, AK, BKC, VEC, true>), grid, block, 0, stream, p);
     G9_HIP(hipGetLastError());
     return 0;
@@ -113,6 +156,8 @@ static int launch_typed(const GemmCall &c) {
     p.alpha = (S)c.alpha;
     p.beta = (S)c.beta;
     p.tiles_m = p.tiles_n = 0;
+    p.P = nullptr;
+    p.kper = p.vec_p = 0;
     const long long es = sizeof(T);
     const long long cal = es * 4 < 16 ? es * 4 : 16;   // alignment of a 4-element group of C
     p.vec_c = ((uintptr_t)c.C % cal == 0) && (c.ldc * es) % cal == 0 && (c.count == 1 || (c.sC * es) % cal == 0);

@@ -237,8 +237,9 @@ def test_hgemm_whole_tile_kernel(g9, torch_dev, M, N, K, count):
 
 def test_banded_launch(tmp_path):
     """GEN9BLAS_MAX_LAUNCH_MS splits a long product into row bands, each its own launch (reference:
-    lib/src/gemm.c:119-164): results equal the unbanded call's. The variable is read once per process, so the banded
-    call runs in a child process (one extra GPU process, sequential)."""
+    lib/src/gemm.c:119-164): results equal the unbanded call's (with split-K off: it picks its slices from the shape,
+    so a band may sum in another order). The variable is read once per process, so the banded call runs in a child
+    process (one extra GPU process, sequential)."""
     import os
     import subprocess
     import sys
@@ -257,6 +258,7 @@ def test_banded_launch(tmp_path):
     for band in ("", "0.0001"):
         env = dict(os.environ)
         env.pop("GEN9BLAS_MAX_LAUNCH_MS", None)
+        env["GEN9BLAS_SPLITK"] = "0"   # a band's split-K choice differs from the whole product's (other rounding)
         if band:
             env["GEN9BLAS_MAX_LAUNCH_MS"] = band
         prefix = str(tmp_path / ("banded" if band else "plain"))
@@ -267,3 +269,41 @@ def test_banded_launch(tmp_path):
         plain = np.load(outs[""] + "_" + dt + ".npy")
         banded = np.load(outs["0.0001"] + "_" + dt + ".npy")
         assert np.array_equal(plain, banded), dt   # bands compute the same per-element sums in the same order
+
+
+def test_gemm_split_k(tmp_path):
+    """Split-K (GEN9BLAS_SPLITK=n forces n slices; by default small products split to fill the CUs): every type and
+    layout, K not a multiple of the slice, alpha/beta with C read once in the reduction, exact on small integers and
+    within the reference bounds on uniform inputs. Runs in a child process because the variable is read once."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.realpath(__file__)))
+    script = tmp_path / "splitk.py"
+    script.write_text(
+        "import sys, numpy as np\n"
+        f"sys.path.insert(0, {os.path.join(root, 'gen9-gpu-blas_amd')!r}); sys.path.insert(0, {os.path.join(root, 'oracle')!r})\n"
+        "import gen9blas as g, oracle as o\n"
+        "rng = np.random.default_rng(8)\n"
+        "bound = {np.float16: 2e-3, np.float32: 1e-6, np.float64: 1e-13}\n"
+        "for dt in (np.float32, np.float64, np.float16):\n"
+        "    for (M, N, K) in [(200, 136, 1000), (64, 64, 777), (130, 260, 4096)]:\n"
+        "        for ta in (0, 1):\n"
+        "            for tb in (0, 1):\n"
+        "                a = rng.integers(-2, 3, (M, K)).astype(dt); b = rng.integers(-2, 3, (K, N)).astype(dt)\n"
+        "                A = np.ascontiguousarray(a.T).T if ta else a; B = np.ascontiguousarray(b.T).T if tb else b\n"
+        "                ref = a.astype(np.int64) @ b.astype(np.int64)\n"
+        "                if np.abs(ref).max() <= 2048 or dt != np.float16:\n"
+        "                    assert np.array_equal(g.gemm(A, B).astype(np.int64), ref), (dt, M, N, K, ta, tb)\n"
+        "                u = rng.uniform(-1, 1, (M, K)).astype(dt); v = rng.uniform(-1, 1, (K, N)).astype(dt)\n"
+        "                c0 = rng.uniform(-1, 1, (M, N)).astype(dt)\n"
+        "                U = np.ascontiguousarray(u.T).T if ta else u; V = np.ascontiguousarray(v.T).T if tb else v\n"
+        "                W = g.gemm(U, V, 0.75, -0.5, c0.copy())\n"
+        "                mean, mx = o.gemm_error(W, u, v, 0.75, -0.5, c0)\n"
+        "                assert mx <= bound[dt], (dt, M, N, K, ta, tb, mx)\n"
+        "print('ok')\n")
+    for forced in ("3", "8"):
+        env = dict(os.environ)
+        env["GEN9BLAS_SPLITK"] = forced
+        r = subprocess.run([sys.executable, str(script)], env=env, capture_output=True, text=True, timeout=200)
+        assert r.returncode == 0 and r.stdout.strip().endswith("ok"), f"GEN9BLAS_SPLITK={forced}: " + r.stderr[-2000:]
