@@ -9,6 +9,7 @@
 #include "internal.h"
 #include "wave.h"
 #include <type_traits>
+#include <stdlib.h>
 
 namespace g9 {
 namespace l12 {
@@ -280,10 +281,24 @@ __global__ void __launch_bounds__(NT) gemv_t1_kernel(int M, int N, int rpp, cons
     for (int e = 0; e < V; e++) s[e] = 0;
     const bool full = VEC && c0 + V <= N;
     if (full) {
-#pragma unroll 4
-        for (int i = i0; i < i1; i++) {
+        // U rows per step: their loads (nontemporal: A is read once) are all issued before the first product
+        constexpr int U = 8;
+        int i = i0;
+        for (; i + U <= i1; i += U) {
+            Vec<T> av[U];
+            R xv[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) av[u] = vload_nt(A + (ll)(i + u) * lda + c0);
+#pragma unroll
+            for (int u = 0; u < U; u++) xv[u] = (R)x[(ll)(i + u) * ix];
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int e = 0; e < V; e++) s[e] = fma_r((R)av[u].e[e], xv[u], s[e]);
+        }
+        for (; i < i1; i++) {
             const R xv = (R)x[(ll)i * ix];
-            const Vec<T> av = vload(A + (ll)i * lda + c0);
+            const Vec<T> av = vload_nt(A + (ll)i * lda + c0);
 #pragma unroll
             for (int e = 0; e < V; e++) s[e] = fma_r((R)av.e[e], xv, s[e]);
         }
@@ -309,13 +324,33 @@ __global__ void __launch_bounds__(NT) gemv_t1_kernel(int M, int N, int rpp, cons
 template <class T>
 __global__ void __launch_bounds__(NT) gemv_t2_kernel(int N, int parts, const typename Comp<T>::R *P,
                                                      typename Comp<T>::R alpha, typename Comp<T>::R beta, T *y, ll iy) {
+    // 64 columns per block; the block's 4 waves each sum every 4th part (loads issued 8 at a time, added in part
+    // order), then wave 0 adds the 4 sums in wave order: a fixed summation order for every column.
     using R = typename Comp<T>::R;
-    const int j = blockIdx.x * NT + threadIdx.x;
-    if (j >= N) return;
+    constexpr int G = NT / 64;
+    const int j = blockIdx.x * 64 + (threadIdx.x & 63), gq = threadIdx.x >> 6;
     R t = 0;
-    for (int r = 0; r < parts; r++) t += P[(ll)r * N + j];
-    T *yp = y + (ll)j * iy;
-    *yp = (T)(beta == R(0) ? alpha * t : fma_r(alpha, t, beta * (R)*yp));
+    if (j < N) {
+        int r = gq;
+        for (; r + 7 * G < parts; r += 8 * G) {
+            R v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = P[(ll)(r + u * G) * N + j];
+#pragma unroll
+            for (int u = 0; u < 8; u++) t += v[u];
+        }
+        for (; r < parts; r += G) t += P[(ll)r * N + j];
+    }
+    __shared__ R red[G][64];
+    red[gq][threadIdx.x & 63] = t;
+    __syncthreads();
+    if (gq == 0 && j < N) {
+        R sum = red[0][threadIdx.x];
+#pragma unroll
+        for (int q = 1; q < G; q++) sum += red[q][threadIdx.x];
+        T *yp = y + (ll)j * iy;
+        *yp = (T)(beta == R(0) ? alpha * sum : fma_r(alpha, sum, beta * (R)*yp));
+    }
 }
 
 // ---------------- GER: A = alpha·x·yᵀ + A ----------------
@@ -426,7 +461,10 @@ int launch_gemv(int es, int trans, int M, int N, double alpha, const void *A, ll
         }
         constexpr int V = VW<T>;
         const int cblocks = (N + NT * V - 1) / (NT * V);
-        int parts = (2048 + cblocks - 1) / cblocks;
+        // about 3 blocks per CU, each summing a band of rows into FP32 (FP64) partials: the best HBM rate in a sweep of
+        // 256-8192 blocks at 16384² (fewer, longer bands keep more loads in flight per thread)
+        const int tgt = 3 * (num_cus > 0 ? num_cus : 256);
+        int parts = (tgt + cblocks - 1) / cblocks;
         const int maxparts = (M + 15) / 16;
         if (parts > maxparts) parts = maxparts;
         if (parts < 1) parts = 1;
@@ -443,7 +481,7 @@ int launch_gemv(int es, int trans, int M, int N, double alpha, const void *A, ll
         else hipLaunchKernelGGL((gemv_t1_kernel<T, false>), grid, dim3(NT), 0, stream, M, N, rpp, Ap, lda, xp, ix, P, (int)(parts == 1), (R)alpha, (R)beta, yp, iy);
         G9_HIP(hipGetLastError());
         if (parts > 1) {
-            hipLaunchKernelGGL((gemv_t2_kernel<T>), dim3((unsigned)((N + NT - 1) / NT)), dim3(NT), 0, stream, N, parts,
+            hipLaunchKernelGGL((gemv_t2_kernel<T>), dim3((unsigned)((N + 63) / 64)), dim3(NT), 0, stream, N, parts,
                                (const R *)P, (R)alpha, (R)beta, yp, iy);
             G9_HIP(hipGetLastError());
         }
