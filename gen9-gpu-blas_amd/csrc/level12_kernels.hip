@@ -232,12 +232,28 @@ __global__ void __launch_bounds__(NT) gemv_n_kernel(int M, int N, typename Comp<
     int j = lane * V;
     if (VEC) {
         const int nvec = N - N % V;
-#pragma unroll 4
+        // U steps per batch: all U·RWN loads of A (nontemporal: A is read once) are issued before the first product
+        constexpr int U = 4;
+        for (; j + (U - 1) * 64 * V < nvec; j += U * 64 * V) {
+            Vec<T> xv[U], av[U][RWN];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                xv[u] = vload(x + j + u * 64 * V);
+#pragma unroll
+                for (int r = 0; r < RWN; r++) av[u][r] = vload_nt(ar[r] + j + u * 64 * V);
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int r = 0; r < RWN; r++)
+#pragma unroll
+                    for (int e = 0; e < V; e++) s[r] = fma_r((R)av[u][r].e[e], (R)xv[u].e[e], s[r]);
+        }
         for (; j < nvec; j += 64 * V) {
             const Vec<T> xv = vload(x + j);
 #pragma unroll
             for (int r = 0; r < RWN; r++) {
-                const Vec<T> av = vload(ar[r] + j);
+                const Vec<T> av = vload_nt(ar[r] + j);
 #pragma unroll
                 for (int e = 0; e < V; e++) s[r] = fma_r((R)av.e[e], (R)xv.e[e], s[r]);
             }
