@@ -123,6 +123,8 @@ static bool hgemm_tiles_apply(const GemmCall &c) {
     }
     if (generic || c.M % 128 || c.N % 128 || c.K % 64 || c.count > 65535) return false;
     const long long es = 2;
+    // each lane's byte offset inside a 256-row (or 64-k-row) tile is 32-bit: rows of up to 8 Mi elements
+    if (c.lda * es * 256 >= (1LL << 32) || c.ldb * es * 256 >= (1LL << 32)) return false;
     return (uintptr_t)c.A % 16 == 0 && (uintptr_t)c.B % 16 == 0 && (uintptr_t)c.C % 16 == 0 && (c.lda * es) % 16 == 0 &&
            (c.ldb * es) % 16 == 0 && (c.ldc * es) % 16 == 0 &&
            (c.count == 1 || ((c.sA * es) % 16 == 0 && (c.sB * es) % 16 == 0 && (c.sC * es) % 16 == 0));

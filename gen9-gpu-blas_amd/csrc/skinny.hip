@@ -49,7 +49,7 @@ int launch_skinny(const SkinnyCall &c) {
     if (c.type == GEN9BLAS_S) return launch_typed<float>(p, vec);
     // FP16, M > 4: the matrix-core kernel when K is a multiple of its 256-k groups and the rows are 16-byte aligned
     // (MI355X, W 4096×4096 rotated over 32 copies: M = 8 11.1 → 8.8 µs, M = 16 16.0 → 9.4 µs per call)
-    if (p.M > 4 && vec && p.K % 256 == 0) {
+    if (p.M > 4 && vec && p.K % 256 == 0 && (c.swn + c.sam) * 2 * 16 < (1LL << 32)) {   // 32-bit lane offsets
         if (p.M <= 8) return launch_mfma<8, 4, 2>(p);
         return launch_mfma<16, 2, 4>(p);
     }
