@@ -76,7 +76,7 @@ static void describe(Operand &o, const void *p, long long rows, long long cols, 
     }
 }
 
-static int gemm_impl(int type, int tA, int tB, int M, int N, int K, double alpha, const void *A, int lda, long long sA,
+int gemm_impl(int type, int tA, int tB, int M, int N, int K, double alpha, const void *A, int lda, long long sA,
                      const void *B, int ldb, long long sB, double beta, void *C, int ldc, long long sC, int count) {
     const double t0 = now_s();
     G9_TRY(begin());

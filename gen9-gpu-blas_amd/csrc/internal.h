@@ -90,6 +90,9 @@ struct GemmCall {
     void *C; long long ldc, sC;
 };
 G9_HIDDEN int launch_gemm(const GemmCall &c);
+// The whole gen9blas_gemm_batched call: checks, operand resolution, skinny / MFMA dispatch, wait (gemm.hip).
+G9_HIDDEN int gemm_impl(int type, int tA, int tB, int M, int N, int K, double alpha, const void *A, int lda, long long sA,
+                        const void *B, int ldb, long long sB, double beta, void *C, int ldc, long long sC, int count);
 struct SkinnyCall {
     int type;                      // GEN9BLAS_H / HS / S
     int M, N, K;                   // C (M×N) = alpha·a·wᵀ + beta·C, a M×K, w N×K, both K-contiguous

@@ -1,6 +1,5 @@
 // Entry points of the reference ABI that this build declares and exports but does not compute yet: level 3 beyond
-// GEMM (SYMM/SYRK/SYR2K/TRMM/TRSM, reference: lib/src/level3.c), persistent packed B (reference: lib/src/packed.c) and
-// the level-2 symmetric/triangular/banded/packed functions (reference: lib/src/level12.c:267-519).
+// GEMM (SYMM/SYRK/SYR2K/TRMM/TRSM, reference: lib/src/level3.c) and the level-2 symmetric/triangular/banded/packed functions (reference: lib/src/level12.c:267-519).
 // Each one validates its type and arguments the way the reference does, then returns GEN9BLAS_ERR_UNSUPPORTED with a
 // message, so a caller (the BLAS shim among them) falls back to its CPU path. Exporting them keeps the ABI whole:
 // loaders that bind every symbol of the header (the ctypes module, the Rust crate) work unchanged.
@@ -17,32 +16,7 @@ int check_type(int type) {
 int not_built(const char *f) { G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "%s is not implemented in this build", f); }
 }  // namespace
 
-struct gen9blas_packed_b {
-    int type;
-};
-
 extern "C" {
-
-gen9blas_packed_b *gen9blas_pack_b(int type, int transB, int K, int N, const void *B, int ldb) {
-    (void)transB; (void)B; (void)ldb;
-    if (check_type(type)) return nullptr;
-    if (K <= 0 || N <= 0) {
-        fail(GEN9BLAS_ERR_INVALID_ARG, "pack_b: K = %d, N = %d", K, N);
-        return nullptr;
-    }
-    not_built("gen9blas_pack_b");
-    return nullptr;
-}
-
-int gen9blas_gemm_pb(int transA, int M, double alpha, const void *A, int lda, const gen9blas_packed_b *Bp, double beta,
-                     void *C, int ldc) {
-    (void)transA; (void)M; (void)alpha; (void)A; (void)lda; (void)beta; (void)C; (void)ldc;
-    G9_TRY(begin());
-    if (!Bp) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "gemm_pb: NULL packed B");
-    return not_built("gen9blas_gemm_pb");
-}
-
-void gen9blas_packed_b_free(gen9blas_packed_b *Bp) { (void)Bp; }
 
 #define G9_UNBUILT(name, ...)                 \
     int name(int type, __VA_ARGS__) {         \

@@ -46,6 +46,10 @@ _lib.gen9blas_free.argtypes = [ctypes.c_void_p]
 _lib.gen9blas_error.restype = ctypes.c_char_p
 _lib.gen9blas_hip_stream.restype = ctypes.c_void_p
 _lib.gen9blas_set_nowait.argtypes = [_i]
+_lib.gen9blas_pack_b.argtypes = [_i, _i, _i, _i, _p, _i]
+_lib.gen9blas_pack_b.restype = _p
+_lib.gen9blas_gemm_pb.argtypes = [_i, _i, _d, _p, _i, _p, _d, _p, _i]
+_lib.gen9blas_packed_b_free.argtypes = [_p]
 GEN9BLAS_H, GEN9BLAS_S, GEN9BLAS_HS, GEN9BLAS_D = 0, 1, 2, 3
 FEAT_FP16, FEAT_FP32, FEAT_FP64 = 0, 1, 2
 _lib.gen9blas_version.restype = ctypes.c_int
