@@ -38,7 +38,7 @@ G9_HIDDEN int begin();
 G9_HIDDEN double now_s();
 
 // ---- operands ----
-enum Slot { SLOT_A = 0, SLOT_B, SLOT_C, SLOT_P, SLOT_Q, NSLOTS };
+enum Slot { SLOT_A = 0, SLOT_B, SLOT_C, SLOT_P, SLOT_Q, SLOT_T, SLOT_X, SLOT_Y, SLOT_W, NSLOTS };
 // Device scratch owned by the library, grown on demand and kept between calls (the reference's work buffers,
 // reference: lib/src/core.c:272-277). Growing waits for queued work first.
 G9_HIDDEN int scratch(int slot, size_t bytes, void **p);

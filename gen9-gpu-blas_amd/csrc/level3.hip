@@ -1,0 +1,393 @@
+// Level 3 beyond GEMM: SYMM, SYRK, SYR2K, TRMM, TRSM, all on the MFMA GEMM kernels.
+//
+// Semantics follow the reference (reference: lib/src/level3.c, declarations lib/gen9blas.h:98-112; row-major, the
+// uplo triangle of a symmetric or triangular A is the one read, diag = 1 means a unit diagonal that is not read):
+// - SYMM: C = alpha·A·B + beta·C (left, A M×M) or alpha·B·A + beta·C (right, A N×N). As the reference (level3.c:
+//   13-60), the symmetric matrix is first made explicit from its triangle (here into a device work buffer), then one
+//   GEMM runs;
+// - TRMM: B = alpha·op(A)·B (left) or alpha·B·op(A) (right). op(A) is made explicit with zeros outside its triangle;
+//   the product runs in row (left) or column (right) bands, each over only the k range where op(A) is non-zero
+//   (4 bands from n = 512: about 62 % of the full work, as level3.c:28-49), into a work buffer copied back to B;
+// - SYRK / SYR2K: only the uplo triangle of C changes. The product runs in row bands over the columns the triangle
+//   needs (level3.c:76-97) into a work buffer, then a merge kernel writes alpha·product + beta·C on the triangle
+//   (C not read when beta = 0). SYR2K joins X = [op(A) | op(B)] and Y = [op(B) | op(A)] so that
+//   X·Yᵀ = op(A)·op(B)ᵀ + op(B)·op(A)ᵀ is one accumulation (level3.c:109-125);
+// - TRSM: op(A)·X = alpha·B (left) or X·op(A) = alpha·B (right), X overwrites B. As the reference (level3.c:127-215)
+//   the problem is brought to L·Y = alpha·R with L lower triangular (an upper matrix by reversing the index order,
+//   the right side by transposition), the diagonal blocks of L are inverted in FP64, and for each block row
+//   Y_i -= L[i, <i]·Y[<i] and Y_i = inv(L_ii)·Y_i run on the GEMM kernels. Blocks are 128 rows (the MFMA tile).
+// Products of the element type round as a GEMM does; the merge / copy passes round once more, as the reference's
+// separate epilogues do.
+#include "internal.h"
+#include <type_traits>
+
+namespace g9 {
+namespace l3 {
+
+typedef long long ll;
+typedef _Float16 f16;
+
+template <class T> struct Acc { using S = float; };
+template <> struct Acc<double> { using S = double; };
+
+template <class F> static int by_es(int es, F f) {
+    if (es == 2) return f((f16 *)nullptr);
+    if (es == 4) return f((float *)nullptr);
+    return f((double *)nullptr);
+}
+
+static unsigned grid_for(ll n) {
+    const ll g = (n + 255) / 256, cap = (ll)(num_cus > 0 ? num_cus : 256) * 16;
+    return (unsigned)(g < 1 ? 1 : g > cap ? cap : g);
+}
+
+// F (n×n, row stride n) = the full matrix G built from the uplo triangle of A (tr: F = Gᵀ). sym: G mirrored from the
+// triangle; otherwise triangular with zeros outside it and, with unit, ones on the diagonal.
+template <class T>
+__global__ void __launch_bounds__(256) expand_kernel(const T *A, ll lda, T *F, int n, int lower, int sym, int unit, int tr) {
+    const ll nn = (ll)n * n;
+    for (ll e = blockIdx.x * 256ll + threadIdx.x; e < nn; e += (ll)gridDim.x * 256) {
+        const int i = (int)(e / n), j = (int)(e % n);
+        const int p = tr ? j : i, q = tr ? i : j;   // F[i][j] = G[p][q]
+        const bool in = lower ? q <= p : q >= p;
+        T v;
+        if (sym) v = in ? A[(ll)p * lda + q] : A[(ll)q * lda + p];
+        else v = in ? ((p == q && unit) ? T(1) : A[(ll)p * lda + q]) : T(0);
+        F[e] = v;
+    }
+}
+
+// C = P + beta·C on the lower (or upper) triangle of the N×N matrix C (C not read when beta = 0; P null: zero).
+template <class T>
+__global__ void __launch_bounds__(256) merge_kernel(const T *P, ll ldp, T *C, ll ldc, int N, int lower,
+                                                    typename Acc<T>::S beta) {
+    using S = typename Acc<T>::S;
+    const ll nn = (ll)N * N;
+    for (ll e = blockIdx.x * 256ll + threadIdx.x; e < nn; e += (ll)gridDim.x * 256) {
+        const int i = (int)(e / N), j = (int)(e % N);
+        if (lower ? j > i : j < i) continue;
+        S v = P ? (S)P[(ll)i * ldp + j] : S(0);
+        T *c = C + (ll)i * ldc + j;
+        if (beta != S(0)) v += beta * (S)*c;
+        *c = (T)v;
+    }
+}
+
+// X = [op(A) | op(B)], Y = [op(B) | op(A)], both N×2K with row stride 2K (op: A stored K×N when trans).
+template <class T>
+__global__ void __launch_bounds__(256) join_kernel(const T *A, ll lda, const T *B, ll ldb, T *X, T *Y, int N, int K, int trans) {
+    const ll k2 = 2ll * K, tot = (ll)N * k2;
+    for (ll e = blockIdx.x * 256ll + threadIdx.x; e < tot; e += (ll)gridDim.x * 256) {
+        const int i = (int)(e / k2), c = (int)(e % k2), k = c < K ? c : c - K;
+        const T a = trans ? A[(ll)k * lda + i] : A[(ll)i * lda + k];
+        const T b = trans ? B[(ll)k * ldb + i] : B[(ll)i * ldb + k];
+        X[e] = c < K ? a : b;
+        Y[e] = c < K ? b : a;
+    }
+}
+
+// TRSM set-up: L (n×n lower) from op'(A) = (tr ? Aᵀ : A) restricted to the triangle of A (uplo), reversed in both
+// indices when rev; unit: ones on the diagonal.
+template <class T>
+__global__ void __launch_bounds__(256) trsm_l_kernel(const T *A, ll lda, T *L, int n, int lower, int tr, int unit, int rev) {
+    const ll nn = (ll)n * n;
+    for (ll e = blockIdx.x * 256ll + threadIdx.x; e < nn; e += (ll)gridDim.x * 256) {
+        const int i = (int)(e / n), j = (int)(e % n);
+        const int p = rev ? n - 1 - i : i, q = rev ? n - 1 - j : j;   // element (p, q) of op'(A)
+        const int r = tr ? q : p, c = tr ? p : q;                      // = A[r][c]
+        const bool in = lower ? c <= r : c >= r;
+        L[e] = in ? ((r == c && unit) ? T(1) : A[(ll)r * lda + c]) : T(0);
+    }
+}
+// Y (n×m, row stride m) = alpha·R with R = B (left, M×N = n×m) or Bᵀ (right), rows reversed when rev.
+template <class T>
+__global__ void __launch_bounds__(256) trsm_y_kernel(const T *B, ll ldb, T *Y, int n, int m, int left, int rev,
+                                                     typename Acc<T>::S alpha) {
+    using S = typename Acc<T>::S;
+    const ll nm = (ll)n * m;
+    for (ll e = blockIdx.x * 256ll + threadIdx.x; e < nm; e += (ll)gridDim.x * 256) {
+        const int i = (int)(e / m), j = (int)(e % m), p = rev ? n - 1 - i : i;
+        const T b = left ? B[(ll)p * ldb + j] : B[(ll)j * ldb + p];
+        Y[e] = (T)(alpha * (S)b);
+    }
+}
+// B = X from Y (inverse of trsm_y_kernel's index map, without alpha).
+template <class T>
+__global__ void __launch_bounds__(256) trsm_store_kernel(const T *Y, T *B, ll ldb, int n, int m, int left, int rev) {
+    const ll nm = (ll)n * m;
+    for (ll e = blockIdx.x * 256ll + threadIdx.x; e < nm; e += (ll)gridDim.x * 256) {
+        const int i = (int)(e / m), j = (int)(e % m), p = rev ? n - 1 - i : i;
+        if (left) B[(ll)p * ldb + j] = Y[e];
+        else B[(ll)j * ldb + p] = Y[e];
+    }
+}
+
+constexpr int TRSM_NB = 128;
+// Inverse of the diagonal block bi of L (rows and columns r0 .. r0+b-1, b ≤ TRSM_NB), in FP64, stored in the element
+// type as a b×b lower matrix at Inv + bi·NB². Thread j forms column j by forward substitution:
+// X[j][j] = 1 / L[j][j], X[i][j] = −(Σ_{k=j}^{i-1} L[i][k]·X[k][j]) / L[i][i]. The columns live in LDS (128 KiB).
+template <class T>
+__global__ void __launch_bounds__(TRSM_NB) trsm_inv_kernel(const T *L, int n, T *Inv) {
+    __shared__ double X[TRSM_NB][TRSM_NB];
+    const int bi = blockIdx.x, r0 = bi * TRSM_NB, b = min(TRSM_NB, n - r0), j = threadIdx.x;
+    if (j < b) {
+        for (int i = 0; i < j; i++) X[i][j] = 0.0;
+        X[j][j] = 1.0 / (double)L[(ll)(r0 + j) * n + r0 + j];
+        for (int i = j + 1; i < b; i++) {
+            const T *li = L + (ll)(r0 + i) * n + r0;
+            double s = 0.0;
+            for (int k = j; k < i; k++) s = __builtin_fma((double)li[k], X[k][j], s);
+            X[i][j] = -s / (double)li[i];
+        }
+    }
+    __syncthreads();
+    T *out = Inv + (ll)bi * TRSM_NB * TRSM_NB;
+    for (int e = threadIdx.x; e < b * b; e += TRSM_NB) out[e] = (T)X[e / b][e % b];
+}
+
+// One GEMM on device operands (no staging, no wait): C = alpha·op(A)·op(B) + beta·C.
+static int dgemm_dev(int type, int tA, int tB, int M, int N, int K, double alpha, const void *A, ll lda, const void *B,
+                     ll ldb, double beta, void *C, ll ldc) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    GemmCall g;
+    g.type = type;
+    g.tA = tA; g.tB = tB;
+    g.M = M; g.N = N; g.K = K;
+    g.count = 1;
+    g.alpha = alpha; g.beta = beta;
+    g.A = A; g.lda = lda; g.sA = 0;
+    g.B = B; g.ldb = ldb; g.sB = 0;
+    g.C = C; g.ldc = ldc; g.sC = 0;
+    return launch_gemm(g);
+}
+
+static int bands(int n) { return n >= 512 ? 4 : 1; }
+static int band_rows(int n) {
+    const int p = bands(n);
+    return ((n + p - 1) / p + 127) / 128 * 128;
+}
+
+static int check_type(int type) {
+    if (type < 0 || type > 3) G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "type %d unavailable", type);
+    return 0;
+}
+
+// Triangle (lower / upper) of C = alpha·X·Yᵀ + beta·C for device X, Y (N×K, or stored K×N when trans) and resolved C.
+static int tri_product(int type, int lower, int trans, int N, int K, double alpha, const void *X, ll ldx, const void *Y,
+                       ll ldy, double beta, void *C, ll ldc) {
+    const int es = elem_size(type);
+    void *P = nullptr;
+    if (K > 0 && alpha != 0.0) {
+        G9_TRY(scratch(SLOT_T, (size_t)N * N * es, &P));
+        const int nb = band_rows(N);
+        for (int i0 = 0; i0 < N; i0 += nb) {
+            const int b = N - i0 < nb ? N - i0 : nb;
+            const int c0 = lower ? 0 : i0, c1 = lower ? i0 + b : N;
+            // rows i0.. of op(X) times columns c0..c1 of op(Y)ᵀ
+            const char *xa = (const char *)X + (trans ? (ll)i0 : (ll)i0 * ldx) * es;
+            const char *yb = (const char *)Y + (trans ? (ll)c0 : (ll)c0 * ldy) * es;
+            G9_TRY(dgemm_dev(type, trans, !trans, b, c1 - c0, K, alpha, xa, ldx, yb, ldy, 0.0,
+                             (char *)P + ((ll)i0 * N + c0) * es, N));
+        }
+    }
+    return by_es(es, [&](auto *tag) -> int {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        using S = typename Acc<T>::S;
+        hipLaunchKernelGGL((merge_kernel<T>), dim3(grid_for((ll)N * N)), dim3(256), 0, stream, (const T *)P, (ll)N, (T *)C,
+                           ldc, N, lower, (S)beta);
+        G9_HIP(hipGetLastError());
+        return 0;
+    });
+}
+
+}  // namespace l3
+}  // namespace g9
+
+using namespace g9;
+using namespace g9::l3;
+
+extern "C" {
+
+int gen9blas_symm(int type, int side, int uplo, int M, int N, double alpha, const void *A, int lda, const void *B, int ldb,
+                  double beta, void *C, int ldc) {
+    G9_TRY(begin());
+    G9_TRY(check_type(type));
+    if (M <= 0 || N <= 0) return 0;
+    const int left = side == GEN9BLAS_LEFT, n = left ? M : N, es = elem_size(type);
+    if (!A || !B || !C) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "symm: NULL matrix pointer");
+    if (lda < n || ldb < N || ldc < N)
+        G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "symm: leading dimension too small (lda %d, ldb %d, ldc %d)", lda, ldb, ldc);
+    Operand oa;
+    oa.host = A; oa.es = es; oa.rows = n; oa.cols = n; oa.caller_ld = lda;
+    G9_TRY(resolve(oa, SLOT_A, true, false, true));
+    void *F;
+    G9_TRY(scratch(SLOT_T, (size_t)n * n * es, &F));
+    G9_TRY(by_es(es, [&](auto *tag) -> int {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL((expand_kernel<T>), dim3(grid_for((ll)n * n)), dim3(256), 0, stream, (const T *)oa.dev, oa.ld,
+                           (T *)F, n, uplo == GEN9BLAS_LOWER, 1, 0, 0);
+        G9_HIP(hipGetLastError());
+        return 0;
+    }));
+    if (left) return gemm_impl(type, 0, 0, M, N, M, alpha, F, n, 0, B, ldb, 0, beta, C, ldc, 0, 1);
+    return gemm_impl(type, 0, 0, M, N, N, alpha, B, ldb, 0, F, n, 0, beta, C, ldc, 0, 1);
+}
+
+int gen9blas_trmm(int type, int side, int uplo, int transA, int diag, int M, int N, double alpha, const void *A, int lda,
+                  void *B, int ldb) {
+    G9_TRY(begin());
+    G9_TRY(check_type(type));
+    if (M <= 0 || N <= 0) return 0;
+    const int left = side == GEN9BLAS_LEFT, n = left ? M : N, es = elem_size(type);
+    if (!A || !B) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "trmm: NULL matrix pointer");
+    if (lda < n || ldb < N) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "trmm: leading dimension too small (lda %d, ldb %d)", lda, ldb);
+    Operand ops[2];
+    ops[0].host = A; ops[0].es = es; ops[0].rows = n; ops[0].cols = n; ops[0].caller_ld = lda;
+    ops[1].host = B; ops[1].es = es; ops[1].rows = M; ops[1].cols = N; ops[1].caller_ld = ldb;
+    G9_TRY(resolve(ops[0], SLOT_A, true, false, true));
+    G9_TRY(resolve(ops[1], SLOT_B, true, true, true));
+    last_zc = (ops[0].zc ? 1 : 0) | (ops[1].zc ? 2 | 4 : 0);
+    void *F, *Z;
+    G9_TRY(scratch(SLOT_T, (size_t)n * n * es, &F));
+    G9_TRY(scratch(SLOT_X, (size_t)M * N * es, &Z));
+    const int tr = transA != 0, lower = (uplo == GEN9BLAS_LOWER) != tr;   // F = op(A) is lower triangular?
+    G9_TRY(by_es(es, [&](auto *tag) -> int {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL((expand_kernel<T>), dim3(grid_for((ll)n * n)), dim3(256), 0, stream, (const T *)ops[0].dev,
+                           ops[0].ld, (T *)F, n, uplo == GEN9BLAS_LOWER, 0, diag != 0, tr);
+        G9_HIP(hipGetLastError());
+        return 0;
+    }));
+    const ll ldB = ops[1].ld;
+    const char *Bd = (const char *)ops[1].dev;
+    const int nb = band_rows(n);
+    for (int i0 = 0; i0 < n; i0 += nb) {
+        const int b = n - i0 < nb ? n - i0 : nb;
+        if (left) {   // Z rows i0..i0+b = alpha·F[i0.., k0..k1]·B[k0..k1, :]
+            const int k0 = lower ? 0 : i0, k1 = lower ? i0 + b : n;
+            G9_TRY(dgemm_dev(type, 0, 0, b, N, k1 - k0, alpha, (const char *)F + ((ll)i0 * n + k0) * es, n,
+                             Bd + (ll)k0 * ldB * es, ldB, 0.0, (char *)Z + (ll)i0 * N * es, N));
+        } else {      // Z columns i0..i0+b = alpha·B[:, k0..k1]·F[k0..k1, i0..]
+            const int k0 = lower ? i0 : 0, k1 = lower ? n : i0 + b;
+            G9_TRY(dgemm_dev(type, 0, 0, M, b, k1 - k0, alpha, Bd + (ll)k0 * es, ldB,
+                             (const char *)F + ((ll)k0 * n + i0) * es, n, 0.0, (char *)Z + (ll)i0 * es, N));
+        }
+    }
+    G9_HIP(hipMemcpy2DAsync(ops[1].dev, (size_t)ldB * es, Z, (size_t)N * es, (size_t)N * es, (size_t)M,
+                            hipMemcpyDeviceToDevice, stream));
+    return finish(ops, 2);
+}
+
+static int syrk_common(int type, int uplo, int trans, int N, int K, double alpha, const void *A, int lda, const void *B,
+                       int ldb, double beta, void *C, int ldc, bool two) {
+    G9_TRY(begin());
+    G9_TRY(check_type(type));
+    if (N <= 0) return 0;
+    if (K < 0) K = 0;
+    const int es = elem_size(type);
+    if (!C || (K > 0 && (!A || (two && !B)))) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "%s: NULL matrix pointer", two ? "syr2k" : "syrk");
+    const int need = trans ? N : K;
+    if ((K > 0 && (lda < need || (two && ldb < need))) || ldc < N)
+        G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "%s: leading dimension too small (lda %d, ldb %d, ldc %d)", two ? "syr2k" : "syrk",
+                lda, ldb, ldc);
+    Operand ops[3];
+    int nops = 0;
+    if (K > 0) {
+        ops[0].host = A; ops[0].es = es; ops[0].rows = trans ? K : N; ops[0].cols = trans ? N : K; ops[0].caller_ld = lda;
+        G9_TRY(resolve(ops[0], SLOT_A, true, false, true));
+        nops = 1;
+        if (two) {
+            ops[1].host = B; ops[1].es = es; ops[1].rows = trans ? K : N; ops[1].cols = trans ? N : K; ops[1].caller_ld = ldb;
+            G9_TRY(resolve(ops[1], SLOT_B, true, false, true));
+            nops = 2;
+        }
+    }
+    Operand &oc = ops[nops];
+    oc.host = C; oc.es = es; oc.rows = N; oc.cols = N; oc.caller_ld = ldc;
+    G9_TRY(resolve(oc, SLOT_C, true, true, true));   // the other triangle is kept: C always comes in
+    const int lower = uplo == GEN9BLAS_LOWER;
+    if (K == 0) {
+        G9_TRY(tri_product(type, lower, 0, N, 0, alpha, nullptr, 0, nullptr, 0, beta, oc.dev, oc.ld));
+    } else if (!two) {
+        G9_TRY(tri_product(type, lower, trans, N, K, alpha, ops[0].dev, ops[0].ld, ops[0].dev, ops[0].ld, beta, oc.dev, oc.ld));
+    } else {
+        void *X, *Y;
+        G9_TRY(scratch(SLOT_X, (size_t)N * 2 * K * es, &X));
+        G9_TRY(scratch(SLOT_Y, (size_t)N * 2 * K * es, &Y));
+        G9_TRY(by_es(es, [&](auto *tag) -> int {
+            using T = std::remove_pointer_t<decltype(tag)>;
+            hipLaunchKernelGGL((join_kernel<T>), dim3(grid_for((ll)N * 2 * K)), dim3(256), 0, stream, (const T *)ops[0].dev,
+                               ops[0].ld, (const T *)ops[1].dev, ops[1].ld, (T *)X, (T *)Y, N, K, trans);
+            G9_HIP(hipGetLastError());
+            return 0;
+        }));
+        G9_TRY(tri_product(type, lower, 0, N, 2 * K, alpha, X, 2ll * K, Y, 2ll * K, beta, oc.dev, oc.ld));
+    }
+    last_zc = (nops > 0 && ops[0].zc ? 1 : 0) | (nops > 1 && ops[1].zc ? 2 : 0) | (oc.zc ? 4 : 0);
+    return finish(ops, nops + 1);
+}
+
+int gen9blas_syrk(int type, int uplo, int trans, int N, int K, double alpha, const void *A, int lda, double beta, void *C,
+                  int ldc) {
+    return syrk_common(type, uplo, trans != 0, N, K, alpha, A, lda, nullptr, 0, beta, C, ldc, false);
+}
+
+int gen9blas_syr2k(int type, int uplo, int trans, int N, int K, double alpha, const void *A, int lda, const void *B, int ldb,
+                   double beta, void *C, int ldc) {
+    return syrk_common(type, uplo, trans != 0, N, K, alpha, A, lda, B, ldb, beta, C, ldc, true);
+}
+
+int gen9blas_trsm(int type, int side, int uplo, int transA, int diag, int M, int N, double alpha, const void *A, int lda,
+                  void *B, int ldb) {
+    G9_TRY(begin());
+    G9_TRY(check_type(type));
+    if (M <= 0 || N <= 0) return 0;
+    const int left = side == GEN9BLAS_LEFT, n = left ? M : N, m = left ? N : M, es = elem_size(type);
+    if (!A || !B) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "trsm: NULL matrix pointer");
+    if (lda < n || ldb < N) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "trsm: leading dimension too small (lda %d, ldb %d)", lda, ldb);
+    Operand ops[2];
+    ops[0].host = A; ops[0].es = es; ops[0].rows = n; ops[0].cols = n; ops[0].caller_ld = lda;
+    ops[1].host = B; ops[1].es = es; ops[1].rows = M; ops[1].cols = N; ops[1].caller_ld = ldb;
+    G9_TRY(resolve(ops[0], SLOT_A, true, false, true));
+    G9_TRY(resolve(ops[1], SLOT_B, true, true, true));
+    last_zc = (ops[0].zc ? 1 : 0) | (ops[1].zc ? 2 | 4 : 0);
+    // L·Y = alpha·R: op'(A) = left ? op(A) : op(A)ᵀ; lower when the triangle of A, transposed or not, is lower
+    const int tr = left ? transA != 0 : transA == 0;
+    const int lower = (uplo == GEN9BLAS_LOWER) != (tr != 0), rev = !lower;
+    const int nbl = (n + TRSM_NB - 1) / TRSM_NB;
+    void *Ld, *Yd, *Iv, *Zd;
+    G9_TRY(scratch(SLOT_T, (size_t)n * n * es, &Ld));
+    G9_TRY(scratch(SLOT_X, (size_t)n * m * es, &Yd));
+    G9_TRY(scratch(SLOT_Y, (size_t)nbl * TRSM_NB * TRSM_NB * es, &Iv));
+    G9_TRY(scratch(SLOT_W, (size_t)TRSM_NB * m * es, &Zd));
+    G9_TRY(by_es(es, [&](auto *tag) -> int {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        using S = typename Acc<T>::S;
+        hipLaunchKernelGGL((trsm_l_kernel<T>), dim3(grid_for((ll)n * n)), dim3(256), 0, stream, (const T *)ops[0].dev,
+                           ops[0].ld, (T *)Ld, n, uplo == GEN9BLAS_LOWER, tr, diag != 0, rev);
+        hipLaunchKernelGGL((trsm_y_kernel<T>), dim3(grid_for((ll)n * m)), dim3(256), 0, stream, (const T *)ops[1].dev,
+                           ops[1].ld, (T *)Yd, n, m, left, rev, (S)alpha);
+        hipLaunchKernelGGL((trsm_inv_kernel<T>), dim3(nbl), dim3(TRSM_NB), 0, stream, (const T *)Ld, n, (T *)Iv);
+        G9_HIP(hipGetLastError());
+        return 0;
+    }));
+    for (int bi = 0; bi < nbl; bi++) {
+        const int i0 = bi * TRSM_NB, b = n - i0 < TRSM_NB ? n - i0 : TRSM_NB;
+        char *Yi = (char *)Yd + (ll)i0 * m * es;
+        if (i0 > 0)   // Y_i -= L[i0.., 0..i0]·Y[0..i0]
+            G9_TRY(dgemm_dev(type, 0, 0, b, m, i0, -1.0, (const char *)Ld + (ll)i0 * n * es, n, Yd, m, 1.0, Yi, m));
+        // Y_i = inv(L_ii)·Y_i (through Z: the product may not overwrite its input)
+        G9_TRY(dgemm_dev(type, 0, 0, b, m, b, 1.0, (const char *)Iv + (ll)bi * TRSM_NB * TRSM_NB * es, b, Yi, m, 0.0, Zd, m));
+        G9_HIP(hipMemcpyAsync(Yi, Zd, (size_t)b * m * es, hipMemcpyDeviceToDevice, stream));
+    }
+    G9_TRY(by_es(es, [&](auto *tag) -> int {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        hipLaunchKernelGGL((trsm_store_kernel<T>), dim3(grid_for((ll)n * m)), dim3(256), 0, stream, (const T *)Yd,
+                           (T *)ops[1].dev, ops[1].ld, n, m, left, rev);
+        G9_HIP(hipGetLastError());
+        return 0;
+    }));
+    return finish(ops, 2);
+}
+
+}  // extern "C"

@@ -1,5 +1,5 @@
-// Entry points of the reference ABI that this build declares and exports but does not compute yet: level 3 beyond
-// GEMM (SYMM/SYRK/SYR2K/TRMM/TRSM, reference: lib/src/level3.c) and the level-2 symmetric/triangular/banded/packed functions (reference: lib/src/level12.c:267-519).
+// Entry points of the reference ABI that this build declares and exports but does not compute yet: the level-2
+// symmetric/triangular/banded/packed functions (reference: lib/src/level12.c:267-519).
 // Each one validates its type and arguments the way the reference does, then returns GEN9BLAS_ERR_UNSUPPORTED with a
 // message, so a caller (the BLAS shim among them) falls back to its CPU path. Exporting them keeps the ABI whole:
 // loaders that bind every symbol of the header (the ctypes module, the Rust crate) work unchanged.
@@ -24,11 +24,6 @@ extern "C" {
         return not_built(#name);              \
     }
 
-G9_UNBUILT(gen9blas_symm, int, int, int, int, double, const void *, int, const void *, int, double, void *, int)
-G9_UNBUILT(gen9blas_syrk, int, int, int, int, double, const void *, int, double, void *, int)
-G9_UNBUILT(gen9blas_syr2k, int, int, int, int, double, const void *, int, const void *, int, double, void *, int)
-G9_UNBUILT(gen9blas_trmm, int, int, int, int, int, int, double, const void *, int, void *, int)
-G9_UNBUILT(gen9blas_trsm, int, int, int, int, int, int, double, const void *, int, void *, int)
 G9_UNBUILT(gen9blas_symv, int, int, double, const void *, int, const void *, int, double, void *, int)
 G9_UNBUILT(gen9blas_trmv, int, int, int, int, const void *, int, void *, int)
 G9_UNBUILT(gen9blas_trsv, int, int, int, int, const void *, int, void *, int)

@@ -72,7 +72,10 @@ def test_functions_outside_this_build_report_unsupported(L):
     """Entry points of the reference ABI that this build exports without computing them return UNSUPPORTED (so the
     BLAS shim falls back to the CPU), after the same type check as the reference."""
     a = np.eye(8, dtype=np.float32)
+    x = np.ones(8, np.float32)
     d = ctypes.c_double
-    assert L.gen9blas_symm(1, 0, 0, 8, 8, d(1.0), a.ctypes.data, 8, a.ctypes.data, 8, d(0.0), a.ctypes.data, 8) == UNSUPPORTED
+    assert L.gen9blas_symv(1, 0, 8, d(1.0), a.ctypes.data, 8, x.ctypes.data, 1, d(0.0), x.ctypes.data, 1) == UNSUPPORTED
+    assert L.gen9blas_symv(9, 0, 8, d(1.0), a.ctypes.data, 8, x.ctypes.data, 1, d(0.0), x.ctypes.data, 1) == UNSUPPORTED
+    assert b"type 9" in L.gen9blas_error()
     assert L.gen9blas_symm(9, 0, 0, 8, 8, d(1.0), a.ctypes.data, 8, a.ctypes.data, 8, d(0.0), a.ctypes.data, 8) == UNSUPPORTED
     assert b"type 9" in L.gen9blas_error()

@@ -1,0 +1,156 @@
+"""Level 3 beyond GEMM on the GPU: SYMM, SYRK, SYR2K, TRMM, TRSM against the float64 closed forms.
+
+Follows the reference's level-3 test (reference: lib/test_level3.py:38-137): the same sides, triangles, transposes and
+unit diagonals, error e = |result − ref| / (|alpha|·(|A|·|B|) + |beta·C|) with the reference's mean / max bounds
+(FP16 both modes 4.9e-4 / 5e-3, FP32 1e-6 / 1e-5, FP64 1e-14 / 1e-13), the other triangle of C unchanged by SYRK and
+SYR2K, and TRSM's solution error max|X − X_ref| / max|X_ref| on well-conditioned triangles (FP64 1e-12, FP32 1e-4, FP16
+5e-3). Added: sizes from 512 (the banded products and several TRSM blocks) and device-resident operands.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [("H", np.float16, False, (4.9e-4, 5e-3)), ("HS", np.float16, True, (4.9e-4, 5e-3)),
+         ("S", np.float32, False, (1e-6, 1e-5)), ("D", np.float64, False, (1e-14, 1e-13))]
+IDS = [t[0] for t in TYPES]
+
+
+def _check(W, ref, scale, tol, mask=None, tag=""):
+    e = np.abs(np.asarray(W, np.float64) - ref) / np.maximum(scale, 1e-30)
+    if mask is not None:
+        e = e[mask]
+    assert e.mean() <= tol[0] and e.max() <= tol[1], f"{tag}: mean {e.mean():.2e} max {e.max():.2e}"
+
+
+def f64(x):
+    return np.asarray(x, np.float64)
+
+
+@pytest.mark.parametrize("kind,dt,acc,tol", TYPES, ids=IDS)
+@pytest.mark.parametrize("M,N", [(70, 45), (520, 300)])
+def test_symm(g9, kind, dt, acc, tol, M, N):
+    rng = np.random.default_rng(1)
+    for side in "LR":
+        for uplo in "LU":
+            n = M if side == "L" else N
+            S = rng.uniform(-1, 1, (n, n)).astype(dt)
+            Ss = np.tril(f64(S)) + np.tril(f64(S), -1).T if uplo == "L" else np.triu(f64(S)) + np.triu(f64(S), 1).T
+            B, C0 = rng.uniform(-1, 1, (M, N)).astype(dt), rng.uniform(-1, 1, (M, N)).astype(dt)
+            W = g9.symm(S, B, side, uplo, 2.0, -1.0, C0.copy(), accurate=acc)
+            P = Ss @ f64(B) if side == "L" else f64(B) @ Ss
+            Pa = np.abs(Ss) @ np.abs(f64(B)) if side == "L" else np.abs(f64(B)) @ np.abs(Ss)
+            _check(W, 2.0 * P - f64(C0), 2.0 * Pa + np.abs(f64(C0)), tol, tag=f"symm {side}{uplo} {M}x{N}")
+
+
+@pytest.mark.parametrize("kind,dt,acc,tol", TYPES, ids=IDS)
+@pytest.mark.parametrize("N,K", [(60, 90), (600, 200)])
+def test_syrk_syr2k(g9, kind, dt, acc, tol, N, K):
+    rng = np.random.default_rng(2)
+    for uplo in "LU":
+        mask = np.tril(np.ones((N, N), bool)) if uplo == "L" else np.triu(np.ones((N, N), bool))
+        for tr in (False, True):
+            A = rng.uniform(-1, 1, (K, N) if tr else (N, K)).astype(dt)
+            B = rng.uniform(-1, 1, (K, N) if tr else (N, K)).astype(dt)
+            C0 = rng.uniform(-1, 1, (N, N)).astype(dt)
+            oA, oB = (f64(A).T, f64(B).T) if tr else (f64(A), f64(B))
+            W = g9.syrk(A, uplo, tr, 0.7, 0.3, C0.copy(), accurate=acc)
+            _check(W, 0.7 * oA @ oA.T + 0.3 * f64(C0), 0.7 * np.abs(oA) @ np.abs(oA).T + 0.3 * np.abs(f64(C0)), tol,
+                   mask, f"syrk {uplo} t={tr}")
+            assert np.array_equal(W[~mask], C0[~mask]), "syrk changed the other triangle"
+            W = g9.syr2k(A, B, uplo, tr, 0.7, 0.3, C0.copy(), accurate=acc)
+            _check(W, 0.7 * (oA @ oB.T + oB @ oA.T) + 0.3 * f64(C0),
+                   0.7 * (np.abs(oA) @ np.abs(oB).T + np.abs(oB) @ np.abs(oA).T) + 0.3 * np.abs(f64(C0)), tol, mask,
+                   f"syr2k {uplo} t={tr}")
+            assert np.array_equal(W[~mask], C0[~mask]), "syr2k changed the other triangle"
+            # beta = 0: C is not read (NaN in the triangle does not propagate), the other triangle stays
+            Cn = C0.copy()
+            Cn[mask] = np.nan
+            W = g9.syrk(A, uplo, tr, 1.0, 0.0, Cn, accurate=acc)
+            assert np.isfinite(W[mask]).all() and np.array_equal(W[~mask], C0[~mask])
+
+
+@pytest.mark.parametrize("kind,dt,acc,tol", TYPES, ids=IDS)
+@pytest.mark.parametrize("M,N", [(50, 70), (530, 260)])
+def test_trmm(g9, kind, dt, acc, tol, M, N):
+    rng = np.random.default_rng(3)
+    for side in "LR":
+        for uplo in "LU":
+            for ta in (False, True):
+                for dg in (False, True):
+                    n = M if side == "L" else N
+                    A, B = rng.uniform(-1, 1, (n, n)).astype(dt), rng.uniform(-1, 1, (M, N)).astype(dt)
+                    T = np.tril(f64(A)) if uplo == "L" else np.triu(f64(A))
+                    if dg:
+                        np.fill_diagonal(T, 1.0)
+                    T = T.T if ta else T
+                    W = g9.trmm(A, B, side, uplo, ta, dg, 1.5, accurate=acc)
+                    P = T @ f64(B) if side == "L" else f64(B) @ T
+                    Pa = np.abs(T) @ np.abs(f64(B)) if side == "L" else np.abs(f64(B)) @ np.abs(T)
+                    _check(W, 1.5 * P, 1.5 * Pa, tol, tag=f"trmm {side}{uplo} tA={ta} diag={dg}")
+
+
+TRSM_TYPES = [("D", np.float64, False, 1e-12), ("S", np.float32, False, 1e-4), ("H", np.float16, False, 5e-3),
+              ("HS", np.float16, True, 5e-3)]
+
+
+@pytest.mark.parametrize("kind,dt,acc,tol", TRSM_TYPES, ids=[t[0] for t in TRSM_TYPES])
+def test_trsm(g9, kind, dt, acc, tol):
+    rng = np.random.default_rng(4)
+    for side in "LR":
+        for uplo in "LU":
+            for ta in (False, True):
+                for dg in (False, True):
+                    for (M, N) in [(40, 30), (300, 200), (70, 600)]:
+                        n = M if side == "L" else N
+                        A = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+                        A[np.diag_indices(n)] = n if not dg else 0.5
+                        if dg:   # the diagonal is not read; conditioning from a scaled off-diagonal part
+                            A *= 1.0 / n
+                            A[np.diag_indices(n)] = 123.0
+                        B = rng.uniform(-1, 1, (M, N)).astype(np.float32)
+                        A, B = A.astype(dt), B.astype(dt)
+                        T = np.tril(f64(A)) if uplo == "L" else np.triu(f64(A))
+                        if dg:
+                            np.fill_diagonal(T, 1.0)
+                        T = T.T if ta else T
+                        Xr = (np.linalg.solve(T, 2.0 * f64(B)) if side == "L" else np.linalg.solve(T.T, 2.0 * f64(B).T).T)
+                        X = f64(g9.trsm(A, B, side, uplo, ta, dg, 2.0, accurate=acc))
+                        e = np.abs(X - Xr).max() / np.abs(Xr).max()
+                        assert e <= tol, f"trsm {kind} {side}{uplo} tA={ta} diag={dg} {M}x{N}: {e:.1e}"
+
+
+def test_level3_device_operands(g9, torch_dev):
+    """SYMM, SYRK, TRMM and TRSM on device tensors through the C ABI: results in place, zero-copy bits set."""
+    torch = torch_dev
+    rng = np.random.default_rng(5)
+    L = g9._lib
+    d, p = ctypes.c_double, ctypes.c_void_p
+    n, m = 256, 192
+    A = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    A[np.diag_indices(n)] = n
+    B = rng.uniform(-1, 1, (n, m)).astype(np.float32)
+    Ad, Bd = torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda()
+    Cd = torch.zeros((n, m), dtype=torch.float32, device="cuda")
+    assert L.gen9blas_symm(1, 0, 0, n, m, d(1.0), p(Ad.data_ptr()), n, p(Bd.data_ptr()), m, d(0.0), p(Cd.data_ptr()), m) == 0
+    torch.cuda.synchronize()
+    Ss = np.tril(f64(A)) + np.tril(f64(A), -1).T
+    _check(Cd.cpu().numpy(), Ss @ f64(B), np.abs(Ss) @ np.abs(f64(B)), (1e-6, 1e-5), tag="symm device")
+    Sd = torch.zeros((n, n), dtype=torch.float32, device="cuda")
+    assert L.gen9blas_syrk(1, 0, 0, n, m, d(1.0), p(Bd.data_ptr()), m, d(0.0), p(Sd.data_ptr()), n) == 0
+    torch.cuda.synchronize()
+    mask = np.tril(np.ones((n, n), bool))
+    _check(Sd.cpu().numpy(), f64(B) @ f64(B).T, np.abs(f64(B)) @ np.abs(f64(B)).T, (1e-6, 1e-5), mask, "syrk device")
+    assert g9.last_zero_copy() == 5
+    Td = Bd.clone()
+    assert L.gen9blas_trmm(1, 0, 1, 0, 0, n, m, d(1.0), p(Ad.data_ptr()), n, p(Td.data_ptr()), m) == 0
+    torch.cuda.synchronize()
+    U = np.triu(f64(A))
+    _check(Td.cpu().numpy(), U @ f64(B), np.abs(U) @ np.abs(f64(B)), (1e-6, 1e-5), tag="trmm device")
+    Xd = Bd.clone()
+    assert L.gen9blas_trsm(1, 0, 1, 0, 0, n, m, d(1.0), p(Ad.data_ptr()), n, p(Xd.data_ptr()), m) == 0
+    torch.cuda.synchronize()
+    Xr = np.linalg.solve(U, f64(B))
+    assert np.abs(Xd.cpu().numpy() - Xr).max() / np.abs(Xr).max() <= 1e-4
