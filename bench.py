@@ -37,8 +37,8 @@ GEMM_CASES = {
     "sgemm_odd_3000x11008x4096_tB_beta05": ("S", None),
 }
 QUICK = ("hgemm_n4096", "hgemm_accurate_n4096", "hbm_read_1GiB", "skinny")
-OTHER_CASES = ("hgemm_n4096_host", "hbm_read_1GiB", "skinny", "saxpy_2^26", "sdot_2^26", "sgemv_16384", "copy_256MiB",
-               "calibration")
+OTHER_CASES = ("hgemm_n4096_host", "hbm_read_1GiB", "skinny", "packed_decode", "level3_n4096", "saxpy_2^26",
+               "sdot_2^26", "sgemv_16384", "copy_256MiB", "calibration")
 
 
 def log(*a):
@@ -204,6 +204,71 @@ def main():
             log("skinny", M, sk[f"M{M}"])
         res["skinny_fp16_4096x4096"] = sk
         del Wd
+
+    # ---------------- packed weights: gemm_pb (M = 1..16) on 32 resident packed copies of a 4096² fp16 W ----------
+    if "packed_decode" in cases:
+        K = N = 4096
+        ncopy = 32
+        packs = []
+        for c in range(ncopy):
+            w = np.random.default_rng(100 + c).standard_normal((K, N), dtype=np.float32) * np.float32(0.02)
+            Wd = to_dev(w.astype(np.float16))   # K×N, packed once (transB = 0) and then released
+            torch.cuda.synchronize()            # the copy ran on torch's stream, pack_b reads on the library's
+            h = L.gen9blas_pack_b(0, 0, K, N, p(Wd.data_ptr()), N)
+            if not h:
+                raise RuntimeError(L.gen9blas_error().decode())
+            packs.append(h)
+            del Wd
+        pk = {}
+        for M in (1, 4, 16):
+            Ad = to_dev(np.random.default_rng(1).standard_normal((M, K), dtype=np.float32).astype(np.float16))
+            Cd = torch.empty((M, N), dtype=torch.float16, device=dev)
+            state = {"j": 0}
+
+            def fn():
+                j = state["j"]
+                state["j"] = (j + 1) % ncopy
+                check(L.gen9blas_gemm_pb(0, M, d(1.0), p(Ad.data_ptr()), K, p(packs[j]), d(0.0), p(Cd.data_ptr()), N))
+            ms = timed(fn, k=max(steps, 32) * 2, w=max(warm, 32))
+            byts = 2.0 * N * K + 2.0 * M * K + 2.0 * M * N
+            pk[f"M{M}"] = hbm_fracs({"us_per_call": round(ms * 1e3, 2), "GBs": round(byts / (ms * 1e-3) / 1e9, 1)})
+            log("packed_decode", M, pk[f"M{M}"])
+        for h in packs:
+            L.gen9blas_packed_b_free(p(h))
+        res["packed_decode_fp16_4096x4096"] = pk
+
+    # ---------------- level 3 beyond GEMM at n = 4096 (useful flops: SYMM 2n³, SYRK n³, SYR2K 2n³, TRMM/TRSM n³) -----
+    if "level3_n4096" in cases:
+        n = 4096
+        l3 = {}
+        for kind, typ, dt in (("S", 1, np.float32), ("D", 3, np.float64)):
+            rng = np.random.default_rng(30)
+            A = rng.uniform(-1, 1, (n, n)) / n
+            A[np.diag_indices(n)] = 1.0            # well-conditioned triangle for TRSM
+            Ad = to_dev(A.astype(dt))
+            Bd = to_dev(rng.uniform(-1, 1, (n, n)).astype(dt))
+            Cd = to_dev(rng.uniform(-1, 1, (n, n)).astype(dt))
+            Xd = torch.empty_like(Bd)
+            a, b, c, x = (p(t.data_ptr()) for t in (Ad, Bd, Cd, Xd))
+            calls = {
+                "symm_LL": (2.0, lambda: check(L.gen9blas_symm(typ, 0, 0, n, n, d(1.0), a, n, b, n, d(0.5), c, n))),
+                "syrk_LN": (1.0, lambda: check(L.gen9blas_syrk(typ, 0, 0, n, n, d(1.0), b, n, d(0.5), c, n))),
+                "syr2k_LN": (2.0, lambda: check(L.gen9blas_syr2k(typ, 0, 0, n, n, d(1.0), a, n, b, n, d(0.5), c, n))),
+                # TRMM/TRSM overwrite their B: a fresh copy first, by the library on its stream (a copy of 64 / 128
+                # MiB, under 1 % of the call, inside the timing)
+                "trmm_LLN": (1.0, lambda: (check(L.gen9blas_copy(typ, n * n, b, 1, x, 1)),
+                                           check(L.gen9blas_trmm(typ, 0, 0, 0, 0, n, n, d(1.0), a, n, x, n)))),
+                "trsm_LLN": (1.0, lambda: (check(L.gen9blas_copy(typ, n * n, b, 1, x, 1)),
+                                           check(L.gen9blas_trsm(typ, 0, 0, 0, 0, n, n, d(1.0), a, n, x, n)))),
+            }
+            for name, (mult, fn) in calls.items():
+                ms = timed(fn, k=max(3, steps // 4), w=1)
+                tf = mult * n ** 3 / (ms * 1e-3) / 1e12
+                l3[f"{kind.lower()}{name}"] = {"ms": round(ms, 3), "tflops": round(tf, 2),
+                                               "frac_of_peak": round(tf / PEAK_TFLOPS[kind], 4)}
+                log("level3", kind, name, l3[f"{kind.lower()}{name}"])
+            del Ad, Bd, Cd, Xd
+        res["level3_n4096"] = l3
 
     # ---------------- level 1/2 ----------------
     n = 1 << 26

@@ -3,8 +3,9 @@
 Checks the reference BLAS layer's contract (reference: lib/src/cblas.c:1-562, lib/test_blas.py, lib/test_blas_d.py)
 on the CPU side: the library loads and finds a CPU BLAS, it exports its own S/D entry points plus a forwarding stub
 for every other BLAS/CBLAS symbol of that CPU BLAS, row- and column-major CBLAS calls and Fortran calls give the
-float64 closed-form results (bounds 1e-5 FP32 / 1e-12 FP64 as in the reference's tests), and forwarded functions
-(here ssymm, dsymm) work. Without a device the routing sends everything to the CPU, so these run anywhere.
+float64 closed-form results (bounds 1e-5 FP32 / 1e-12 FP64 as in the reference's tests), the level-3 functions the
+shim routes itself (SYMM, SYRK, SYR2K, TRMM, TRSM) pass every option through, and forwarded functions (here ssymv,
+dsymv) work. Without a device the routing sends everything to the CPU, so these run anywhere.
 """
 import ctypes
 import os
@@ -111,12 +112,34 @@ def test_mixed_precision_dots(L):
 
 
 @pytest.mark.parametrize("P", ["s", "d"])
-def test_forwarded_symm(L, P):
+def test_forwarded_symv(L, P):
     """A function the shim forwards to the CPU BLAS by a tail jump (not routed): results as BLAS."""
     dt = DT[P]
     A = rng.uniform(-1, 1, (30, 30)).astype(dt)
     S = np.tril(A) + np.tril(A, -1).T            # the lower triangle defines the symmetric matrix
-    B = rng.uniform(-1, 1, (30, 20)).astype(dt)
-    C = np.zeros((30, 20), dt)
-    getattr(L, f"cblas_{P}symm")(U.ROW, 141, 122, 30, 20, 1.0, U.ptr(A), 30, U.ptr(B), 20, 0.0, U.ptr(C), 20)
-    assert U.ref_error(C, S.astype(np.float64) @ B, np.abs(S.astype(np.float64)) @ np.abs(B)) <= TOL[P]
+    x, y = rng.uniform(-1, 1, 30).astype(dt), np.zeros(30, dt)
+    getattr(L, f"cblas_{P}symv")(U.ROW, 122, 30, 1.0, U.ptr(A), 30, U.ptr(x), 1, 0.0, U.ptr(y), 1)
+    S64 = S.astype(np.float64)
+    assert U.ref_error(y, S64 @ x, np.abs(S64) @ np.abs(x)) <= TOL[P]
+
+
+@pytest.mark.parametrize("P", ["s", "d"])
+@pytest.mark.parametrize("op", U.L3)
+def test_level3_routed_functions_on_cpu(L, P, op):
+    """SYMM/SYRK/SYR2K/TRMM/TRSM through the shim's own entry points (CBLAS row- and column-major, Fortran), every
+    side / triangle / transpose / diagonal: without a device they reach the CPU BLAS with arguments intact."""
+    dt = DT[P]
+    dims = (23, 31) if op in ("syrk", "syr2k") else (29, 19)
+    for opt in U.L3_OPTS[op]:
+        for order in (U.ROW, U.COL, "F"):
+            A, B, C0 = U.l3_case(rng, dt, op, opt, dims)
+            a, b = U.to_mem(A, order), U.to_mem(B, order)
+            c = U.to_mem(C0, order)
+            tgt = c if op in ("symm", "syrk", "syr2k") else b
+            U.call_l3(L, P, order, op, opt, dims, 0.75, -0.5, a[:2], b[:2], c[:2])
+            got = tgt[2](tgt[0])
+            ref, scale, mask = U.l3_ref(op, opt, 0.75, -0.5, A, B, C0)
+            tol = U.L3_TRSM_TOL[P] if op == "trsm" else U.L3_TOL[P]
+            assert U.l3_error(op, got, ref, scale, mask) <= tol, (opt, order)
+            if mask is not None:
+                assert np.array_equal(got[~mask], C0.astype(np.float64)[~mask]), (opt, order)

@@ -105,3 +105,53 @@ def test_mixed_dots_fp64_on_device(L, capfd, torch_dev):
     got = L.cblas_sdsdot(v.size, 0.25, U.ptr(vd), 1, U.ptr(wd), 1)   # FP64 sum, one rounding to float
     assert abs(got - (0.25 + exact)) <= 6e-8 * abs(0.25 + exact)
     assert routes(capfd) == ["GPU", "GPU"]
+
+
+L3_BIG = {"symm": (800, 800), "syrk": (800, 1600), "syr2k": (800, 800), "trmm": (1000, 1000), "trsm": (1000, 1000)}
+
+
+def _l3_run(L, P, op, opt, order, dims, torch=None):
+    """One level-3 call through the shim on fresh random operands; returns the error against the float64 closed form
+    and whether the entries outside the defined triangle stayed as they were."""
+    dt = DT[P]
+    A, B, C0 = U.l3_case(rng, dt, op, opt, dims)
+    a, b, c = (U.to_mem(X, order, torch) for X in (A, B, C0))
+    U.call_l3(L, P, order, op, opt, dims, 0.75, -0.5, a[:2], b[:2], c[:2])
+    if torch is not None:
+        torch.cuda.synchronize()
+    tgt = c if op in ("symm", "syrk", "syr2k") else b
+    got = tgt[2](tgt[0])
+    ref, scale, mask = U.l3_ref(op, opt, 0.75, -0.5, A, B, C0)
+    kept = mask is None or np.array_equal(got[~mask], C0.astype(np.float64)[~mask])
+    return U.l3_error(op, got, ref, scale, mask), kept
+
+
+@pytest.mark.parametrize("P", ["s", "d"])
+@pytest.mark.parametrize("op", U.L3)
+def test_level3_host_routes_by_size(L, capfd, P, op):
+    """Host-memory SYMM/SYRK/SYR2K/TRMM/TRSM: the GPU from 1e9 flops, the CPU BLAS below; CBLAS both orders and
+    Fortran give BLAS results either way."""
+    tol = U.L3_TRSM_TOL[P] if op == "trsm" else U.L3_TOL[P]
+    opt = U.L3_OPTS[op][-1]
+    big = L3_BIG[op]
+    for dims, side in ((big, "GPU"), ((big[0] // 4, big[1] // 4), "CPU")):
+        for order in (U.ROW, U.COL, "F"):
+            capfd.readouterr()
+            err, kept = _l3_run(L, P, op, opt, order, dims)
+            assert routes(capfd) == [side], (dims, order)
+            assert err <= tol and kept, (dims, order, err)
+
+
+@pytest.mark.parametrize("P", ["s", "d"])
+@pytest.mark.parametrize("op", U.L3)
+def test_level3_device_operands_every_option(L, capfd, torch_dev, P, op):
+    """Device operands go to the GPU at any size over 2^16 elements: every side / triangle / transpose / diagonal in
+    CBLAS row- and column-major and Fortran, i.e. every mapping of a column-major call onto the row-major library."""
+    tol = U.L3_TRSM_TOL[P] if op == "trsm" else U.L3_TOL[P]
+    dims = (280, 200) if op in ("syrk", "syr2k") else (300, 260)
+    for opt in U.L3_OPTS[op]:
+        for order in (U.ROW, U.COL, "F"):
+            capfd.readouterr()
+            err, kept = _l3_run(L, P, op, opt, order, dims, torch_dev)
+            assert routes(capfd) == ["GPU"], (opt, order)
+            assert err <= tol and kept, (opt, order, err)
