@@ -1,0 +1,700 @@
+// Level-2 routines on symmetric, triangular, banded and packed matrices: SYMV, TRMV, TRSV, SYR, SYR2 (full storage)
+// and GBMV, SBMV, TBMV, TBSV, SPMV, TPMV, TPSV, SPR, SPR2 (reference: lib/src/level12.c:267-519, arithmetic of
+// lib/kernels/level12.cl:424-640).
+//
+// One storage model covers every layout: element (i, j) sits at a[rs(i) + j] for j in the stored range
+// [lo(i), hi(i)] of row i.
+//   full storage, row stride ld:   rs(i) = i·ld                  range [0, ncols), cut to j ≤ i (lower) or j ≥ i (upper)
+//   band, KL below / KU above:     rs(i) = i·(ld − 1) + KL       range [i − KL, i + KU] ∩ [0, ncols)
+//   packed upper, order n:         rs(i) = i·n − i(i − 1)/2 − i  range [i, n)
+//   packed lower:                  rs(i) = i(i + 1)/2            range [0, i]
+// A unit diagonal takes j = i out of the range (the stored diagonal is not read).
+//
+// Products y = alpha·op(A)·x + beta·y make one pass over the stored elements. A wave owns a group of 64·V columns
+// (V elements of 16 bytes per lane for aligned full storage, one element per lane otherwise) and a band of rows.
+// Each element read adds a·x_j to its row sum (op(A) = A) and/or a·x_i to its column sum (op(A) = Aᵀ, and the
+// mirrored half of a symmetric matrix), so a symmetric matrix is read once, from its stored triangle. Row sums are
+// reduced across the wave (transposing butterfly) into one FP32 (FP64) partial per row and column group, column sums
+// stay in registers into one partial per column and row band; a second kernel adds the partials of each output in a
+// fixed order and applies alpha / beta once, so results do not depend on scheduling. FP16 is computed in FP32 as in
+// the reference (level12.cl:1-3).
+//
+// Triangular solves run over diagonal blocks of 128 rows: one workgroup loads the block of op(A) into LDS and one
+// wave substitutes (lanes own rows, the solved value of each step is broadcast from its lane), then the rows after
+// the block are updated in parallel, two launches per block as in the reference (level12.c:303-347). The work
+// vector is FP32 (FP64 for FP64), also for FP16 (level12.c:301).
+#include "internal.h"
+#include "wave.h"
+#include <type_traits>
+
+namespace g9 {
+namespace l2 {
+
+typedef long long ll;
+typedef _Float16 f16;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+template <class T> struct Comp { using R = float; };
+template <> struct Comp<double> { using R = double; };
+template <class T> constexpr int VW = 16 / (int)sizeof(T);
+template <class T> union Vec {
+    u32x4 u;
+    T e[VW<T>];
+};
+__device__ __forceinline__ float fma_r(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+__device__ __forceinline__ double fma_r(double a, double b, double c) { return __builtin_fma(a, b, c); }
+
+enum { F_FULL = 0, F_BAND, F_PACKU, F_PACKL };
+enum { TRI_NONE = 0, TRI_LOWER = 1, TRI_UPPER = 2 };
+enum { DIR_ROW = 1, DIR_COL = 2 };
+
+struct Shape {
+    ll ld;              // row stride (full, band)
+    int KL, KU;         // band widths below / above the diagonal
+    int n;              // order of a packed matrix
+    int nrows, ncols;
+    int tri;            // TRI_*: the stored triangle
+    int unit;           // unit diagonal: j = i not stored
+};
+
+template <int FMT> __device__ __forceinline__ ll row_start(const Shape &s, int i) {
+    if constexpr (FMT == F_FULL) return (ll)i * s.ld;
+    else if constexpr (FMT == F_BAND) return (ll)i * (s.ld - 1) + s.KL;
+    else if constexpr (FMT == F_PACKU) return (ll)i * s.n - (ll)i * (i - 1) / 2 - i;
+    else return (ll)i * (i + 1) / 2;
+}
+__device__ __forceinline__ void stored_range(const Shape &s, bool band, int i, int &lo, int &hi) {
+    lo = 0;
+    hi = s.ncols - 1;
+    if (band) {
+        lo = max(lo, i - s.KL);
+        hi = min(hi, i + s.KU);
+    }
+    if (s.tri == TRI_LOWER) hi = min(hi, i - s.unit);
+    else if (s.tri == TRI_UPPER) lo = max(lo, i + s.unit);
+}
+
+// ---------------- products ----------------
+constexpr int NT = 256;
+constexpr int U = 8;   // rows per batch: their loads are all issued before the first product
+template <class T, int V, int FMT>
+__global__ void __launch_bounds__(NT) mv_kernel(Shape s, const T *__restrict__ a, const T *x, ll ix, int rpp, int dirs,
+                                                int skipdiag, typename Comp<T>::R *P, typename Comp<T>::R *Q) {
+    using R = typename Comp<T>::R;
+    constexpr bool band = FMT == F_BAND;
+    const int lane = threadIdx.x & 63;
+    const int g = blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
+    if ((ll)g * 64 * V >= s.ncols) return;
+    const int g0 = g * 64 * V, g1 = min(g0 + 64 * V, s.ncols) - 1, c0 = g0 + lane * V;
+    // rows whose stored range can reach the group's columns, within this row band
+    int rb = blockIdx.y * rpp, re = min(s.nrows, rb + rpp);
+    if (s.tri == TRI_LOWER) rb = max(rb, g0);
+    if (s.tri == TRI_UPPER) re = min(re, g1 + 1);
+    if (band) {
+        rb = max(rb, g0 - s.KU);
+        re = min(re, g1 + s.KL + 1);
+    }
+    R xc[V], sc[V];
+#pragma unroll
+    for (int e = 0; e < V; e++) {
+        xc[e] = (dirs & DIR_ROW) && c0 + e < s.ncols ? (R)x[(ll)(c0 + e) * ix] : R(0);
+        sc[e] = 0;
+    }
+    for (int i = rb; i < re; i += U) {
+        R av[U][V];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int r = i + u;
+            int lo, hi;
+            stored_range(s, band, r, lo, hi);
+            if (r >= re) hi = lo - 1;
+            const T *ar = a + row_start<FMT>(s, r);
+            if constexpr (V > 1) {
+                if (c0 >= lo && c0 + V - 1 <= hi) {
+                    Vec<T> v;
+                    v.u = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(ar + c0));
+#pragma unroll
+                    for (int e = 0; e < V; e++) av[u][e] = (R)v.e[e];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < V; e++) av[u][e] = c0 + e >= lo && c0 + e <= hi ? (R)ar[c0 + e] : R(0);
+                }
+            } else {
+                av[u][0] = c0 >= lo && c0 <= hi ? (R)ar[c0] : R(0);
+            }
+        }
+        if (dirs & DIR_COL) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                if (i + u >= re) break;
+                const R xr = (R)x[(ll)(i + u) * ix];
+#pragma unroll
+                for (int e = 0; e < V; e++)
+                    if (!skipdiag || c0 + e != i + u) sc[e] = fma_r(av[u][e], xr, sc[e]);
+            }
+        }
+        if (dirs & DIR_ROW) {
+            R rs[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                R t = 0;
+#pragma unroll
+                for (int e = 0; e < V; e++) t = fma_r(av[u][e], xc[e], t);
+                rs[u] = t;
+            }
+            int base = 0;
+            butterfly<0, U>(rs, lane, base);
+            if ((lane & (64 / U - 1)) == 0 && i + base < re) Q[(ll)g * s.nrows + i + base] = rs[0];
+        }
+    }
+    if (dirs & DIR_COL) {
+#pragma unroll
+        for (int e = 0; e < V; e++)
+            if (c0 + e < s.ncols) P[(ll)blockIdx.y * s.ncols + c0 + e] = sc[e];
+    }
+}
+
+// y_k = alpha·(Σ_band P[band][k] + Σ_group Q[group][k] (+ x_k for a unit diagonal)) + beta·y_k, partials in index
+// order; y is not read when beta = 0 (reference: level12.cl:280).
+template <class T>
+__global__ void __launch_bounds__(NT) mv_finish(Shape s, int band, int ny, int dirs, int parts, int gw,
+                                                const typename Comp<T>::R *P, const typename Comp<T>::R *Q,
+                                                typename Comp<T>::R alpha, typename Comp<T>::R beta, const T *x, ll ix,
+                                                int add_x, T *y, ll iy) {
+    using R = typename Comp<T>::R;
+    const int k = blockIdx.x * NT + threadIdx.x;
+    if (k >= ny) return;
+    R t = 0;
+    if (dirs & DIR_COL)
+        for (int p = 0; p < parts; p++) t += P[(ll)p * ny + k];
+    if (dirs & DIR_ROW) {
+        int lo, hi;
+        stored_range(s, band, k, lo, hi);
+        if (lo <= hi)
+            for (int g = lo / gw; g <= hi / gw; g++) t += Q[(ll)g * ny + k];
+    }
+    if (add_x) t += (R)x[(ll)k * ix];
+    T *yp = y + (ll)k * iy;
+    *yp = (T)(beta == R(0) ? alpha * t : fma_r(alpha, t, beta * (R)*yp));
+}
+
+// ---------------- rank-1 / rank-2 updates of the stored elements ----------------
+// A = alpha·x·yᵀ + A (SYR, SPR: y = x) or alpha·(x·yᵀ + y·xᵀ) + A (SYR2, SPR2) on the stored triangle
+// (reference: level12.cl:466-476, 622-630: fma(alpha·x_i, y_j, a), then fma(alpha·y_i, x_j, ·)).
+template <class T, int FMT>
+__global__ void __launch_bounds__(NT) rank_kernel(Shape s, typename Comp<T>::R alpha, const T *x, ll ix, const T *y,
+                                                  ll iy, int two, T *a) {
+    using R = typename Comp<T>::R;
+    for (int i = blockIdx.y; i < s.nrows; i += gridDim.y) {
+        int lo, hi;
+        stored_range(s, FMT == F_BAND, i, lo, hi);
+        const R xi = alpha * (R)x[(ll)i * ix];
+        const R yi = two ? alpha * (R)y[(ll)i * iy] : R(0);
+        T *ar = a + row_start<FMT>(s, i);
+        for (int j = lo + blockIdx.x * NT + threadIdx.x; j <= hi; j += gridDim.x * NT) {
+            R v = fma_r(xi, (R)y[(ll)j * iy], (R)ar[j]);
+            if (two) v = fma_r(yi, (R)x[(ll)j * ix], v);
+            ar[j] = (T)v;
+        }
+    }
+}
+
+// ---------------- triangular solves ----------------
+constexpr int SB = 128;   // rows per diagonal block
+template <class T, class R>
+__global__ void __launch_bounds__(NT) to_work(int n, const T *x, ll ix, R *xf) {
+    const int i = blockIdx.x * NT + threadIdx.x;
+    if (i < n) xf[i] = (R)x[(ll)i * ix];
+}
+template <class T, class R>
+__global__ void __launch_bounds__(NT) from_work(int n, const R *xf, T *x, ll ix) {
+    const int i = blockIdx.x * NT + threadIdx.x;
+    if (i < n) x[(ll)i * ix] = (T)xf[i];
+}
+
+__device__ __forceinline__ float lane_value(float v, int k) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), k));
+}
+__device__ __forceinline__ double lane_value(double v, int k) {
+    const long long b = __builtin_bit_cast(long long, v);
+    const int lo = __builtin_amdgcn_readlane((int)b, k), hi = __builtin_amdgcn_readlane((int)(b >> 32), k);
+    return __builtin_bit_cast(double, (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+
+// Diagonal block [p, p + b) of op(A), b ≤ SB: op(A)(p + r, p + c) goes to Lt[c'][r'] (column-major, padded rows
+// against bank conflicts), with r' = r, c' = c for forward substitution (op(A) lower) and both reversed for backward
+// substitution, so the solve below is always forward. The block is read in memory order: along rows of A.
+template <class T, int FMT>
+__global__ void __launch_bounds__(NT) solve_block(Shape s, const T *__restrict__ a, int trans, int fwd, int p, int b,
+                                                  typename Comp<T>::R *xf) {
+    using R = typename Comp<T>::R;
+    __shared__ R Lt[SB][SB + 1];
+    for (int e = threadIdx.x; e < b * b; e += NT) {
+        const int q = e / b, w = e % b;
+        // (i, j): element of A, w runs along its row; (r, c): the same element in op(A)
+        const int i = p + q, j = p + w, r = trans ? w : q, c = trans ? q : w;
+        int lo, hi;
+        stored_range(s, FMT == F_BAND, i, lo, hi);
+        const R v = j >= lo && j <= hi ? (R)a[row_start<FMT>(s, i) + j] : R(0);
+        Lt[fwd ? c : b - 1 - c][fwd ? r : b - 1 - r] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x >= 64) return;
+    const int l = threadIdx.x;
+    const auto idx = [&](int r) { return p + (fwd ? r : b - 1 - r); };
+    R v0 = l < b ? xf[idx(l)] : R(0), v1 = l + 64 < b ? xf[idx(l + 64)] : R(0);
+    for (int k = 0; k < b; k++) {
+        R xk = k < 64 ? lane_value(v0, k) : lane_value(v1, k - 64);
+        if (!s.unit) xk = xk / Lt[k][k];
+        if (l == k) v0 = xk;
+        else if (l > k) v0 = fma_r(-Lt[k][l], xk, v0);
+        if (l + 64 == k) v1 = xk;
+        else if (l + 64 > k && l + 64 < b) v1 = fma_r(-Lt[k][l + 64], xk, v1);
+    }
+    if (l < b) xf[idx(l)] = v0;
+    if (l + 64 < b) xf[idx(l + 64)] = v1;
+}
+
+// x_r -= Σ_{c in [p, p+b)} A(r, c)·x_c for r in [r0, r1) (op(A) = A): a wave takes 8 rows, its lanes the block's
+// columns (b ≤ 128: two per lane), then the butterfly sums the 8 rows.
+template <class T, int FMT>
+__global__ void __launch_bounds__(NT) update_rows(Shape s, const T *__restrict__ a, int p, int b, int r0, int r1,
+                                                  typename Comp<T>::R *xf) {
+    using R = typename Comp<T>::R;
+    constexpr int RW = 8;
+    const int lane = threadIdx.x & 63;
+    const int rbase = r0 + (blockIdx.x * (NT / 64) + (threadIdx.x >> 6)) * RW;
+    if (rbase >= r1) return;
+    const int ca = p + lane, cb = p + 64 + lane;
+    const R x0 = lane < b ? xf[ca] : R(0), x1 = lane + 64 < b ? xf[cb] : R(0);
+    R t[RW];
+#pragma unroll
+    for (int u = 0; u < RW; u++) {
+        const int r = rbase + u;
+        int lo, hi;
+        stored_range(s, FMT == F_BAND, r, lo, hi);
+        if (r >= r1) hi = lo - 1;
+        const T *ar = a + row_start<FMT>(s, r);
+        const R e0 = lane < b && ca >= lo && ca <= hi ? (R)ar[ca] : R(0);
+        const R e1 = lane + 64 < b && cb >= lo && cb <= hi ? (R)ar[cb] : R(0);
+        t[u] = fma_r(e1, x1, e0 * x0);
+    }
+    int base = 0;
+    butterfly<0, RW>(t, lane, base);
+    if ((lane & (64 / RW - 1)) == 0 && rbase + base < r1) xf[rbase + base] -= t[0];
+}
+
+// x_r -= Σ_{c in [p, p+b)} A(c, r)·x_c for r in [r0, r1) (op(A) = Aᵀ): a thread per r, rows c of A in order
+// (neighbouring threads read neighbouring elements of a row).
+template <class T, int FMT>
+__global__ void __launch_bounds__(NT) update_cols(Shape s, const T *__restrict__ a, int p, int b, int r0, int r1,
+                                                  typename Comp<T>::R *xf) {
+    using R = typename Comp<T>::R;
+    const int r = r0 + blockIdx.x * NT + threadIdx.x;
+    if (r >= r1) return;
+    R t = 0;
+    for (int c = p; c < p + b; c++) {
+        int lo, hi;
+        stored_range(s, FMT == F_BAND, c, lo, hi);
+        if (r >= lo && r <= hi) t = fma_r((R)a[row_start<FMT>(s, c) + r], xf[c], t);
+    }
+    xf[r] -= t;
+}
+
+// ---------------- launchers ----------------
+template <class F> static int by_type(int es, F f) {
+    if (es == 2) return f((f16 *)nullptr);
+    if (es == 4) return f((float *)nullptr);
+    return f((double *)nullptr);
+}
+template <class F> static int by_fmt(int fmt, F f) {
+    if (fmt == F_FULL) return f(std::integral_constant<int, F_FULL>());
+    if (fmt == F_BAND) return f(std::integral_constant<int, F_BAND>());
+    if (fmt == F_PACKU) return f(std::integral_constant<int, F_PACKU>());
+    return f(std::integral_constant<int, F_PACKL>());
+}
+static unsigned blocks(ll n, int per) { return (unsigned)((n + per - 1) / per); }
+
+// y = alpha·(sums over the stored elements in the directions `dirs`) + beta·y (+ x for add_x); ny outputs.
+static int launch_mv(int es, int fmt, const Shape &s, const void *a, const void *x, ll ix, int dirs, int skipdiag,
+                     double alpha, double beta, int add_x, void *y, ll iy, int ny) {
+    return by_type(es, [&](auto *tag) -> int {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        using R = typename Comp<T>::R;
+        const bool vec = fmt == F_FULL && (uintptr_t)a % 16 == 0 && (s.ld * (ll)sizeof(T)) % 16 == 0;
+        const int V = vec ? VW<T> : 1, gw = 64 * V;
+        const ll groups = (s.ncols + gw - 1) / gw;
+        const unsigned gx = blocks(groups, NT / 64);
+        // about 4 blocks per CU over the row bands (half of them idle on a triangle)
+        const int cus = num_cus > 0 ? num_cus : 256;
+        ll parts = (4LL * cus + gx - 1) / gx;
+        const ll maxparts = (s.nrows + U - 1) / U;
+        if (parts > maxparts) parts = maxparts;
+        if (parts < 1) parts = 1;
+        if (parts > 65535) parts = 65535;
+        ll rpp = (s.nrows + parts - 1) / parts;
+        rpp = (rpp + U - 1) / U * U;
+        parts = (s.nrows + rpp - 1) / rpp;
+        void *pp = nullptr, *qq = nullptr;
+        if (dirs & DIR_COL) G9_TRY(scratch(SLOT_P, (size_t)parts * s.ncols * sizeof(R), &pp));
+        if (dirs & DIR_ROW) G9_TRY(scratch(SLOT_Q, (size_t)groups * s.nrows * sizeof(R), &qq));
+        R *P = (R *)pp, *Q = (R *)qq;
+        const T *ap = (const T *)a, *xp = (const T *)x;
+        const dim3 grid(gx, (unsigned)parts);
+        G9_TRY(by_fmt(fmt, [&](auto fc) -> int {
+            constexpr int FMT = decltype(fc)::value;
+            if constexpr (FMT == F_FULL) {
+                if (vec) {
+                    hipLaunchKernelGGL((mv_kernel<T, VW<T>, FMT>), grid, dim3(NT), 0, stream, s, ap, xp, ix, (int)rpp, dirs,
+                                       skipdiag, P, Q);
+                    return 0;
+                }
+            }
+            hipLaunchKernelGGL((mv_kernel<T, 1, FMT>), grid, dim3(NT), 0, stream, s, ap, xp, ix, (int)rpp, dirs, skipdiag,
+                               P, Q);
+            return 0;
+        }));
+        G9_HIP(hipGetLastError());
+        hipLaunchKernelGGL((mv_finish<T>), dim3(blocks(ny, NT)), dim3(NT), 0, stream, s, (int)(fmt == F_BAND), ny, dirs,
+                           (int)parts, gw, (const R *)P, (const R *)Q, (R)alpha, (R)beta, xp, ix, add_x, (T *)y, iy);
+        G9_HIP(hipGetLastError());
+        return 0;
+    });
+}
+
+static int launch_rank(int es, int fmt, const Shape &s, double alpha, const void *x, ll ix, const void *y, ll iy, int two,
+                       void *a) {
+    return by_type(es, [&](auto *tag) -> int {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        using R = typename Comp<T>::R;
+        const dim3 grid(blocks(s.ncols, NT) < 8 ? blocks(s.ncols, NT) : 8, s.nrows < 65535 ? (unsigned)s.nrows : 65535u);
+        G9_TRY(by_fmt(fmt, [&](auto fc) -> int {
+            constexpr int FMT = decltype(fc)::value;
+            hipLaunchKernelGGL((rank_kernel<T, FMT>), grid, dim3(NT), 0, stream, s, (R)alpha, (const T *)x, ix, (const T *)y,
+                               iy, two, (T *)a);
+            return 0;
+        }));
+        G9_HIP(hipGetLastError());
+        return 0;
+    });
+}
+
+// Solves op(A)·z = x in place. `lower`: op(A) is lower triangular (forward substitution); kb: rows below (forward)
+// or above (backward) a block that op(A) can reach, n for full and packed storage, the band width for a band.
+static int launch_solve(int es, int fmt, const Shape &s, const void *a, int trans, int lower, int kb, void *x, ll ix) {
+    return by_type(es, [&](auto *tag) -> int {
+        using T = std::remove_pointer_t<decltype(tag)>;
+        using R = typename Comp<T>::R;
+        const int n = s.nrows;
+        void *wp;
+        G9_TRY(scratch(SLOT_T, (size_t)n * sizeof(R), &wp));
+        R *xf = (R *)wp;
+        hipLaunchKernelGGL((to_work<T, R>), dim3(blocks(n, NT)), dim3(NT), 0, stream, n, (const T *)x, ix, xf);
+        G9_HIP(hipGetLastError());
+        const int nb = (n + SB - 1) / SB;
+        G9_TRY(by_fmt(fmt, [&](auto fc) -> int {
+            constexpr int FMT = decltype(fc)::value;
+            for (int q = 0; q < nb; q++) {
+                const int p = (lower ? q : nb - 1 - q) * SB, b = n - p < SB ? n - p : SB;
+                hipLaunchKernelGGL((solve_block<T, FMT>), dim3(1), dim3(NT), 0, stream, s, (const T *)a, trans, lower, p, b, xf);
+                G9_HIP(hipGetLastError());
+                int r0, r1;
+                if (lower) {
+                    r0 = p + b;
+                    r1 = (ll)p + b + kb < n ? p + b + kb : n;
+                } else {
+                    r0 = p - kb > 0 ? p - kb : 0;
+                    r1 = p;
+                }
+                if (r1 <= r0) continue;
+                if (trans)
+                    hipLaunchKernelGGL((update_cols<T, FMT>), dim3(blocks(r1 - r0, NT)), dim3(NT), 0, stream, s, (const T *)a,
+                                       p, b, r0, r1, xf);
+                else
+                    hipLaunchKernelGGL((update_rows<T, FMT>), dim3(blocks(r1 - r0, 8 * (NT / 64))), dim3(NT), 0, stream, s,
+                                       (const T *)a, p, b, r0, r1, xf);
+                G9_HIP(hipGetLastError());
+            }
+            return 0;
+        }));
+        hipLaunchKernelGGL((from_work<T, R>), dim3(blocks(n, NT)), dim3(NT), 0, stream, n, (const R *)xf, (T *)x, ix);
+        G9_HIP(hipGetLastError());
+        return 0;
+    });
+}
+
+// ---------------- entry-point helpers ----------------
+static int l2_es(int type, int *es) {
+    G9_TRY(begin());
+    if (type == GEN9BLAS_H || type == GEN9BLAS_HS) *es = 2;
+    else if (type == GEN9BLAS_S) *es = 4;
+    else if (type == GEN9BLAS_D) *es = 8;
+    else G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "type %d unavailable", type);
+    return 0;
+}
+static void vec(Operand &o, const void *p, int n, int inc, int es) {
+    o.host = p;
+    o.es = es;
+    o.rows = 1;
+    o.cols = (ll)(n - 1) * (inc < 0 ? -(ll)inc : inc) + 1;
+    o.caller_ld = o.cols;
+}
+static void mat(Operand &o, const void *p, int rows, int cols, int ld, int es) {
+    o.host = p;
+    o.es = es;
+    o.rows = rows;
+    o.cols = cols;
+    o.caller_ld = ld;
+}
+static ll voff(int n, int inc) { return inc < 0 ? (ll)(n - 1) * -(ll)inc : 0; }
+static ll packed_len(int n) { return (ll)n * (n + 1) / 2; }
+static int tri_of(int uplo) { return uplo == GEN9BLAS_UPPER ? TRI_UPPER : TRI_LOWER; }
+
+#define L2_BEGIN(n, bad_inc)                                                          \
+    const double t0_ = now_s();                                                       \
+    int es;                                                                           \
+    G9_TRY(l2_es(type, &es));                                                         \
+    if ((n) <= 0) return 0;                                                           \
+    if (bad_inc) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "vector increment 0");
+
+// y = alpha·op(A)·x + beta·y with the matrix operand already described in `oa` (resolved here).
+static int product_y(double t0, int es, int fmt, Shape s, Operand &oa, bool repitch, int dirs, int skipdiag, double alpha,
+                     const void *x, int incx, int nx, double beta, void *y, int incy, int ny) {
+    Operand o[3];
+    o[0] = oa;
+    vec(o[1], x, nx, incx, es);
+    vec(o[2], y, ny, incy, es);
+    G9_TRY(resolve(o[0], SLOT_A, true, false, repitch));
+    G9_TRY(resolve(o[1], SLOT_B, true, false, false));
+    G9_TRY(resolve(o[2], SLOT_C, beta != 0.0 || (incy != 1 && incy != -1), true, false));
+    s.ld = o[0].ld;
+    prof_begin();
+    G9_TRY(launch_mv(es, fmt, s, o[0].dev, (const char *)o[1].dev + voff(nx, incx) * es, incx, dirs, skipdiag, alpha, beta,
+                     0, (char *)o[2].dev + voff(ny, incy) * es, incy, ny));
+    prof_end();
+    G9_TRY(finish(o, 3));
+    prof_collect(t0);
+    return 0;
+}
+
+// x = op(A)·x (triangular): the product goes through the partial buffers, so x may be overwritten by the finish.
+static int product_x(double t0, int es, int fmt, Shape s, Operand &oa, bool repitch, int trans, void *x, int incx, int n) {
+    Operand o[2];
+    o[0] = oa;
+    vec(o[1], x, n, incx, es);
+    G9_TRY(resolve(o[0], SLOT_A, true, false, repitch));
+    G9_TRY(resolve(o[1], SLOT_B, true, true, false));
+    s.ld = o[0].ld;
+    char *xd = (char *)o[1].dev + voff(n, incx) * es;
+    prof_begin();
+    G9_TRY(launch_mv(es, fmt, s, o[0].dev, xd, incx, trans ? DIR_COL : DIR_ROW, 0, 1.0, 0.0, s.unit, xd, incx, n));
+    prof_end();
+    G9_TRY(finish(o, 2));
+    prof_collect(t0);
+    return 0;
+}
+
+static int solve_x(double t0, int es, int fmt, Shape s, Operand &oa, bool repitch, int trans, int kb, void *x, int incx,
+                   int n) {
+    Operand o[2];
+    o[0] = oa;
+    vec(o[1], x, n, incx, es);
+    G9_TRY(resolve(o[0], SLOT_A, true, false, repitch));
+    G9_TRY(resolve(o[1], SLOT_B, true, true, false));
+    s.ld = o[0].ld;
+    const int lower = (s.tri == TRI_LOWER) != (trans != 0);
+    prof_begin();
+    G9_TRY(launch_solve(es, fmt, s, o[0].dev, trans != 0, lower, kb, (char *)o[1].dev + voff(n, incx) * es, incx));
+    prof_end();
+    G9_TRY(finish(o, 2));
+    prof_collect(t0);
+    return 0;
+}
+
+static int rank_update(double t0, int es, int fmt, Shape s, Operand &oa, double alpha, const void *x, int incx,
+                       const void *y, int incy, int n) {
+    const int two = y != nullptr;
+    Operand o[3];
+    o[0] = oa;
+    vec(o[1], x, n, incx, es);
+    if (two) vec(o[2], y, n, incy, es);
+    G9_TRY(resolve(o[0], SLOT_A, true, true, fmt == F_FULL));
+    G9_TRY(resolve(o[1], SLOT_B, true, false, false));
+    if (two) G9_TRY(resolve(o[2], SLOT_C, true, false, false));
+    s.ld = o[0].ld;
+    const char *xd = (const char *)o[1].dev + voff(n, incx) * es;
+    const char *yd = two ? (const char *)o[2].dev + voff(n, incy) * es : xd;
+    prof_begin();
+    G9_TRY(launch_rank(es, fmt, s, alpha, xd, incx, yd, two ? incy : incx, two, o[0].dev));
+    prof_end();
+    G9_TRY(finish(o, two ? 3 : 2));
+    prof_collect(t0);
+    return 0;
+}
+
+static Shape full_shape(int n, int tri, int unit) {
+    Shape s{};
+    s.nrows = s.ncols = s.n = n;
+    s.tri = tri;
+    s.unit = unit;
+    return s;
+}
+static Shape band_shape(int rows, int cols, int KL, int KU, int tri, int unit) {
+    Shape s{};
+    s.nrows = rows;
+    s.ncols = s.n = cols;
+    s.KL = KL;
+    s.KU = KU;
+    s.tri = tri;
+    s.unit = unit;
+    return s;
+}
+
+}  // namespace l2
+}  // namespace g9
+
+using namespace g9;
+using namespace g9::l2;
+
+extern "C" {
+
+// ---- full storage (reference: lib/src/level12.c:267-370) ----
+int gen9blas_symv(int type, int uplo, int n, double alpha, const void *A, int lda, const void *x, int incx, double beta,
+                  void *y, int incy) {
+    L2_BEGIN(n, !incx || !incy);
+    if (lda < n) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "lda < n");
+    Operand oa;
+    mat(oa, A, n, n, lda, es);
+    return product_y(t0_, es, F_FULL, full_shape(n, tri_of(uplo), 0), oa, true, DIR_ROW | DIR_COL, 1, alpha, x, incx, n,
+                     beta, y, incy, n);
+}
+
+int gen9blas_trmv(int type, int uplo, int trans, int diag, int n, const void *A, int lda, void *x, int incx) {
+    L2_BEGIN(n, !incx);
+    if (lda < n) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "lda < n");
+    Operand oa;
+    mat(oa, A, n, n, lda, es);
+    return product_x(t0_, es, F_FULL, full_shape(n, tri_of(uplo), diag != 0), oa, true, trans != 0, x, incx, n);
+}
+
+int gen9blas_trsv(int type, int uplo, int trans, int diag, int n, const void *A, int lda, void *x, int incx) {
+    L2_BEGIN(n, !incx);
+    if (lda < n) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "lda < n");
+    Operand oa;
+    mat(oa, A, n, n, lda, es);
+    return solve_x(t0_, es, F_FULL, full_shape(n, tri_of(uplo), diag != 0), oa, true, trans, n, x, incx, n);
+}
+
+int gen9blas_syr(int type, int uplo, int n, double alpha, const void *x, int incx, void *A, int lda) {
+    L2_BEGIN(n, !incx);
+    if (lda < n) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "lda < n");
+    Operand oa;
+    mat(oa, A, n, n, lda, es);
+    return rank_update(t0_, es, F_FULL, full_shape(n, tri_of(uplo), 0), oa, alpha, x, incx, nullptr, 0, n);
+}
+
+int gen9blas_syr2(int type, int uplo, int n, double alpha, const void *x, int incx, const void *y, int incy, void *A,
+                  int lda) {
+    L2_BEGIN(n, !incx || !incy);
+    if (lda < n) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "lda < n");
+    Operand oa;
+    mat(oa, A, n, n, lda, es);
+    return rank_update(t0_, es, F_FULL, full_shape(n, tri_of(uplo), 0), oa, alpha, x, incx, y, incy, n);
+}
+
+// ---- band and packed storage (reference: lib/src/level12.c:372-519) ----
+int gen9blas_gbmv(int type, int trans, int M, int N, int KL, int KU, double alpha, const void *A, int lda, const void *x,
+                  int incx, double beta, void *y, int incy) {
+    if (KL < 0 || KU < 0 || lda < KL + KU + 1) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "gbmv: KL, KU, lda");
+    const int nx = trans ? M : N, ny = trans ? N : M;
+    L2_BEGIN(nx < ny ? nx : ny, !incx || !incy);
+    Operand oa;
+    mat(oa, A, M, KL + KU + 1, lda, es);
+    return product_y(t0_, es, F_BAND, band_shape(M, N, KL, KU, TRI_NONE, 0), oa, false, trans ? DIR_COL : DIR_ROW, 0,
+                     alpha, x, incx, nx, beta, y, incy, ny);
+}
+
+int gen9blas_sbmv(int type, int uplo, int N, int K, double alpha, const void *A, int lda, const void *x, int incx,
+                  double beta, void *y, int incy) {
+    if (K < 0 || lda < K + 1) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "sbmv: K, lda");
+    L2_BEGIN(N, !incx || !incy);
+    const int up = uplo == GEN9BLAS_UPPER;
+    Operand oa;
+    mat(oa, A, N, K + 1, lda, es);
+    return product_y(t0_, es, F_BAND, band_shape(N, N, up ? 0 : K, up ? K : 0, tri_of(uplo), 0), oa, false,
+                     DIR_ROW | DIR_COL, 1, alpha, x, incx, N, beta, y, incy, N);
+}
+
+int gen9blas_tbmv(int type, int uplo, int trans, int diag, int N, int K, const void *A, int lda, void *x, int incx) {
+    if (K < 0 || lda < K + 1) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "tbmv: K, lda");
+    L2_BEGIN(N, !incx);
+    const int up = uplo == GEN9BLAS_UPPER;
+    Operand oa;
+    mat(oa, A, N, K + 1, lda, es);
+    return product_x(t0_, es, F_BAND, band_shape(N, N, up ? 0 : K, up ? K : 0, tri_of(uplo), diag != 0), oa, false,
+                     trans != 0, x, incx, N);
+}
+
+int gen9blas_tbsv(int type, int uplo, int trans, int diag, int N, int K, const void *A, int lda, void *x, int incx) {
+    if (K < 0 || lda < K + 1) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "tbsv: K, lda");
+    L2_BEGIN(N, !incx);
+    const int up = uplo == GEN9BLAS_UPPER;
+    Operand oa;
+    mat(oa, A, N, K + 1, lda, es);
+    return solve_x(t0_, es, F_BAND, band_shape(N, N, up ? 0 : K, up ? K : 0, tri_of(uplo), diag != 0), oa, false, trans, K,
+                   x, incx, N);
+}
+
+int gen9blas_spmv(int type, int uplo, int N, double alpha, const void *Ap, const void *x, int incx, double beta, void *y,
+                  int incy) {
+    L2_BEGIN(N, !incx || !incy);
+    Operand oa;
+    vec(oa, Ap, (int)0, 1, es);
+    oa.cols = packed_len(N);
+    oa.caller_ld = oa.cols;
+    const int up = uplo == GEN9BLAS_UPPER;
+    return product_y(t0_, es, up ? F_PACKU : F_PACKL, full_shape(N, tri_of(uplo), 0), oa, false, DIR_ROW | DIR_COL, 1,
+                     alpha, x, incx, N, beta, y, incy, N);
+}
+
+int gen9blas_tpmv(int type, int uplo, int trans, int diag, int N, const void *Ap, void *x, int incx) {
+    L2_BEGIN(N, !incx);
+    Operand oa;
+    vec(oa, Ap, (int)0, 1, es);
+    oa.cols = packed_len(N);
+    oa.caller_ld = oa.cols;
+    const int up = uplo == GEN9BLAS_UPPER;
+    return product_x(t0_, es, up ? F_PACKU : F_PACKL, full_shape(N, tri_of(uplo), diag != 0), oa, false, trans != 0, x,
+                     incx, N);
+}
+
+int gen9blas_tpsv(int type, int uplo, int trans, int diag, int N, const void *Ap, void *x, int incx) {
+    L2_BEGIN(N, !incx);
+    Operand oa;
+    vec(oa, Ap, (int)0, 1, es);
+    oa.cols = packed_len(N);
+    oa.caller_ld = oa.cols;
+    const int up = uplo == GEN9BLAS_UPPER;
+    return solve_x(t0_, es, up ? F_PACKU : F_PACKL, full_shape(N, tri_of(uplo), diag != 0), oa, false, trans, N, x, incx, N);
+}
+
+int gen9blas_spr(int type, int uplo, int N, double alpha, const void *x, int incx, void *Ap) {
+    L2_BEGIN(N, !incx);
+    Operand oa;
+    vec(oa, Ap, (int)0, 1, es);
+    oa.cols = packed_len(N);
+    oa.caller_ld = oa.cols;
+    const int up = uplo == GEN9BLAS_UPPER;
+    return rank_update(t0_, es, up ? F_PACKU : F_PACKL, full_shape(N, tri_of(uplo), 0), oa, alpha, x, incx, nullptr, 0, N);
+}
+
+int gen9blas_spr2(int type, int uplo, int N, double alpha, const void *x, int incx, const void *y, int incy, void *Ap) {
+    L2_BEGIN(N, !incx || !incy);
+    Operand oa;
+    vec(oa, Ap, (int)0, 1, es);
+    oa.cols = packed_len(N);
+    oa.caller_ld = oa.cols;
+    const int up = uplo == GEN9BLAS_UPPER;
+    return rank_update(t0_, es, up ? F_PACKU : F_PACKL, full_shape(N, tri_of(uplo), 0), oa, alpha, x, incx, y, incy, N);
+}
+
+}  // extern "C"

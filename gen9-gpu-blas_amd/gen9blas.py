@@ -533,3 +533,204 @@ def ger(alpha, x, y, A):
     if nx != M or ny != N:
         raise ValueError("lengths of x, y do not match A")
     _check(_lib.gen9blas_ger(_kind_basic(t), M, N, alpha, px, ix, py, iy, pa, lda)); return A
+
+
+# ---------------- level 2 on symmetric, triangular, banded and packed matrices ----------------
+# Full storage: a square matrix of which the `uplo` triangle is used (an A.T view passes as the other triangle, no
+# copy). Band: a row-major array (rows, KL+KU+1) with A[i, j] in row i, column KL + j − i (symmetric / triangular:
+# lower KL = K, KU = 0; upper KL = 0, KU = K). Packed: a contiguous vector of n(n+1)/2 elements holding the rows of
+# the triangle (upper: j = i..n−1, lower: j = 0..i). (reference: lib/gen9blas.py:424-610)
+for _name, _types in {
+        "gen9blas_symv": [_i, _i, _i, _d, _p, _i, _p, _i, _d, _p, _i], "gen9blas_trmv": [_i] * 5 + [_p, _i, _p, _i],
+        "gen9blas_trsv": [_i] * 5 + [_p, _i, _p, _i], "gen9blas_syr": [_i, _i, _i, _d, _p, _i, _p, _i],
+        "gen9blas_syr2": [_i, _i, _i, _d, _p, _i, _p, _i, _p, _i],
+        "gen9blas_gbmv": [_i] * 6 + [_d, _p, _i, _p, _i, _d, _p, _i], "gen9blas_sbmv": [_i] * 4 + [_d, _p, _i, _p, _i, _d, _p, _i],
+        "gen9blas_tbmv": [_i] * 6 + [_p, _i, _p, _i], "gen9blas_tbsv": [_i] * 6 + [_p, _i, _p, _i],
+        "gen9blas_spmv": [_i] * 3 + [_d, _p, _p, _i, _d, _p, _i], "gen9blas_tpmv": [_i] * 5 + [_p, _p, _i],
+        "gen9blas_tpsv": [_i] * 5 + [_p, _p, _i], "gen9blas_spr": [_i] * 3 + [_d, _p, _i, _p],
+        "gen9blas_spr2": [_i] * 3 + [_d, _p, _i, _p, _i, _p],
+        "gen9blas_rotm": [_i, _i, _p, _i, _p, _i, ctypes.POINTER(_d)]}.items():
+    getattr(_lib, _name).argtypes = _types
+_fptr = ctypes.POINTER(_f)
+_lib.gen9blas_rotg.argtypes = [_fptr] * 4
+_lib.gen9blas_rotmg.argtypes = [_fptr, _fptr, _fptr, _f, _fptr]
+
+
+def _sq(A, t, uplo):
+    """(array, pointer, n, ld, transposed, triangle in memory) of a square matrix; a transposed view swaps uplo."""
+    A, pa, r, c, lda, tr = _mat(A, t)
+    if r != c:
+        raise ValueError("expected a square matrix")
+    return A, pa, r, lda, tr, ({"L": "U", "U": "L"}[uplo] if tr else uplo)
+
+
+def _y_for(y, n, t, like):
+    """(y, pointer, inc, beta applies) for an output vector of length n: a new one when y is None."""
+    if y is None:
+        y = _new_vec(n, t, like)
+        y, py, _, iy = _vec(y, t, True)
+        return y, py, iy, False
+    y, py, ny, iy = _vec(y, t, True)
+    if ny != n:
+        raise ValueError("length of y does not match A")
+    return y, py, iy, True
+
+
+def symv(A, x, uplo="L", alpha=1.0, beta=0.0, y=None):
+    """y = alpha·A·x + beta·y, A symmetric from its `uplo` triangle; without y: a new vector."""
+    _init(); t = _dtype_of(A); A, pa, n, lda, _, u = _sq(A, t, uplo)
+    x, px, nx, ix = _vec(x, t)
+    if nx != n:
+        raise ValueError("length of x does not match A")
+    y, py, iy, given = _y_for(y, n, t, x)
+    _check(_lib.gen9blas_symv(_kind_basic(t), _TRI[u], n, alpha, pa, lda, px, ix, beta if given else 0.0, py, iy))
+    return y
+
+
+def trmv(A, x, uplo="L", trans=False, diag=False):
+    """x = op(A)·x in place, A triangular (`uplo`; diag=True: unit diagonal). Returns x."""
+    _init(); t = _dtype_of(x); A, pa, n, lda, tr, u = _sq(A, t, uplo)
+    x, px, nx, ix = _vec(x, t, True)
+    if nx != n:
+        raise ValueError("length of x does not match A")
+    _check(_lib.gen9blas_trmv(_kind_basic(t), _TRI[u], int(trans) ^ tr, int(diag), n, pa, lda, px, ix)); return x
+
+
+def trsv(A, x, uplo="L", trans=False, diag=False):
+    """Solves op(A)·z = x and stores z in x, A triangular. Returns x."""
+    _init(); t = _dtype_of(x); A, pa, n, lda, tr, u = _sq(A, t, uplo)
+    x, px, nx, ix = _vec(x, t, True)
+    if nx != n:
+        raise ValueError("length of x does not match A")
+    _check(_lib.gen9blas_trsv(_kind_basic(t), _TRI[u], int(trans) ^ tr, int(diag), n, pa, lda, px, ix)); return x
+
+
+def syr(alpha, x, A, uplo="L"):
+    """A = alpha·x·xᵀ + A on the `uplo` triangle (in place). Returns A."""
+    _init(); t = _dtype_of(A); A, pa, M, N, lda, _ = _mat(A, t, True)
+    x, px, n, ix = _vec(x, t)
+    if not M == N == n:
+        raise ValueError("dimensions do not match")
+    _check(_lib.gen9blas_syr(_kind_basic(t), _TRI[uplo], n, alpha, px, ix, pa, lda)); return A
+
+
+def syr2(alpha, x, y, A, uplo="L"):
+    """A = alpha·(x·yᵀ + y·xᵀ) + A on the `uplo` triangle (in place). Returns A."""
+    _init(); t = _dtype_of(A); A, pa, M, N, lda, _ = _mat(A, t, True)
+    x, px, n, ix = _vec(x, t); y, py, ny, iy = _vec(y, t)
+    if not M == N == n == ny:
+        raise ValueError("dimensions do not match")
+    _check(_lib.gen9blas_syr2(_kind_basic(t), _TRI[uplo], n, alpha, px, ix, py, iy, pa, lda)); return A
+
+
+def _band(A, t, width, write=False):
+    A, pa, rows, w, lda, tr = _mat(A, t, write)
+    if tr or w != width:
+        raise ValueError(f"band: expected a row-major array with {width} columns")
+    return A, pa, rows, lda
+
+
+def _packed(Ap, t, n, write=False):
+    Ap, pp, m, inc = _vec(Ap, t, write)
+    if inc != 1 or m != n * (n + 1) // 2:
+        raise ValueError(f"packed: expected a contiguous vector of length {n * (n + 1) // 2}")
+    return Ap, pp
+
+
+def gbmv(A, x, M, N, KL, KU, alpha=1.0, beta=0.0, y=None, trans=False):
+    """y = alpha·op(A)·x + beta·y, A an M×N band matrix stored as an (M, KL+KU+1) array."""
+    _init(); t = _dtype_of(A); A, pa, m, lda = _band(A, t, KL + KU + 1)
+    if m != M:
+        raise ValueError("number of band rows != M")
+    x, px, nx, ix = _vec(x, t)
+    if nx != (M if trans else N):
+        raise ValueError("length of x")
+    y, py, iy, given = _y_for(y, N if trans else M, t, x)
+    _check(_lib.gen9blas_gbmv(_kind_basic(t), int(trans), M, N, KL, KU, alpha, pa, lda, px, ix, beta if given else 0.0,
+                              py, iy))
+    return y
+
+
+def sbmv(A, x, K, uplo="L", alpha=1.0, beta=0.0, y=None):
+    """y = alpha·A·x + beta·y, A symmetric band (array (n, K+1), triangle `uplo`)."""
+    _init(); t = _dtype_of(A); A, pa, n, lda = _band(A, t, K + 1)
+    x, px, nx, ix = _vec(x, t)
+    if nx != n:
+        raise ValueError("length of x")
+    y, py, iy, given = _y_for(y, n, t, x)
+    _check(_lib.gen9blas_sbmv(_kind_basic(t), _TRI[uplo], n, K, alpha, pa, lda, px, ix, beta if given else 0.0, py, iy))
+    return y
+
+
+def tbmv(A, x, K, uplo="L", trans=False, diag=False):
+    """x = op(A)·x in place, A triangular band (array (n, K+1))."""
+    _init(); t = _dtype_of(x); A, pa, n, lda = _band(A, t, K + 1); x, px, nx, ix = _vec(x, t, True)
+    if nx != n:
+        raise ValueError("length of x")
+    _check(_lib.gen9blas_tbmv(_kind_basic(t), _TRI[uplo], int(trans), int(diag), n, K, pa, lda, px, ix)); return x
+
+
+def tbsv(A, x, K, uplo="L", trans=False, diag=False):
+    """Solves op(A)·z = x in place, A triangular band (array (n, K+1))."""
+    _init(); t = _dtype_of(x); A, pa, n, lda = _band(A, t, K + 1); x, px, nx, ix = _vec(x, t, True)
+    if nx != n:
+        raise ValueError("length of x")
+    _check(_lib.gen9blas_tbsv(_kind_basic(t), _TRI[uplo], int(trans), int(diag), n, K, pa, lda, px, ix)); return x
+
+
+def spmv(Ap, x, uplo="L", alpha=1.0, beta=0.0, y=None):
+    """y = alpha·A·x + beta·y, A symmetric packed (vector of n(n+1)/2)."""
+    _init(); t = _dtype_of(Ap); x, px, n, ix = _vec(x, t); Ap, pp = _packed(Ap, t, n)
+    y, py, iy, given = _y_for(y, n, t, x)
+    _check(_lib.gen9blas_spmv(_kind_basic(t), _TRI[uplo], n, alpha, pp, px, ix, beta if given else 0.0, py, iy)); return y
+
+
+def tpmv(Ap, x, uplo="L", trans=False, diag=False):
+    """x = op(A)·x in place, A triangular packed."""
+    _init(); t = _dtype_of(x); x, px, n, ix = _vec(x, t, True); Ap, pp = _packed(Ap, t, n)
+    _check(_lib.gen9blas_tpmv(_kind_basic(t), _TRI[uplo], int(trans), int(diag), n, pp, px, ix)); return x
+
+
+def tpsv(Ap, x, uplo="L", trans=False, diag=False):
+    """Solves op(A)·z = x in place, A triangular packed."""
+    _init(); t = _dtype_of(x); x, px, n, ix = _vec(x, t, True); Ap, pp = _packed(Ap, t, n)
+    _check(_lib.gen9blas_tpsv(_kind_basic(t), _TRI[uplo], int(trans), int(diag), n, pp, px, ix)); return x
+
+
+def spr(alpha, x, Ap, uplo="L"):
+    """A = alpha·x·xᵀ + A, A packed (in place). Returns Ap."""
+    _init(); t = _dtype_of(Ap); x, px, n, ix = _vec(x, t); Ap, pp = _packed(Ap, t, n, True)
+    _check(_lib.gen9blas_spr(_kind_basic(t), _TRI[uplo], n, alpha, px, ix, pp)); return Ap
+
+
+def spr2(alpha, x, y, Ap, uplo="L"):
+    """A = alpha·(x·yᵀ + y·xᵀ) + A, A packed (in place). Returns Ap."""
+    _init(); t = _dtype_of(Ap); x, px, n, ix = _vec(x, t); y, py, ny, iy = _vec(y, t)
+    if ny != n:
+        raise ValueError("lengths of x, y")
+    Ap, pp = _packed(Ap, t, n, True)
+    _check(_lib.gen9blas_spr2(_kind_basic(t), _TRI[uplo], n, alpha, px, ix, py, iy, pp)); return Ap
+
+
+def rotm(x, y, param):
+    """x, y = h11·x + h12·y, h21·x + h22·y in place; param = (flag, h11, h21, h12, h22) as in BLAS."""
+    _init(); t = _dtype_of(x); x, px, n, ix = _vec(x, t, True); y, py, ny, iy = _vec(y, t, True)
+    if ny != n:
+        raise ValueError("lengths differ")
+    pr = (_d * 5)(*[float(v) for v in param])
+    _check(_lib.gen9blas_rotm(_kind_basic(t), n, px, ix, py, iy, pr)); return x, y
+
+
+def rotg(a, b):
+    """(r, z, c, s) of the Givens rotation that zeroes b (computed on the host)."""
+    w = [_f(a), _f(b), _f(), _f()]
+    _lib.gen9blas_rotg(*[ctypes.byref(v) for v in w])
+    return tuple(v.value for v in w)
+
+
+def rotmg(d1, d2, x1, y1):
+    """(d1, d2, x1, param) of the modified Givens rotation (computed on the host); param has 5 entries."""
+    w = [_f(d1), _f(d2), _f(x1)]
+    pr = (_f * 5)()
+    _lib.gen9blas_rotmg(*[ctypes.byref(v) for v in w], _f(y1), pr)
+    return w[0].value, w[1].value, w[2].value, np.array(pr[:], np.float32)

@@ -145,6 +145,74 @@ def gemv(A, x, alpha=1.0, beta=0.0, y=None, trans=False):
     return out
 
 
+# ---------------- level 2: symmetric, triangular, band and packed storage (float64 closed forms) ----------------
+# The arithmetic of these routines is a plain sum of products (FP32 / FP64 accumulation, reference:
+# lib/kernels/level12.cl:424-640), so the oracle is the float64 product of the matrix the storage describes; what a
+# kernel can get wrong is the storage mapping, restated here element by element.
+def band_dense(P, M, N, KL, KU):
+    """M×N float64 matrix of a row-major band array P (rows of lda >= KL+KU+1): A(r, c) = P[r, KL + c − r] for
+    −KL <= c − r <= KU, zero elsewhere (reference: lib/kernels/level12.cl:584-590, lib/gen9blas.h:147-150)."""
+    P = np.asarray(P, np.float64)
+    D = np.zeros((M, N))
+    for r in range(M):
+        for c in range(max(0, r - KL), min(N, r + KU + 1)):
+            D[r, c] = P[r, KL + c - r]
+    return D
+
+
+def packed_dense(Ap, n, uplo):
+    """n×n float64 triangle of a packed vector: upper row r (c = r..n−1) starts at r·n − r(r−1)/2, lower row r
+    (c = 0..r) at r(r+1)/2 (reference: lib/kernels/level12.cl:588-590, lib/gen9blas.h:150-151)."""
+    Ap = np.asarray(Ap, np.float64)
+    D = np.zeros((n, n))
+    for r in range(n):
+        if uplo == "U":
+            s0 = r * n - r * (r - 1) // 2
+            D[r, r:] = Ap[s0:s0 + n - r]
+        else:
+            s0 = r * (r + 1) // 2
+            D[r, :r + 1] = Ap[s0:s0 + r + 1]
+    return D
+
+
+def triangle(D, uplo, unit=False):
+    """The `uplo` triangle of D (float64); unit: ones on the diagonal instead of the stored values."""
+    T = np.tril(D) if uplo == "L" else np.triu(D)
+    if unit:
+        np.fill_diagonal(T, 1.0)
+    return T
+
+
+def symmetric(D, uplo):
+    """The symmetric matrix whose `uplo` triangle is that of D."""
+    T = triangle(D, uplo)
+    return T + T.T - np.diag(np.diag(T))
+
+
+def mv(Op, x, alpha=1.0, beta=0.0, y=None):
+    """(alpha·Op·x + beta·y, its scale |alpha|·|Op|·|x| + |beta·y|) in float64: the product and the error scale of
+    the reference's level-2 test (reference: lib/test_level12.py:27-35, 105-113)."""
+    X = np.asarray(x, np.float64)
+    r, s = alpha * (Op @ X), abs(alpha) * (np.abs(Op) @ np.abs(X))
+    if beta:
+        Y = np.asarray(y, np.float64)
+        r, s = r + beta * Y, s + abs(beta) * np.abs(Y)
+    return r, s
+
+
+def solve(Op, b):
+    """op(A)·z = b for a triangular float64 op(A), by substitution in the order of the reference's blocked solve
+    (reference: lib/kernels/level12.cl:493-548: forward for a lower op(A), backward for an upper one)."""
+    n = Op.shape[0]
+    z = np.array(b, np.float64)
+    lower = np.allclose(Op, np.tril(Op))
+    for k in (range(n) if lower else range(n - 1, -1, -1)):
+        z[k] /= Op[k, k]
+        rest = slice(k + 1, n) if lower else slice(0, k)
+        z[rest] -= Op[rest, k] * z[k]
+    return z
+
+
 # ---------------- the reference's error metric ----------------
 def gemm_error(W, opA, opB, alpha=1.0, beta=0.0, C0=None):
     """Element-wise e = |W − ref| / (|alpha|·Σ|a·b| + |beta·c|) against the float64 product of the same (rounded)

@@ -1,0 +1,236 @@
+"""Level-2 parity on the GPU: SYMV, TRMV, TRSV, SYR, SYR2 on full storage and GBMV, SBMV, TBMV, TBSV, SPMV, TPMV,
+TPSV, SPR, SPR2 on band and packed storage, through the C ABI (gen9blas.py) against the oracle's float64 restatement
+of each storage format (oracle.band_dense / packed_dense / triangle / symmetric / solve).
+
+Cases follow the reference's level-2 test (reference: lib/test_level12.py:98-146, 180-259): orders 1, 5, 63, 64, 65,
+200, 1000; both triangles, both transposes, unit and stored diagonals, an A.T view (the other triangle in memory),
+strided and negative-stride vectors; band shapes (M, N, KL, KU) and (n, K) as there. Bounds as there: error relative
+to |alpha|·|op(A)|·|x| + |beta·y|, FP32 1e-6, FP16 2e-3, FP64 1e-13; solutions relative to max|z|: FP32 1e-5,
+FP16 3e-3, FP64 1e-12. Device-resident cases at n = 4096 exercise the multi-block solves and both load paths of the
+product kernel (16-byte rows and an odd row stride).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = {np.float32: 1e-6, np.float16: 2e-3, np.float64: 1e-13}
+SOLVE_TOL = {np.float32: 1e-5, np.float16: 3e-3, np.float64: 1e-12}
+DTYPES = [np.float32, np.float16, np.float64]
+rng = np.random.default_rng(12)
+
+
+def check(name, W, ref, scale, tol):
+    e = float(np.max(np.abs(np.asarray(W, np.float64) - ref) / np.maximum(scale, 6.2e-5 if tol > 1e-5 else 1e-30)))
+    assert e <= tol, f"{name}: {e:.1e} > {tol:.0e}"
+
+
+def vector(n, dt, step=1, shift=0):
+    base = rng.uniform(-1, 1, n * abs(step) + shift + 3).astype(dt)
+    v = base[shift:shift + n * abs(step):abs(step)]
+    return v[::-1] if step < 0 else v
+
+
+def f64(a):
+    return np.asarray(a, np.float64)
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("n", [1, 5, 63, 64, 65, 200, 1000])
+def test_full_storage(g9, orc, dt, n):
+    tol = TOL[dt]
+    A = rng.uniform(-1, 1, (n, n)).astype(dt)
+    Ad = f64(A)
+    for uplo in "LU":
+        S = orc.symmetric(Ad, uplo)
+        x, y0 = vector(n, dt, -2, 1), vector(n, dt, 3)
+        ref, scale = orc.mv(S, x, 0.5, 2.0, y0)
+        g9.symv(A, x, uplo=uplo, alpha=0.5, beta=2.0, y=y0)
+        check(f"symv {uplo} n={n}", y0, ref, scale, tol)
+        ref, scale = orc.mv(orc.symmetric(Ad.T, uplo), x)
+        check(f"symv A.T {uplo} n={n}", g9.symv(A.T, x, uplo=uplo), ref, scale, tol)
+        for trans in (False, True):
+            for diag in (False, True):
+                label = f"{uplo} trans={int(trans)} diag={int(diag)} n={n}"
+                Op = orc.triangle(Ad, uplo, diag)
+                Op = Op.T if trans else Op
+                xx = vector(n, dt, 2)
+                ref, scale = orc.mv(Op, xx)
+                g9.trmv(A, xx, uplo=uplo, trans=trans, diag=diag)
+                check("trmv " + label, xx, ref, scale, tol)
+                # solve: well conditioned (large diagonal; with a unit diagonal, small off-diagonal entries)
+                if diag:
+                    Ab = (Ad / n).astype(dt)
+                else:
+                    Ab = A.copy()
+                    np.fill_diagonal(Ab, np.where(np.diag(Ad) < 0, -1, 1) * n / 4 + np.diag(Ad))
+                Ob = orc.triangle(f64(Ab), uplo, diag)
+                Ob = Ob.T if trans else Ob
+                b = vector(n, dt, -1)
+                ref = orc.solve(Ob, f64(b))
+                g9.trsv(Ab, b, uplo=uplo, trans=trans, diag=diag)
+                check("trsv " + label, b, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+        xs, ys = vector(n, dt, 1, 2), vector(n, dt, -3, 0)
+        X, Y = f64(xs), f64(ys)
+        mask = np.tril(np.ones((n, n), bool)) if uplo == "L" else np.triu(np.ones((n, n), bool))
+        A1 = A.copy()
+        g9.syr(-0.5, xs, A1, uplo=uplo)
+        check(f"syr {uplo} n={n}", A1, np.where(mask, Ad - 0.5 * np.outer(X, X), Ad),
+              np.abs(Ad) + 0.5 * np.outer(np.abs(X), np.abs(X)), tol)
+        A2 = A.copy()
+        g9.syr2(0.25, xs, ys, A2, uplo=uplo)
+        check(f"syr2 {uplo} n={n}", A2, np.where(mask, Ad + 0.25 * (np.outer(X, Y) + np.outer(Y, X)), Ad),
+              np.abs(Ad) + 0.25 * (np.outer(np.abs(X), np.abs(Y)) + np.outer(np.abs(Y), np.abs(X))), tol)
+
+
+def to_band(D, KL, KU):
+    M, N = D.shape
+    P = np.zeros((M, KL + KU + 1), D.dtype)
+    for i in range(M):
+        for j in range(max(0, i - KL), min(N, i + KU + 1)):
+            P[i, KL + j - i] = D[i, j]
+    return P
+
+
+def band_mask(M, N, KL, KU):
+    i, j = np.indices((M, N))
+    return (j - i >= -KL) & (j - i <= KU)
+
+
+def pack(D, uplo):
+    return D[np.triu_indices(D.shape[0])] if uplo == "U" else D[np.tril_indices(D.shape[0])]
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("M,N,KL,KU", [(1, 1, 0, 0), (50, 40, 3, 5), (300, 310, 0, 7), (257, 200, 30, 0),
+                                       (100, 100, 99, 99), (1200, 1100, 2, 300)])
+def test_gbmv(g9, orc, dt, M, N, KL, KU):
+    tol = TOL[dt]
+    D = f64(rng.uniform(-1, 1, (M, N)).astype(dt)) * band_mask(M, N, KL, KU)
+    P = to_band(D, KL, KU).astype(dt)
+    assert np.array_equal(orc.band_dense(P, M, N, KL, KU), D)
+    for tr in (False, True):
+        x, y0 = vector(M if tr else N, dt, -2), vector(N if tr else M, dt, 3)
+        ref, scale = orc.mv(D.T if tr else D, x, 0.5, 2.0, y0)
+        g9.gbmv(P, x, M, N, KL, KU, alpha=0.5, beta=2.0, y=y0, trans=tr)
+        check(f"gbmv {M}x{N} KL={KL} KU={KU} tr={tr}", y0, ref, scale, tol)
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("n,K", [(1, 0), (60, 4), (300, 17), (130, 129), (700, 70)])
+def test_band_packed(g9, orc, dt, n, K):
+    tol = TOL[dt]
+    Dp = f64(rng.uniform(-1, 1, (n, n)).astype(dt))
+    for uplo in "UL":
+        g = uplo == "U"
+        KL, KU = (0, K) if g else (K, 0)
+        T = Dp * band_mask(n, n, KL, KU)
+        P = to_band(T, KL, KU).astype(dt)
+        x = vector(n, dt, 2)
+        ref, scale = orc.mv(orc.symmetric(T, uplo), x, 1.5)
+        check(f"sbmv n={n} K={K} {uplo}", g9.sbmv(P, x, K, uplo=uplo, alpha=1.5), ref, scale, tol)
+        Tp = orc.triangle(Dp, uplo)
+        Ap = pack(Tp, uplo).astype(dt)
+        assert np.array_equal(orc.packed_dense(Ap, n, uplo), Tp)
+        y0 = vector(n, dt, -1)
+        ref, scale = orc.mv(orc.symmetric(Tp, uplo), x, 0.5, -1.0, y0)
+        g9.spmv(Ap, x, uplo=uplo, alpha=0.5, beta=-1.0, y=y0)
+        check(f"spmv n={n} {uplo}", y0, ref, scale, tol)
+        for tr in (False, True):
+            for dg in (False, True):
+                label = f"n={n} K={K} {uplo} tr={tr} diag={dg}"
+                Ob, Op = orc.triangle(T, uplo, dg), orc.triangle(Tp, uplo, dg)
+                Ob, Op = (Ob.T, Op.T) if tr else (Ob, Op)
+                x = vector(n, dt, -3)
+                ref, scale = orc.mv(Ob, x)
+                g9.tbmv(P, x, K, uplo=uplo, trans=tr, diag=dg)
+                check("tbmv " + label, x, ref, scale, tol)
+                x = vector(n, dt, 1)
+                ref, scale = orc.mv(Op, x)
+                g9.tpmv(Ap, x, uplo=uplo, trans=tr, diag=dg)
+                check("tpmv " + label, x, ref, scale, tol)
+                # solves: well conditioned (small off-diagonal entries, diagonal 1..2)
+                Ts = T / max(K, 1) / 4
+                np.fill_diagonal(Ts, 1 + np.abs(np.diag(T)))
+                Ps = to_band(Ts, KL, KU).astype(dt)
+                Os = orc.triangle(orc.band_dense(Ps, n, n, KL, KU), uplo, dg)
+                b = vector(n, dt, 2)
+                ref = orc.solve(Os.T if tr else Os, f64(b))
+                g9.tbsv(Ps, b, K, uplo=uplo, trans=tr, diag=dg)
+                check("tbsv " + label, b, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+                Tq = Tp / n
+                np.fill_diagonal(Tq, 1 + np.abs(np.diag(Tp)))
+                Aq = pack(Tq, uplo).astype(dt)
+                Oq = orc.triangle(orc.packed_dense(Aq, n, uplo), uplo, dg)
+                b = vector(n, dt, -1)
+                ref = orc.solve(Oq.T if tr else Oq, f64(b))
+                g9.tpsv(Aq, b, uplo=uplo, trans=tr, diag=dg)
+                check("tpsv " + label, b, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+        xs, ys = vector(n, dt, 1), vector(n, dt, -2)
+        X, Y = f64(xs), f64(ys)
+        Ap1 = Ap.copy()
+        g9.spr(-0.5, xs, Ap1, uplo=uplo)
+        check(f"spr n={n} {uplo}", Ap1, pack(orc.triangle(Tp - 0.5 * np.outer(X, X), uplo), uplo),
+              pack(np.abs(Tp) + 0.5 * np.outer(np.abs(X), np.abs(X)), uplo), tol)
+        Ap2 = Ap.copy()
+        g9.spr2(0.25, xs, ys, Ap2, uplo=uplo)
+        check(f"spr2 n={n} {uplo}", Ap2, pack(orc.triangle(Tp + 0.25 * (np.outer(X, Y) + np.outer(Y, X)), uplo), uplo),
+              pack(np.abs(Tp) + 0.25 * (np.outer(np.abs(X), np.abs(Y)) + np.outer(np.abs(Y), np.abs(X))), uplo), tol)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+@pytest.mark.parametrize("odd_ld", [False, True])
+def test_level2_device_n4096(g9, orc, torch_dev, dt, odd_ld):
+    """n = 4096 on device tensors: 32 diagonal blocks per solve; odd_ld passes a view with row stride 4097, which takes
+    the element-wise load path of the product kernel instead of the 16-byte one."""
+    torch = torch_dev
+    n = 4096
+    base = rng.uniform(-1, 1, (n, n + 1 if odd_ld else n)).astype(dt)
+    A = base[:, :n]
+    Ad = f64(A)
+    Adev = torch.from_numpy(base).cuda()[:, :n]
+    assert Adev.stride()[0] == (n + 1 if odd_ld else n)
+    x = rng.uniform(-1, 1, n).astype(dt)
+    xd = torch.from_numpy(x).cuda()
+    for uplo in "LU":
+        ref, scale = orc.mv(orc.symmetric(Ad, uplo), x, 1.25)
+        check(f"symv {uplo}", g9.symv(Adev, xd, uplo=uplo, alpha=1.25).cpu().numpy(), ref, scale, TOL[dt])
+        for trans in (False, True):
+            Op = orc.triangle(Ad, uplo)
+            Op = Op.T if trans else Op
+            v = xd.clone()
+            g9.trmv(Adev, v, uplo=uplo, trans=trans)
+            ref, scale = orc.mv(Op, x)
+            check(f"trmv {uplo} trans={trans}", v.cpu().numpy(), ref, scale, TOL[dt])
+        Ab = base.copy()
+        np.fill_diagonal(Ab[:, :n], np.where(np.diag(Ad) < 0, -1, 1) * n / 4 + np.diag(Ad))
+        Abd = torch.from_numpy(Ab).cuda()[:, :n]
+        for trans in (False, True):
+            Ob = orc.triangle(f64(Ab[:, :n]), uplo)
+            Ob = Ob.T if trans else Ob
+            v = xd.clone()
+            g9.trsv(Abd, v, uplo=uplo, trans=trans)
+            ref = orc.solve(Ob, f64(x))
+            check(f"trsv {uplo} trans={trans}", v.cpu().numpy(), ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+        Ap = pack(orc.triangle(Ad, uplo), uplo).astype(dt)
+        ref, scale = orc.mv(orc.symmetric(Ad, uplo), x)
+        check(f"spmv {uplo}", g9.spmv(torch.from_numpy(Ap).cuda(), xd, uplo=uplo).cpu().numpy(), ref, scale, TOL[dt])
+
+
+def test_level2_errors(g9):
+    """Status codes as in the reference (reference: lib/src/level12.c:267-519): lda < n and band widths are
+    INVALID_ARG, a zero increment is INVALID_ARG, an unknown type UNSUPPORTED, an empty problem 0 with nothing
+    read."""
+    L = g9._lib
+    a = np.zeros((4, 4), np.float32)
+    x = np.zeros(4, np.float32)
+    p = a.ctypes.data
+    px = x.ctypes.data
+    assert L.gen9blas_symv(1, 0, 4, 1.0, p, 3, px, 1, 0.0, px, 1) == -3
+    assert L.gen9blas_trsv(1, 0, 0, 0, 4, p, 4, px, 0) == -3
+    assert L.gen9blas_gbmv(1, 0, 4, 4, -1, 0, 1.0, p, 4, px, 1, 0.0, px, 1) == -3
+    assert L.gen9blas_gbmv(1, 0, 4, 4, 2, 2, 1.0, p, 4, px, 1, 0.0, px, 1) == -3
+    assert L.gen9blas_tbsv(1, 0, 0, 0, 4, 4, p, 4, px, 1) == -3
+    assert L.gen9blas_spmv(7, 0, 4, 1.0, p, px, 1, 0.0, px, 1) == -2
+    assert L.gen9blas_tpsv(1, 0, 0, 0, 0, None, None, 1) == 0
+    assert L.gen9blas_syr2(1, 0, -1, 1.0, None, 1, None, 1, None, 1) == 0

@@ -248,3 +248,89 @@ def test_golden_fixtures():
     v = np.load(os.path.join(GOLDEN, "level12_small.npz"))
     assert abs(O.dot(v["x"], v["y"]) - float(v["dot"])) <= 1e-12 * float(v["dot_scale"])
     assert np.max(np.abs(O.gemv(v["A"], v["x"][:v["A"].shape[1]]) - v["gemv"]) / v["gemv_scale"]) <= 1e-6
+
+
+# ---------------- level 2 storage (band, packed, triangles) ----------------
+def _band_from(D, KL, KU, width=None):
+    """Row-major band array of D built diagonal by diagonal (independent of oracle.band_dense's row loop)."""
+    M, N = D.shape
+    P = np.zeros((M, width or KL + KU + 1))
+    for d in range(-KL, KU + 1):            # diagonal c − r = d sits in column KL + d
+        r = np.arange(max(0, -d), min(M, N - d))
+        P[r, KL + d] = D[r, r + d]
+    return P
+
+
+@pytest.mark.parametrize("M,N,KL,KU", [(1, 1, 0, 0), (50, 40, 3, 5), (300, 310, 0, 7), (257, 200, 30, 0),
+                                       (100, 100, 99, 99), (7, 30, 2, 40)])
+def test_band_storage_against_openblas(M, N, KL, KU):
+    """oracle.band_dense against an independent diagonal-wise packer (round trip, exact) and against OpenBLAS dgbmv
+    (the reference's CPU path) reading the same row-major array as the column-major band of Aᵀ (kl = KU, ku = KL),
+    which is how a CBLAS row-major call maps onto Fortran storage."""
+    from scipy.linalg import blas
+    rng = np.random.default_rng(M * 1000 + N)
+    i, j = np.indices((M, N))
+    D = rng.uniform(-1, 1, (M, N)) * ((j - i >= -KL) & (j - i <= KU))
+    P = _band_from(D, KL, KU, width=KL + KU + 3)          # lda > KL+KU+1: padding columns never read
+    P[:, KL + KU + 1:] = np.nan
+    assert np.array_equal(O.band_dense(P, M, N, KL, KU), D)
+    if N < KL + KU + 1:
+        return   # SciPy's dgbmv wrapper requires m >= kl + ku + 1 (its own check; BLAS needs only lda >= kl + ku + 1)
+    x, xt = rng.uniform(-1, 1, N), rng.uniform(-1, 1, M)
+    Pf = np.asfortranarray(P.T)
+    assert np.allclose(blas.dgbmv(N, M, KU, KL, 1.0, Pf, x, trans=1), D @ x, rtol=0, atol=1e-13)
+    assert np.allclose(blas.dgbmv(N, M, KU, KL, 1.0, Pf, xt, trans=0), D.T @ xt, rtol=0, atol=1e-13)
+
+
+@pytest.mark.parametrize("n", [1, 2, 60, 130])
+@pytest.mark.parametrize("uplo", ["U", "L"])
+def test_packed_and_symmetric_band_against_openblas(n, uplo):
+    """oracle.packed_dense against NumPy's row-major triangle indices (round trip, exact); symmetric products of the
+    packed and band storages against OpenBLAS dspmv / dsbmv, and triangular ones against dtpmv / dtbmv, on the same
+    arrays (row-major upper = column-major lower of the transpose); oracle.solve against dtpsv and the residual."""
+    from scipy.linalg import blas
+    rng = np.random.default_rng(n + (uplo == "U"))
+    D = rng.uniform(-1, 1, (n, n))
+    T = O.triangle(D, uplo)
+    idx = np.triu_indices(n) if uplo == "U" else np.tril_indices(n)
+    Ap = D[idx]
+    assert np.array_equal(O.packed_dense(Ap, n, uplo), T)
+    x = rng.uniform(-1, 1, n)
+    fl = int(uplo == "U")                         # Fortran triangle of the transpose
+    assert np.allclose(blas.dspmv(n, 1.0, Ap, x, lower=fl), O.symmetric(D, uplo) @ x, rtol=0, atol=1e-13)
+    for trans in (0, 1):
+        for unit in (0, 1):
+            Op = O.triangle(D, uplo, unit)
+            Op = Op.T if trans else Op
+            assert np.allclose(blas.dtpmv(n, Ap, x, lower=fl, trans=1 - trans, diag=unit), Op @ x, rtol=0, atol=1e-13)
+            S = Op / n                               # well conditioned: small off-diagonal entries
+            np.fill_diagonal(S, 2 + np.abs(np.diag(Op)) if not unit else 1.0)
+            b = S @ x
+            z = O.solve(S, b)
+            assert np.allclose(S @ z, b, rtol=0, atol=1e-12) and np.allclose(z, x, rtol=0, atol=1e-12)
+    K = max(0, min(n - 1, 5))
+    i, j = np.indices((n, n))
+    Tb = T * (np.abs(j - i) <= K)
+    P = _band_from(Tb, 0 if uplo == "U" else K, K if uplo == "U" else 0)
+    assert np.array_equal(O.band_dense(P, n, n, 0 if uplo == "U" else K, K if uplo == "U" else 0), Tb)
+    S = Tb + Tb.T - np.diag(np.diag(Tb))
+    assert np.allclose(blas.dsbmv(K, 1.0, np.asfortranarray(P.T), x, lower=fl), S @ x, rtol=0, atol=1e-13)
+    assert np.allclose(blas.dtbmv(K, np.asfortranarray(P.T), x, lower=fl, trans=1), Tb @ x, rtol=0, atol=1e-13)
+
+
+def test_solve_order_and_planted_mistakes():
+    """oracle.solve handles both substitution orders, and a planted transpose or dropped diagonal fails the
+    residual check that the GPU tests rely on."""
+    rng = np.random.default_rng(5)
+    n = 40
+    L = np.tril(rng.uniform(-1, 1, (n, n))) / n
+    np.fill_diagonal(L, 1 + rng.uniform(0, 1, n))
+    b = rng.uniform(-1, 1, n)
+    for Op in (L, L.T):
+        z = O.solve(Op, b)
+        assert np.allclose(Op @ z, b, rtol=0, atol=1e-13)
+        wrong = O.solve(Op.T, b)
+        assert not np.allclose(Op @ wrong, b, rtol=0, atol=1e-6)
+    U = np.triu(L.T)
+    np.fill_diagonal(U, 1.0)
+    assert not np.allclose(U @ O.solve(L.T, b), b, rtol=0, atol=1e-6)   # unit diagonal is not the stored one
