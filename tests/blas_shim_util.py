@@ -176,3 +176,179 @@ L3_OPTS = {"symm": [(s, u, "N", "N") for s in "LR" for u in "UL"],
            "trsm": [(s, u, t, dg) for s in "LR" for u in "UL" for t in "NT" for dg in "NU"]}
 L3_TOL = {"s": 1e-5, "d": 1e-12}   # BLAS results (normwise per entry); TRSM solution error: 1e-4 / 1e-12
 L3_TRSM_TOL = {"s": 1e-4, "d": 1e-12}
+
+
+# ---------------- level 2 on symmetric, triangular, band and packed matrices through the shim ----------------
+L2_SYM = ("symv", "sbmv", "spmv")
+L2_TRI = ("trmv", "trsv", "tbmv", "tbsv", "tpmv", "tpsv")
+L2_RANK = ("syr", "syr2", "spr", "spr2")
+L2 = L2_SYM + L2_TRI + L2_RANK + ("gbmv",)
+OWN |= {f"cblas_{p}{f}" for p in "sd" for f in L2} | {f"{p}{f}_" for p in "sd" for f in L2}
+
+
+def band_rows(D, KL, KU):
+    """Row-major band array of D (element (r, c) at [r, KL + c − r])."""
+    M, N = D.shape
+    P = np.zeros((M, KL + KU + 1), D.dtype)
+    for r in range(M):
+        for c in range(max(0, r - KL), min(N, r + KU + 1)):
+            P[r, KL + c - r] = D[r, c]
+    return P
+
+
+def packed_rows(T, uplo):
+    return T[np.triu_indices(T.shape[0])] if uplo == "U" else T[np.tril_indices(T.shape[0])]
+
+
+def l2_storage(op, D, uplo, K, KL, KU, order):
+    """Memory of the matrix operand for `order` (ROW; COL or "F": column-major): the column-major storage of a
+    matrix is the row-major storage of its transpose (band widths swapped, packed triangle flipped)."""
+    col = order != ROW
+    X = D.T if col else D
+    fl = {"U": "L", "L": "U"}[uplo] if col else uplo
+    if op in ("gbmv",):
+        return band_rows(X, KU, KL) if col else band_rows(X, KL, KU), KL + KU + 1
+    if op in ("sbmv", "tbmv", "tbsv"):
+        lo, up = (K, 0) if fl == "L" else (0, K)
+        return band_rows(X, lo, up), K + 1
+    if op in ("spmv", "tpmv", "tpsv", "spr", "spr2"):
+        return packed_rows(X, fl), 0
+    return np.array(X, order="C"), D.shape[1]
+
+
+def call_l2(L, P, order, op, o, m, n, K, KL, KU, alpha, beta, A, lda, x, incx, y, incy):
+    """One level-2 call: CBLAS in `order` or Fortran ("F"); o = (uplo, trans, diag) letters; A, x, y device tensors
+    or NumPy arrays (y unused where the routine has none)."""
+    R = f if P == "s" else d
+    uplo, tr, dg = o
+    if order == "F":
+        ch = lambda c: ctypes.c_char_p(c.encode())
+        ri = lambda v: ctypes.byref(i(v))
+        rr = lambda v: ctypes.byref(R(v))
+        a = {"symv": [ch(uplo), ri(n), rr(alpha), ptr(A), ri(lda), ptr(x), ri(incx), rr(beta), ptr(y), ri(incy)],
+             "sbmv": [ch(uplo), ri(n), ri(K), rr(alpha), ptr(A), ri(lda), ptr(x), ri(incx), rr(beta), ptr(y), ri(incy)],
+             "spmv": [ch(uplo), ri(n), rr(alpha), ptr(A), ptr(x), ri(incx), rr(beta), ptr(y), ri(incy)],
+             "trmv": [ch(uplo), ch(tr), ch(dg), ri(n), ptr(A), ri(lda), ptr(x), ri(incx)],
+             "tbmv": [ch(uplo), ch(tr), ch(dg), ri(n), ri(K), ptr(A), ri(lda), ptr(x), ri(incx)],
+             "tpmv": [ch(uplo), ch(tr), ch(dg), ri(n), ptr(A), ptr(x), ri(incx)],
+             "syr": [ch(uplo), ri(n), rr(alpha), ptr(x), ri(incx), ptr(A), ri(lda)],
+             "syr2": [ch(uplo), ri(n), rr(alpha), ptr(x), ri(incx), ptr(y), ri(incy), ptr(A), ri(lda)],
+             "spr": [ch(uplo), ri(n), rr(alpha), ptr(x), ri(incx), ptr(A)],
+             "spr2": [ch(uplo), ri(n), rr(alpha), ptr(x), ri(incx), ptr(y), ri(incy), ptr(A)],
+             "gbmv": [ch(tr), ri(m), ri(n), ri(KL), ri(KU), rr(alpha), ptr(A), ri(lda), ptr(x), ri(incx), rr(beta),
+                      ptr(y), ri(incy)]}
+        a["trsv"], a["tbsv"], a["tpsv"] = a["trmv"], a["tbmv"], a["tpmv"]
+        getattr(L, f"{P}{op}_")(*a[op])
+        return
+    u, t, dd = UPLO[uplo], T if tr == "T" else NT, DIAG[dg]
+    c = lambda v: R(v)
+    a = {"symv": [order, u, n, c(alpha), ptr(A), lda, ptr(x), incx, c(beta), ptr(y), incy],
+         "sbmv": [order, u, n, K, c(alpha), ptr(A), lda, ptr(x), incx, c(beta), ptr(y), incy],
+         "spmv": [order, u, n, c(alpha), ptr(A), ptr(x), incx, c(beta), ptr(y), incy],
+         "trmv": [order, u, t, dd, n, ptr(A), lda, ptr(x), incx],
+         "tbmv": [order, u, t, dd, n, K, ptr(A), lda, ptr(x), incx],
+         "tpmv": [order, u, t, dd, n, ptr(A), ptr(x), incx],
+         "syr": [order, u, n, c(alpha), ptr(x), incx, ptr(A), lda],
+         "syr2": [order, u, n, c(alpha), ptr(x), incx, ptr(y), incy, ptr(A), lda],
+         "spr": [order, u, n, c(alpha), ptr(x), incx, ptr(A)],
+         "spr2": [order, u, n, c(alpha), ptr(x), incx, ptr(y), incy, ptr(A)],
+         "gbmv": [order, t, m, n, KL, KU, c(alpha), ptr(A), lda, ptr(x), incx, c(beta), ptr(y), incy]}
+    a["trsv"], a["tbsv"], a["tpsv"] = a["trmv"], a["tbmv"], a["tpmv"]
+    getattr(L, f"cblas_{P}{op}")(*a[op])
+
+
+def l2_opts(op):
+    if op in L2_SYM or op in L2_RANK:
+        return [(u, "N", "N") for u in "UL"]
+    if op == "gbmv":
+        return [("U", t, "N") for t in "NT"]
+    return [(u, t, dg) for u in "UL" for t in "NT" for dg in "NU"]
+
+
+def l2_case(rng, dt, op, o, n, K):
+    """Logical operands of one call: (D, x, y, m, KL, KU). D is the logical matrix with the entries the routine reads
+    (band / triangle applied); solves get a well-conditioned D."""
+    uplo, tr, dg = o
+    m, KL, KU = n, 0, 0
+    if op == "gbmv":
+        m, KL, KU = n + 7, 3, K
+    D = rng.uniform(-1, 1, (m, n))
+    ii, jj = np.indices(D.shape)
+    if op == "gbmv":
+        D *= (jj - ii >= -KL) & (jj - ii <= KU)
+    elif op in ("sbmv", "tbmv", "tbsv"):
+        D *= np.abs(jj - ii) <= K
+    if op in ("trsv", "tbsv", "tpsv"):
+        D = D / n
+        D[np.diag_indices(n)] = 1.5 + rng.uniform(0, 1, n)
+    nx = m if (op == "gbmv" and tr == "T") else n
+    ny = n if (op == "gbmv" and tr == "T") else m
+    return D.astype(dt), rng.uniform(-1, 1, nx).astype(dt), rng.uniform(-1, 1, ny).astype(dt), m, KL, KU
+
+
+def l2_ref(op, o, alpha, beta, D, x, y):
+    """float64 result and scale of one call on logical operands (solves: scale None)."""
+    uplo, tr, dg = o
+    D, X, Y = (np.asarray(v, np.float64) for v in (D, x, y))
+    tri = np.tril if uplo == "L" else np.triu
+    if op in L2_SYM:
+        S = tri(D) + tri(D).T - np.diag(np.diag(D))
+        return alpha * S @ X + beta * Y, abs(alpha) * np.abs(S) @ np.abs(X) + abs(beta * Y)
+    if op == "gbmv":
+        Op = D.T if tr == "T" else D
+        return alpha * Op @ X + beta * Y, abs(alpha) * np.abs(Op) @ np.abs(X) + abs(beta * Y)
+    if op in L2_TRI:
+        Tm = tri(D)
+        if dg == "U":
+            np.fill_diagonal(Tm, 1.0)
+        Op = Tm.T if tr == "T" else Tm
+        if op in ("trmv", "tbmv", "tpmv"):
+            return Op @ X, np.abs(Op) @ np.abs(X)
+        from scipy.linalg import solve_triangular
+        return solve_triangular(Op, X, lower=(uplo == "L") != (tr == "T")), None
+    # rank updates: the full logical matrix after the update of the `uplo` triangle
+    upd = np.outer(X, X) if op in ("syr", "spr") else np.outer(X, Y) + np.outer(Y, X)
+    sc = np.outer(np.abs(X), np.abs(X)) if op in ("syr", "spr") else np.outer(np.abs(X), np.abs(Y)) * 2
+    mask = tri(np.ones(D.shape, bool))
+    return np.where(mask, D + alpha * upd, D), np.abs(D) + abs(alpha) * sc
+
+
+def l2_result(op, o, order, A_mem, x_mem, y_mem, n, K, KL, KU, dt):
+    """The logical result read back from memory: the vector (x or y) or, for rank updates, the logical matrix."""
+    host = lambda v: np.asarray(v.cpu().numpy() if hasattr(v, "cpu") else v, np.float64)
+    if op in L2_TRI:
+        return host(x_mem)
+    if op not in L2_RANK:
+        return host(y_mem)
+    a = host(A_mem)
+    uplo = o[0]
+    col = order != ROW
+    fl = {"U": "L", "L": "U"}[uplo] if col else uplo
+    if op in ("syr", "syr2"):
+        return a.T if col else a
+    Tm = np.zeros((n, n))
+    Tm[np.triu_indices(n) if fl == "U" else np.tril_indices(n)] = a
+    return Tm.T if col else Tm
+
+
+def l2_run(L, P, op, o, order, n, K, rng, dt, torch=None, alpha=0.75, beta=-0.5):
+    """One level-2 call through the shim on fresh operands: (error, routes checked by the caller). Solves: error of the
+    solution relative to its max; rank updates: over the updated triangle (full storage: the whole matrix, since the
+    other triangle must stay as it was)."""
+    D, x, y, m, KL, KU = l2_case(rng, dt, op, o, n, K)
+    A_mem, lda = l2_storage(op, D, o[0], K, KL, KU, order)
+    A_mem = np.array(A_mem, dt)
+    xm, ym = x.copy(), y.copy()
+    if torch is not None:
+        A_mem, xm, ym = (torch.from_numpy(v).cuda() for v in (A_mem, xm, ym))
+    call_l2(L, P, order, op, o, m, n, K, KL, KU, alpha, beta, A_mem, lda, xm, 1, ym, 1)   # logical shape, any order
+    if torch is not None:
+        torch.cuda.synchronize()
+    got = l2_result(op, o, order, A_mem, xm, ym, n, K, KL, KU, dt)
+    ref, scale = l2_ref(op, o, alpha, beta, D, x, y)
+    if scale is None:
+        return float(np.abs(got - ref).max() / np.abs(ref).max())
+    if op in ("spr", "spr2"):
+        mask = (np.tril if o[0] == "L" else np.triu)(np.ones((n, n), bool))
+        got, ref, scale = got[mask], ref[mask], scale[mask]
+    return float((np.abs(got - ref) / np.maximum(scale, 1e-300)).max())

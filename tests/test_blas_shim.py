@@ -4,8 +4,8 @@ Checks the reference BLAS layer's contract (reference: lib/src/cblas.c:1-562, li
 on the CPU side: the library loads and finds a CPU BLAS, it exports its own S/D entry points plus a forwarding stub
 for every other BLAS/CBLAS symbol of that CPU BLAS, row- and column-major CBLAS calls and Fortran calls give the
 float64 closed-form results (bounds 1e-5 FP32 / 1e-12 FP64 as in the reference's tests), the level-3 functions the
-shim routes itself (SYMM, SYRK, SYR2K, TRMM, TRSM) pass every option through, and forwarded functions (here ssymv,
-dsymv) work. Without a device the routing sends everything to the CPU, so these run anywhere.
+shim routes itself (SYMM, SYRK, SYR2K, TRMM, TRSM and the symmetric / triangular / band / packed level 2) pass every
+option through, and forwarded functions (here complex GEMV) work. Without a device the routing sends everything to the CPU, so these run anywhere.
 """
 import ctypes
 import os
@@ -111,16 +111,19 @@ def test_mixed_precision_dots(L):
     assert abs(L.cblas_sdsdot(999, 0.5, U.ptr(v), 1, U.ptr(w), 1) - (0.5 + exact)) <= 1e-5 * scale
 
 
-@pytest.mark.parametrize("P", ["s", "d"])
-def test_forwarded_symv(L, P):
-    """A function the shim forwards to the CPU BLAS by a tail jump (not routed): results as BLAS."""
-    dt = DT[P]
-    A = rng.uniform(-1, 1, (30, 30)).astype(dt)
-    S = np.tril(A) + np.tril(A, -1).T            # the lower triangle defines the symmetric matrix
-    x, y = rng.uniform(-1, 1, 30).astype(dt), np.zeros(30, dt)
-    getattr(L, f"cblas_{P}symv")(U.ROW, 122, 30, 1.0, U.ptr(A), 30, U.ptr(x), 1, 0.0, U.ptr(y), 1)
-    S64 = S.astype(np.float64)
-    assert U.ref_error(y, S64 @ x, np.abs(S64) @ np.abs(x)) <= TOL[P]
+@pytest.mark.parametrize("P", ["c", "z"])
+def test_forwarded_complex_gemv(L, P):
+    """A function the shim forwards to the CPU BLAS by a tail jump (complex GEMV: not routed): results as BLAS."""
+    dt = np.complex64 if P == "c" else np.complex128
+    A = (rng.uniform(-1, 1, (30, 20)) + 1j * rng.uniform(-1, 1, (30, 20))).astype(dt)
+    x = (rng.uniform(-1, 1, 20) + 1j * rng.uniform(-1, 1, 20)).astype(dt)
+    y = np.zeros(30, dt)
+    one, zero = np.array([1.0 + 0j], dt), np.array([0j], dt)
+    fn = getattr(L, f"cblas_{P}gemv")
+    fn.argtypes = [U.i, U.i, U.i, U.i, U.p, U.p, U.i, U.p, U.i, U.p, U.p, U.i]
+    fn(U.ROW, U.NT, 30, 20, U.ptr(one), U.ptr(A), 20, U.ptr(x), 1, U.ptr(zero), U.ptr(y), 1)
+    A64 = A.astype(np.complex128)
+    assert U.ref_error(np.abs(y - A64 @ x), 0, np.abs(A64) @ np.abs(x)) <= (1e-5 if P == "c" else 1e-12)
 
 
 @pytest.mark.parametrize("P", ["s", "d"])
@@ -143,3 +146,17 @@ def test_level3_routed_functions_on_cpu(L, P, op):
             assert U.l3_error(op, got, ref, scale, mask) <= tol, (opt, order)
             if mask is not None:
                 assert np.array_equal(got[~mask], C0.astype(np.float64)[~mask]), (opt, order)
+
+
+@pytest.mark.parametrize("P", ["s", "d"])
+@pytest.mark.parametrize("op", U.L2)
+def test_level2_every_option_cpu(L, P, op):
+    """SYMV/SBMV/SPMV, TRMV/TRSV/TBMV/TBSV/TPMV/TPSV, SYR/SYR2/SPR/SPR2 and GBMV through the shim in CBLAS row- and
+    column-major and Fortran, every triangle / transpose / diagonal: without a device every call reaches the CPU BLAS
+    with its own arguments, and the results match the float64 closed forms (this also pins the tests' storage
+    builders against OpenBLAS, the reference's CPU path)."""
+    tol = 1e-4 if P == "s" else 1e-12
+    for o in U.l2_opts(op):
+        for order in (U.ROW, U.COL, "F"):
+            err = U.l2_run(L, P, op, o, order, 30, 4, rng, DT[P])
+            assert err <= tol, (o, order, err)

@@ -155,3 +155,27 @@ def test_level3_device_operands_every_option(L, capfd, torch_dev, P, op):
             err, kept = _l3_run(L, P, op, opt, order, dims, torch_dev)
             assert routes(capfd) == ["GPU"], (opt, order)
             assert err <= tol and kept, (opt, order, err)
+
+
+L2_DIMS = {"symv": (300, 0), "trmv": (300, 0), "trsv": (300, 0), "syr": (300, 0), "syr2": (300, 0),
+           "sbmv": (1500, 50), "tbmv": (1500, 50), "tbsv": (1500, 50), "gbmv": (1500, 50),
+           "spmv": (400, 0), "tpmv": (400, 0), "tpsv": (400, 0), "spr": (400, 0), "spr2": (400, 0)}
+
+
+@pytest.mark.parametrize("P", ["s", "d"])
+@pytest.mark.parametrize("op", U.L2)
+def test_level2_device_operands_every_option(L, capfd, torch_dev, P, op):
+    """Symmetric / triangular / band / packed level 2 with device operands (2^16 elements and more) run on the GPU:
+    every triangle / transpose / diagonal in CBLAS row- and column-major and Fortran, i.e. every mapping of a
+    column-major call onto the row-major library. Host operands stay on the CPU BLAS (one pass over host memory)."""
+    n, K = L2_DIMS[op]
+    tol = 1e-4 if P == "s" else 1e-12
+    for o in U.l2_opts(op):
+        for order in (U.ROW, U.COL, "F"):
+            capfd.readouterr()
+            err = U.l2_run(L, P, op, o, order, n, K, rng, DT[P], torch_dev)
+            assert routes(capfd) == ["GPU"], (o, order)
+            assert err <= tol, (o, order, err)
+    capfd.readouterr()
+    err = U.l2_run(L, P, op, U.l2_opts(op)[0], U.ROW, n, K, rng, DT[P])
+    assert routes(capfd) == ["CPU"] and err <= tol
