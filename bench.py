@@ -38,7 +38,7 @@ GEMM_CASES = {
 }
 QUICK = ("hgemm_n4096", "hgemm_accurate_n4096", "hbm_read_1GiB", "skinny")
 OTHER_CASES = ("hgemm_n4096_host", "hbm_read_1GiB", "skinny", "packed_decode", "level3_n4096", "saxpy_2^26",
-               "sdot_2^26", "sgemv_16384", "copy_256MiB", "calibration")
+               "sdot_2^26", "sgemv_16384", "level2_16384", "copy_256MiB", "calibration")
 
 
 def log(*a):
@@ -303,6 +303,44 @@ def main():
             res[k] = hbm_fracs({"ms": round(ms, 4), "GBs": round(byts / (ms * 1e-3) / 1e9, 1)})
             log(k, res[k])
         del Ad
+
+    if "level2_16384" in cases:
+        # FP32 n = 16384 on device buffers. Algorithmic bytes: the stored triangle once (n(n+1)/2 elements, 512 MiB)
+        # plus the vectors; SYR2 reads and writes the triangle. TRSV restores its right-hand side by a library copy
+        # on the same stream before each solve (64 KiB, inside the timing).
+        m = 16384
+        rng = np.random.default_rng(31)
+        A = rng.uniform(-1, 1, (m, m)).astype(np.float32) / np.float32(m)
+        A[np.diag_indices(m)] = 1.0
+        Ad = to_dev(A)
+        del A
+        Apd = to_dev(np.random.default_rng(32).uniform(-1, 1, m * (m + 1) // 2).astype(np.float32))
+        xv = to_dev(np.random.default_rng(20).uniform(-1, 1, m).astype(np.float32))
+        yv = to_dev(np.random.default_rng(21).uniform(-1, 1, m).astype(np.float32))
+        wv = torch.empty_like(xv)
+        a, ap, x, y, w = (p(t.data_ptr()) for t in (Ad, Apd, xv, yv, wv))
+        tri = 4.0 * m * (m + 1) / 2
+        calls = {
+            "ssymv_L": (tri + 12.0 * m, lambda: check(L.gen9blas_symv(1, 0, m, d(1.0), a, m, x, 1, d(0.0), y, 1))),
+            "ssymv_U": (tri + 12.0 * m, lambda: check(L.gen9blas_symv(1, 1, m, d(1.0), a, m, x, 1, d(0.0), y, 1))),
+            "strmv_LN": (tri + 8.0 * m, lambda: (check(L.gen9blas_copy(1, m, x, 1, w, 1)),
+                                                 check(L.gen9blas_trmv(1, 0, 0, 0, m, a, m, w, 1)))),
+            "strmv_LT": (tri + 8.0 * m, lambda: (check(L.gen9blas_copy(1, m, x, 1, w, 1)),
+                                                 check(L.gen9blas_trmv(1, 0, 1, 0, m, a, m, w, 1)))),
+            "strsv_LN": (tri + 8.0 * m, lambda: (check(L.gen9blas_copy(1, m, x, 1, w, 1)),
+                                                 check(L.gen9blas_trsv(1, 0, 0, 0, m, a, m, w, 1)))),
+            "strsv_LT": (tri + 8.0 * m, lambda: (check(L.gen9blas_copy(1, m, x, 1, w, 1)),
+                                                 check(L.gen9blas_trsv(1, 0, 1, 0, m, a, m, w, 1)))),
+            "sspmv_L": (tri + 12.0 * m, lambda: check(L.gen9blas_spmv(1, 0, m, d(1.0), ap, x, 1, d(0.0), y, 1))),
+            "ssyr2_L": (2 * tri + 8.0 * m, lambda: check(L.gen9blas_syr2(1, 0, m, d(1e-3), x, 1, y, 1, a, m))),
+        }
+        l2 = {}
+        for name, (byts, fn) in calls.items():
+            ms = timed(fn, k=max(5, steps // 2), w=2)
+            l2[name] = hbm_fracs({"ms": round(ms, 4), "GBs": round(byts / (ms * 1e-3) / 1e9, 1)})
+            log("level2", name, l2[name])
+        res["level2_16384"] = l2
+        del Ad, Apd
 
     g9.set_nowait(False)
 

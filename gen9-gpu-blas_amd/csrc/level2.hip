@@ -75,18 +75,22 @@ __device__ __forceinline__ void stored_range(const Shape &s, bool band, int i, i
 
 // ---------------- products ----------------
 constexpr int NT = 256;
-constexpr int U = 8;   // rows per batch: their loads are all issued before the first product
+// Rows per batch: 16 (V > 1: 16 bytes per lane, a wave has 16 KiB of loads outstanding).
+template <int V> constexpr int UB = 16;
 template <class T, int V, int FMT>
-__global__ void __launch_bounds__(NT) mv_kernel(Shape s, const T *__restrict__ a, const T *x, ll ix, int rpp, int dirs,
+__global__ void __launch_bounds__(NT) mv_kernel(Shape s, const T *__restrict__ a, const T *__restrict__ x, ll ix, int rpp, int dirs,
                                                 int skipdiag, typename Comp<T>::R *P, typename Comp<T>::R *Q) {
     using R = typename Comp<T>::R;
     constexpr bool band = FMT == F_BAND;
+    constexpr int U = UB<V>;
     const int lane = threadIdx.x & 63;
-    const int g = blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
-    if ((ll)g * 64 * V >= s.ncols) return;
+    // A workgroup owns column group blockIdx.x and row band blockIdx.y; its waves take consecutive quarters of the
+    // band (the wave index is uniform across a wave: loop bounds derived from it stay in scalar registers).
+    const int g = blockIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g0 = g * 64 * V, g1 = min(g0 + 64 * V, s.ncols) - 1, c0 = g0 + lane * V;
-    // rows whose stored range can reach the group's columns, within this row band
-    int rb = blockIdx.y * rpp, re = min(s.nrows, rb + rpp);
+    const int rpw = rpp / (NT / 64);
+    // rows whose stored range can reach the group's columns, within this wave's quarter of the band
+    int rb = blockIdx.y * rpp + w * rpw, re = min(s.nrows, rb + rpw);
     if (s.tri == TRI_LOWER) rb = max(rb, g0);
     if (s.tri == TRI_UPPER) re = min(re, g1 + 1);
     if (band) {
@@ -99,88 +103,179 @@ __global__ void __launch_bounds__(NT) mv_kernel(Shape s, const T *__restrict__ a
         xc[e] = (dirs & DIR_ROW) && c0 + e < s.ncols ? (R)x[(ll)(c0 + e) * ix] : R(0);
         sc[e] = 0;
     }
-    for (int i = rb; i < re; i += U) {
-        R av[U][V];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int r = i + u;
-            int lo, hi;
-            stored_range(s, band, r, lo, hi);
-            if (r >= re) hi = lo - 1;
-            const T *ar = a + row_start<FMT>(s, r);
-            if constexpr (V > 1) {
-                if (c0 >= lo && c0 + V - 1 <= hi) {
-                    Vec<T> v;
-                    v.u = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(ar + c0));
-#pragma unroll
-                    for (int e = 0; e < V; e++) av[u][e] = (R)v.e[e];
-                } else {
-#pragma unroll
-                    for (int e = 0; e < V; e++) av[u][e] = c0 + e >= lo && c0 + e <= hi ? (R)ar[c0 + e] : R(0);
-                }
-            } else {
-                av[u][0] = c0 >= lo && c0 <= hi ? (R)ar[c0] : R(0);
-            }
+    // Rows [fa, fb) store every column of the group and not its diagonal (the stored range is monotonic in the row
+    // for every layout): they are read whole and used without masks. The other rows, near the diagonal or the band's
+    // edges, take the checked path.
+    int fa = rb, fb = re;
+    if (g0 + 64 * V > s.ncols) {
+        fb = fa;
+    } else {
+        if (band) {
+            fa = max(fa, g1 - s.KU);
+            fb = min(fb, g0 + s.KL + 1);
         }
-        if (dirs & DIR_COL) {
+        if (s.tri == TRI_LOWER) fa = max(fa, g1 + 1);
+        if (s.tri == TRI_UPPER) fb = min(fb, g0);
+    }
+    fa = min(fa, re);                 // inside this band: rb <= fa <= fb <= re
+    fb = max(fa, min(fb, re));
+    fb = fa + (fb - fa) / U * U;      // whole batches
+    auto reduce_rows = [&](int i, int rend, R (&rs)[U]) {
+        int base = 0;
+        butterfly<0, U>(rs, lane, base);
+        if ((lane & (64 / U - 1)) == 0 && i + base < rend) Q[(ll)g * s.nrows + i + base] = rs[0];
+    };
+    // checked rows [r0, r1): an element is read only where stored, a 16-byte chunk whole when it meets the stored
+    // range inside the matrix's columns (its elements outside the range are masked when used)
+    auto checked = [&](int r0, int r1) {
+        for (int i = r0; i < r1; i += U) {
+            T el[U][V];
+            R xr[U];
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                if (i + u >= re) break;
-                const R xr = (R)x[(ll)(i + u) * ix];
+                const int r = i + u;
+                int lo, hi;
+                stored_range(s, band, r, lo, hi);
+                if (r >= r1) hi = lo - 1;
+                const T *ar = a + row_start<FMT>(s, r);
+                if constexpr (V > 1) {
+                    if (c0 <= hi && c0 + V - 1 >= lo && c0 + V <= s.ncols) {
+                        const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(ar + c0));
+                        __builtin_memcpy(el[u], &t, 16);
+                    } else {
 #pragma unroll
-                for (int e = 0; e < V; e++)
-                    if (!skipdiag || c0 + e != i + u) sc[e] = fma_r(av[u][e], xr, sc[e]);
+                        for (int e = 0; e < V; e++) el[u][e] = c0 + e >= lo && c0 + e <= hi ? ar[c0 + e] : T(0);
+                    }
+                } else {
+                    el[u][0] = c0 >= lo && c0 <= hi ? ar[c0] : T(0);
+                }
+                xr[u] = (dirs & DIR_COL) && r < r1 ? (R)x[(ll)r * ix] : R(0);
             }
-        }
-        if (dirs & DIR_ROW) {
             R rs[U];
 #pragma unroll
             for (int u = 0; u < U; u++) {
+                const int r = i + u;
+                int lo, hi;
+                stored_range(s, band, r, lo, hi);
+                if (r >= r1) hi = lo - 1;
                 R t = 0;
 #pragma unroll
-                for (int e = 0; e < V; e++) t = fma_r(av[u][e], xc[e], t);
+                for (int e = 0; e < V; e++) {
+                    const int j = c0 + e;
+                    const R av = j >= lo && j <= hi ? (R)el[u][e] : R(0);
+                    if ((dirs & DIR_COL) && (!skipdiag || j != r)) sc[e] = fma_r(av, xr[u], sc[e]);
+                    t = fma_r(av, xc[e], t);
+                }
                 rs[u] = t;
             }
-            int base = 0;
-            butterfly<0, U>(rs, lane, base);
-            if ((lane & (64 / U - 1)) == 0 && i + base < re) Q[(ll)g * s.nrows + i + base] = rs[0];
+            if (dirs & DIR_ROW) reduce_rows(i, r1, rs);
         }
-    }
-    if (dirs & DIR_COL) {
+    };
+    // unchecked rows: every load of a batch is issued before the first product
+    auto load = [&](int i, T (&el)[U][V], R (&xr)[U]) {
 #pragma unroll
-        for (int e = 0; e < V; e++)
-            if (c0 + e < s.ncols) P[(ll)blockIdx.y * s.ncols + c0 + e] = sc[e];
+        for (int u = 0; u < U; u++) {
+            const T *ar = a + row_start<FMT>(s, i + u) + c0;
+            if constexpr (V > 1) {
+                const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(ar));
+                __builtin_memcpy(el[u], &t, 16);
+            } else {
+                el[u][0] = *ar;
+            }
+            xr[u] = (dirs & DIR_COL) ? (R)x[(ll)(i + u) * ix] : R(0);
+        }
+    };
+    auto use = [&](int i, const T (&el)[U][V], const R (&xr)[U]) {
+        R rs[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            R t = 0;
+#pragma unroll
+            for (int e = 0; e < V; e++) {
+                const R av = (R)el[u][e];
+                if (dirs & DIR_COL) sc[e] = fma_r(av, xr[u], sc[e]);
+                t = fma_r(av, xc[e], t);
+            }
+            rs[u] = t;
+        }
+        if (dirs & DIR_ROW) reduce_rows(i, fb, rs);
+    };
+    checked(rb, fa);
+    for (int i = fa; i < fb; i += U) {
+        T el[U][V];
+        R xr[U];
+        load(i, el, xr);
+        use(i, el, xr);
+    }
+    checked(fb, re);
+    if (dirs & DIR_COL) {   // the band's column sums: the 4 waves' sums added in wave order
+        __shared__ R red[NT / 64][64 * V];
+#pragma unroll
+        for (int e = 0; e < V; e++) red[w][lane * V + e] = sc[e];
+        __syncthreads();
+        if (w == 0) {
+#pragma unroll
+            for (int e = 0; e < V; e++) {
+                R t = red[0][lane * V + e];
+#pragma unroll
+                for (int q = 1; q < NT / 64; q++) t += red[q][lane * V + e];
+                if (c0 + e < s.ncols) P[(ll)blockIdx.y * s.ncols + c0 + e] = t;
+            }
+        }
     }
 }
 
-// y_k = alpha·(Σ_band P[band][k] + Σ_group Q[group][k] (+ x_k for a unit diagonal)) + beta·y_k, partials in index
-// order; y is not read when beta = 0 (reference: level12.cl:280).
+// y_k = alpha·(Σ_band P[band][k] + Σ_group Q[group][k] (+ x_k for a unit diagonal)) + beta·y_k; y is not read when
+// beta = 0 (reference: level12.cl:280). A workgroup takes 64 outputs; wave q adds every 4th partial from the q-th
+// (loads issued 8 at a time), then wave 0 adds the 4 sums in wave order: a fixed order for every output.
 template <class T>
 __global__ void __launch_bounds__(NT) mv_finish(Shape s, int band, int ny, int dirs, int parts, int gw,
                                                 const typename Comp<T>::R *P, const typename Comp<T>::R *Q,
                                                 typename Comp<T>::R alpha, typename Comp<T>::R beta, const T *x, ll ix,
                                                 int add_x, T *y, ll iy) {
     using R = typename Comp<T>::R;
-    const int k = blockIdx.x * NT + threadIdx.x;
-    if (k >= ny) return;
+    constexpr int G = NT / 64;
+    const int lane = threadIdx.x & 63, q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int k = blockIdx.x * 64 + lane;
+    auto sum = [&](const R *base, int first, int last, R t) {   // Σ base[j·ny], j = first + q, first + q + G, ... ≤ last
+        int j = first + q;
+        for (; j + 7 * G <= last; j += 8 * G) {
+            R v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = base[(ll)(j + u * G) * ny];
+#pragma unroll
+            for (int u = 0; u < 8; u++) t += v[u];
+        }
+        for (; j <= last; j += G) t += base[(ll)j * ny];
+        return t;
+    };
     R t = 0;
-    if (dirs & DIR_COL)
-        for (int p = 0; p < parts; p++) t += P[(ll)p * ny + k];
-    if (dirs & DIR_ROW) {
-        int lo, hi;
-        stored_range(s, band, k, lo, hi);
-        if (lo <= hi)
-            for (int g = lo / gw; g <= hi / gw; g++) t += Q[(ll)g * ny + k];
+    if (k < ny) {
+        if (dirs & DIR_COL) t = sum(P + k, 0, parts - 1, t);
+        if (dirs & DIR_ROW) {
+            int lo, hi;
+            stored_range(s, band, k, lo, hi);
+            if (lo <= hi) t = sum(Q + k, lo / gw, hi / gw, t);
+        }
     }
-    if (add_x) t += (R)x[(ll)k * ix];
+    __shared__ R red[G][64];
+    red[q][lane] = t;
+    __syncthreads();
+    if (q != 0 || k >= ny) return;
+    R u = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < G; w++) u += red[w][lane];
+    if (add_x) u += (R)x[(ll)k * ix];
     T *yp = y + (ll)k * iy;
-    *yp = (T)(beta == R(0) ? alpha * t : fma_r(alpha, t, beta * (R)*yp));
+    *yp = (T)(beta == R(0) ? alpha * u : fma_r(alpha, u, beta * (R)*yp));
 }
 
 // ---------------- rank-1 / rank-2 updates of the stored elements ----------------
 // A = alpha·x·yᵀ + A (SYR, SPR: y = x) or alpha·(x·yᵀ + y·xᵀ) + A (SYR2, SPR2) on the stored triangle
-// (reference: level12.cl:466-476, 622-630: fma(alpha·x_i, y_j, a), then fma(alpha·y_i, x_j, ·)).
-template <class T, int FMT>
+// (reference: level12.cl:466-476, 622-630: fma(alpha·x_i, y_j, a), then fma(alpha·y_i, x_j, ·)). V > 1: full
+// storage with 16-byte rows and contiguous x, y: a thread updates 16 bytes of a row at a time, element by element
+// only in the chunks the triangle cuts.
+template <class T, int V, int FMT>
 __global__ void __launch_bounds__(NT) rank_kernel(Shape s, typename Comp<T>::R alpha, const T *x, ll ix, const T *y,
                                                   ll iy, int two, T *a) {
     using R = typename Comp<T>::R;
@@ -190,10 +285,30 @@ __global__ void __launch_bounds__(NT) rank_kernel(Shape s, typename Comp<T>::R a
         const R xi = alpha * (R)x[(ll)i * ix];
         const R yi = two ? alpha * (R)y[(ll)i * iy] : R(0);
         T *ar = a + row_start<FMT>(s, i);
-        for (int j = lo + blockIdx.x * NT + threadIdx.x; j <= hi; j += gridDim.x * NT) {
-            R v = fma_r(xi, (R)y[(ll)j * iy], (R)ar[j]);
-            if (two) v = fma_r(yi, (R)x[(ll)j * ix], v);
-            ar[j] = (T)v;
+        const int step = gridDim.x * NT * V;
+        for (int c = lo / V * V + (blockIdx.x * NT + threadIdx.x) * V; c <= hi; c += step) {
+            if (V > 1 && c >= lo && c + V - 1 <= hi) {
+                Vec<T> av, xv, yv;
+                av.u = *reinterpret_cast<const u32x4 *>(ar + c);
+                yv.u = *reinterpret_cast<const u32x4 *>(y + c);
+                if (two) xv.u = *reinterpret_cast<const u32x4 *>(x + c);
+#pragma unroll
+                for (int e = 0; e < V; e++) {
+                    R v = fma_r(xi, (R)yv.e[e], (R)av.e[e]);
+                    if (two) v = fma_r(yi, (R)xv.e[e], v);
+                    av.e[e] = (T)v;
+                }
+                *reinterpret_cast<u32x4 *>(ar + c) = av.u;
+            } else {
+#pragma unroll
+                for (int e = 0; e < V; e++) {
+                    const int j = c + e;
+                    if (j < lo || j > hi) continue;
+                    R v = fma_r(xi, (R)y[(ll)j * iy], (R)ar[j]);
+                    if (two) v = fma_r(yi, (R)x[(ll)j * ix], v);
+                    ar[j] = (T)v;
+                }
+            }
         }
     }
 }
@@ -220,38 +335,86 @@ __device__ __forceinline__ double lane_value(double v, int k) {
     return __builtin_bit_cast(double, (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
 }
 
-// Diagonal block [p, p + b) of op(A), b ≤ SB: op(A)(p + r, p + c) goes to Lt[c'][r'] (column-major, padded rows
-// against bank conflicts), with r' = r, c' = c for forward substitution (op(A) lower) and both reversed for backward
-// substitution, so the solve below is always forward. The block is read in memory order: along rows of A.
+// Diagonal block [p, p + b) of op(A), b ≤ SB. In solve order (r' = r, c' = c for forward substitution, op(A)
+// lower; both reversed for backward substitution, so the solve below is always forward) the entries below the
+// diagonal, op(A)(p + r, p + c) with c' < r', go to Lt[c'][r'] (column-major, padded rows against bank conflicts);
+// the diagonal goes to dg[r'] and Lt holds zeros on and above it. The block is read along rows of A, a thread's 64
+// loads all in flight at once. The substitution runs in one wave: lane l owns rows l and l + 64 and the reciprocals of
+// their diagonal entries. At step k, x_k = v_k·(1/d_k) is read from lane k and every row subtracts Lt[k][row]·x_k: a
+// row's value stops changing once its own step is past, since its column entries there are zero. Columns are read from
+// LDS 8 steps at a time, so the sequential chain per step is a multiply, a lane read and a fused multiply-add
+// (reference: level12.cl:493-548; the reference divides by the diagonal, here its reciprocal is taken once: the
+// solution differs by rounding only).
 template <class T, int FMT>
 __global__ void __launch_bounds__(NT) solve_block(Shape s, const T *__restrict__ a, int trans, int fwd, int p, int b,
                                                   typename Comp<T>::R *xf) {
     using R = typename Comp<T>::R;
+    constexpr int RPT = SB * SB / NT;   // elements per thread
+    constexpr int KS = 8;               // steps per LDS read
     __shared__ R Lt[SB][SB + 1];
-    for (int e = threadIdx.x; e < b * b; e += NT) {
-        const int q = e / b, w = e % b;
-        // (i, j): element of A, w runs along its row; (r, c): the same element in op(A)
-        const int i = p + q, j = p + w, r = trans ? w : q, c = trans ? q : w;
-        int lo, hi;
-        stored_range(s, FMT == F_BAND, i, lo, hi);
-        const R v = j >= lo && j <= hi ? (R)a[row_start<FMT>(s, i) + j] : R(0);
-        Lt[fwd ? c : b - 1 - c][fwd ? r : b - 1 - r] = v;
+    __shared__ R dg[SB];
+    {
+        // column of A in the block; first row (uniform across a wave: row bounds and offsets are scalar)
+        const int w = threadIdx.x % SB, q0 = __builtin_amdgcn_readfirstlane(threadIdx.x / SB);
+        R v[RPT];
+#pragma unroll
+        for (int u = 0; u < RPT; u++) {
+            const int q = u * (NT / SB) + q0;
+            int lo, hi;
+            stored_range(s, FMT == F_BAND, p + q, lo, hi);
+            v[u] = q < b && w < b && p + w >= lo && p + w <= hi ? (R)a[row_start<FMT>(s, p + q) + p + w] : R(0);
+        }
+#pragma unroll
+        for (int u = 0; u < RPT; u++) {
+            const int q = u * (NT / SB) + q0;
+            // (q, w): element of A in the block; (r, c): the same element in op(A); (r2, c2): in solve order
+            const int r = trans ? w : q, c = trans ? q : w;
+            const int r2 = fwd ? r : b - 1 - r, c2 = fwd ? c : b - 1 - c;
+            if (q < b && w < b) {
+                Lt[c2][r2] = c2 < r2 ? v[u] : R(0);
+                if (c2 == r2) dg[r2] = v[u];
+            }
+        }
     }
     __syncthreads();
     if (threadIdx.x >= 64) return;
-    const int l = threadIdx.x;
+    const int l = threadIdx.x, n0 = b < 64 ? b : 64;
     const auto idx = [&](int r) { return p + (fwd ? r : b - 1 - r); };
-    R v0 = l < b ? xf[idx(l)] : R(0), v1 = l + 64 < b ? xf[idx(l + 64)] : R(0);
-    for (int k = 0; k < b; k++) {
-        R xk = k < 64 ? lane_value(v0, k) : lane_value(v1, k - 64);
-        if (!s.unit) xk = xk / Lt[k][k];
-        if (l == k) v0 = xk;
-        else if (l > k) v0 = fma_r(-Lt[k][l], xk, v0);
-        if (l + 64 == k) v1 = xk;
-        else if (l + 64 > k && l + 64 < b) v1 = fma_r(-Lt[k][l + 64], xk, v1);
+    const bool has1 = l + 64 < b;
+    R v0 = l < b ? xf[idx(l)] : R(0), v1 = has1 ? xf[idx(l + 64)] : R(0);
+    const R r0 = s.unit || l >= b ? R(1) : R(1) / dg[l], r1 = s.unit || !has1 ? R(1) : R(1) / dg[l + 64];
+    // rows at or past b read stale LDS: they belong to lanes whose values are never written back
+    const auto col = [&](int k, int row) { return Lt[k][row]; };
+    int k = 0;
+    for (; k + KS <= n0; k += KS) {
+        R c0[KS], c1[KS];
+#pragma unroll
+        for (int u = 0; u < KS; u++) {
+            c0[u] = col(k + u, l);
+            c1[u] = col(k + u, l + 64);
+        }
+#pragma unroll
+        for (int u = 0; u < KS; u++) {
+            const R xk = lane_value(v0 * r0, k + u);
+            v0 = fma_r(-c0[u], xk, v0);
+            v1 = fma_r(-c1[u], xk, v1);
+        }
     }
-    if (l < b) xf[idx(l)] = v0;
-    if (l + 64 < b) xf[idx(l + 64)] = v1;
+    for (; k < n0; k++) {
+        const R xk = lane_value(v0 * r0, k);
+        v0 = fma_r(-col(k, l), xk, v0);
+        v1 = fma_r(-col(k, l + 64), xk, v1);
+    }
+    for (; k + KS <= b; k += KS) {
+        R c1[KS];
+#pragma unroll
+        for (int u = 0; u < KS; u++) c1[u] = col(k + u, l + 64);
+#pragma unroll
+        for (int u = 0; u < KS; u++) v1 = fma_r(-c1[u], lane_value(v1 * r1, k + u - 64), v1);
+    }
+    for (; k < b; k++) v1 = fma_r(-col(k, l + 64), lane_value(v1 * r1, k - 64), v1);
+    if (l < b) xf[idx(l)] = v0 * r0;
+    if (has1) xf[idx(l + 64)] = v1 * r1;
 }
 
 // x_r -= Σ_{c in [p, p+b)} A(r, c)·x_c for r in [r0, r1) (op(A) = A): a wave takes 8 rows, its lanes the block's
@@ -262,7 +425,7 @@ __global__ void __launch_bounds__(NT) update_rows(Shape s, const T *__restrict__
     using R = typename Comp<T>::R;
     constexpr int RW = 8;
     const int lane = threadIdx.x & 63;
-    const int rbase = r0 + (blockIdx.x * (NT / 64) + (threadIdx.x >> 6)) * RW;
+    const int rbase = r0 + (blockIdx.x * (NT / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * RW;
     if (rbase >= r1) return;
     const int ca = p + lane, cb = p + 64 + lane;
     const R x0 = lane < b ? xf[ca] : R(0), x1 = lane + 64 < b ? xf[cb] : R(0);
@@ -283,21 +446,38 @@ __global__ void __launch_bounds__(NT) update_rows(Shape s, const T *__restrict__
     if ((lane & (64 / RW - 1)) == 0 && rbase + base < r1) xf[rbase + base] -= t[0];
 }
 
-// x_r -= Σ_{c in [p, p+b)} A(c, r)·x_c for r in [r0, r1) (op(A) = Aᵀ): a thread per r, rows c of A in order
-// (neighbouring threads read neighbouring elements of a row).
+// x_r -= Σ_{c in [p, p+b)} A(c, r)·x_c for r in [r0, r1) (op(A) = Aᵀ): a workgroup takes 64 consecutive r, each
+// of its waves 32 of the block's rows c (all 32 loads in flight; neighbouring lanes read neighbouring elements of a
+// row of A), then wave 0 adds the 4 sums in wave order.
 template <class T, int FMT>
 __global__ void __launch_bounds__(NT) update_cols(Shape s, const T *__restrict__ a, int p, int b, int r0, int r1,
                                                   typename Comp<T>::R *xf) {
     using R = typename Comp<T>::R;
-    const int r = r0 + blockIdx.x * NT + threadIdx.x;
-    if (r >= r1) return;
+    constexpr int G = NT / 64, CW = SB / G;
+    const int lane = threadIdx.x & 63, q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = r0 + blockIdx.x * 64 + lane;
     R t = 0;
-    for (int c = p; c < p + b; c++) {
-        int lo, hi;
-        stored_range(s, FMT == F_BAND, c, lo, hi);
-        if (r >= lo && r <= hi) t = fma_r((R)a[row_start<FMT>(s, c) + r], xf[c], t);
+    if (r < r1) {
+        R v[CW];
+#pragma unroll
+        for (int u = 0; u < CW; u++) {
+            const int c = p + q * CW + u;
+            int lo, hi;
+            stored_range(s, FMT == F_BAND, c, lo, hi);
+            v[u] = q * CW + u < b && r >= lo && r <= hi ? (R)a[row_start<FMT>(s, c) + r] : R(0);
+        }
+#pragma unroll
+        for (int u = 0; u < CW; u++)
+            if (q * CW + u < b) t = fma_r(v[u], xf[p + q * CW + u], t);
     }
-    xf[r] -= t;
+    __shared__ R red[G][64];
+    red[q][lane] = t;
+    __syncthreads();
+    if (q != 0 || r >= r1) return;
+    R u = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < G; w++) u += red[w][lane];
+    xf[r] -= u;
 }
 
 // ---------------- launchers ----------------
@@ -323,23 +503,25 @@ static int launch_mv(int es, int fmt, const Shape &s, const void *a, const void 
         const bool vec = fmt == F_FULL && (uintptr_t)a % 16 == 0 && (s.ld * (ll)sizeof(T)) % 16 == 0;
         const int V = vec ? VW<T> : 1, gw = 64 * V;
         const ll groups = (s.ncols + gw - 1) / gw;
-        const unsigned gx = blocks(groups, NT / 64);
-        // about 4 blocks per CU over the row bands (half of them idle on a triangle)
+        // a workgroup per (column group, band of rows), its 4 waves on quarters of the band; about 16 workgroups per
+        // CU, so the dispatcher balances the uneven work of a triangle (about half the workgroups find no rows)
+        constexpr int RU = 16 * (NT / 64);   // a band is whole batches for each wave
         const int cus = num_cus > 0 ? num_cus : 256;
-        ll parts = (4LL * cus + gx - 1) / gx;
-        const ll maxparts = (s.nrows + U - 1) / U;
+        ll parts = (16LL * cus + groups - 1) / groups;
+        const ll maxparts = (s.nrows + RU - 1) / RU;
         if (parts > maxparts) parts = maxparts;
         if (parts < 1) parts = 1;
         if (parts > 65535) parts = 65535;
         ll rpp = (s.nrows + parts - 1) / parts;
-        rpp = (rpp + U - 1) / U * U;
+        rpp = (rpp + RU - 1) / RU * RU;
         parts = (s.nrows + rpp - 1) / rpp;
+        if (groups > 0x7fffffffLL) G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "level 2: %lld column groups", groups);
         void *pp = nullptr, *qq = nullptr;
         if (dirs & DIR_COL) G9_TRY(scratch(SLOT_P, (size_t)parts * s.ncols * sizeof(R), &pp));
         if (dirs & DIR_ROW) G9_TRY(scratch(SLOT_Q, (size_t)groups * s.nrows * sizeof(R), &qq));
         R *P = (R *)pp, *Q = (R *)qq;
         const T *ap = (const T *)a, *xp = (const T *)x;
-        const dim3 grid(gx, (unsigned)parts);
+        const dim3 grid((unsigned)groups, (unsigned)parts);
         G9_TRY(by_fmt(fmt, [&](auto fc) -> int {
             constexpr int FMT = decltype(fc)::value;
             if constexpr (FMT == F_FULL) {
@@ -354,7 +536,7 @@ static int launch_mv(int es, int fmt, const Shape &s, const void *a, const void 
             return 0;
         }));
         G9_HIP(hipGetLastError());
-        hipLaunchKernelGGL((mv_finish<T>), dim3(blocks(ny, NT)), dim3(NT), 0, stream, s, (int)(fmt == F_BAND), ny, dirs,
+        hipLaunchKernelGGL((mv_finish<T>), dim3(blocks(ny, 64)), dim3(NT), 0, stream, s, (int)(fmt == F_BAND), ny, dirs,
                            (int)parts, gw, (const R *)P, (const R *)Q, (R)alpha, (R)beta, xp, ix, add_x, (T *)y, iy);
         G9_HIP(hipGetLastError());
         return 0;
@@ -366,11 +548,22 @@ static int launch_rank(int es, int fmt, const Shape &s, double alpha, const void
     return by_type(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
         using R = typename Comp<T>::R;
-        const dim3 grid(blocks(s.ncols, NT) < 8 ? blocks(s.ncols, NT) : 8, s.nrows < 65535 ? (unsigned)s.nrows : 65535u);
+        const auto al = [](const void *q) { return (uintptr_t)q % 16 == 0; };
+        const bool vec = fmt == F_FULL && al(a) && (s.ld * (ll)sizeof(T)) % 16 == 0 && ix == 1 && iy == 1 && al(x) && al(y);
+        const int V = vec ? VW<T> : 1;
+        const unsigned gx = blocks(s.ncols, NT * V) < 8 ? blocks(s.ncols, NT * V) : 8;
+        const dim3 grid(gx, s.nrows < 65535 ? (unsigned)s.nrows : 65535u);
         G9_TRY(by_fmt(fmt, [&](auto fc) -> int {
             constexpr int FMT = decltype(fc)::value;
-            hipLaunchKernelGGL((rank_kernel<T, FMT>), grid, dim3(NT), 0, stream, s, (R)alpha, (const T *)x, ix, (const T *)y,
-                               iy, two, (T *)a);
+            if constexpr (FMT == F_FULL) {
+                if (vec) {
+                    hipLaunchKernelGGL((rank_kernel<T, VW<T>, FMT>), grid, dim3(NT), 0, stream, s, (R)alpha, (const T *)x, ix,
+                                       (const T *)y, iy, two, (T *)a);
+                    return 0;
+                }
+            }
+            hipLaunchKernelGGL((rank_kernel<T, 1, FMT>), grid, dim3(NT), 0, stream, s, (R)alpha, (const T *)x, ix,
+                               (const T *)y, iy, two, (T *)a);
             return 0;
         }));
         G9_HIP(hipGetLastError());
@@ -407,7 +600,7 @@ static int launch_solve(int es, int fmt, const Shape &s, const void *a, int tran
                 }
                 if (r1 <= r0) continue;
                 if (trans)
-                    hipLaunchKernelGGL((update_cols<T, FMT>), dim3(blocks(r1 - r0, NT)), dim3(NT), 0, stream, s, (const T *)a,
+                    hipLaunchKernelGGL((update_cols<T, FMT>), dim3(blocks(r1 - r0, 64)), dim3(NT), 0, stream, s, (const T *)a,
                                        p, b, r0, r1, xf);
                 else
                     hipLaunchKernelGGL((update_rows<T, FMT>), dim3(blocks(r1 - r0, 8 * (NT / 64))), dim3(NT), 0, stream, s,
