@@ -214,7 +214,7 @@ def main():
             w = np.random.default_rng(100 + c).standard_normal((K, N), dtype=np.float32) * np.float32(0.02)
             Wd = to_dev(w.astype(np.float16))   # K×N, packed once (transB = 0) and then released
             torch.cuda.synchronize()            # the copy ran on torch's stream, pack_b reads on the library's
-            h = L.gen9blas_pack_b(0, 0, K, N, p(Wd.data_ptr()), N)
+            h = L.gen9blas_pack_b(2, 0, K, N, p(Wd.data_ptr()), N)   # GEN9BLAS_HS: also what gemm_pb_skinny takes
             if not h:
                 raise RuntimeError(L.gen9blas_error().decode())
             packs.append(h)
@@ -233,6 +233,27 @@ def main():
             byts = 2.0 * N * K + 2.0 * M * K + 2.0 * M * N
             pk[f"M{M}"] = hbm_fracs({"us_per_call": round(ms * 1e3, 2), "GBs": round(byts / (ms * 1e-3) / 1e9, 1)})
             log("packed_decode", M, pk[f"M{M}"])
+        # gen9blas_gemm_pb_skinny: FP32 activations on the same packed FP16 weights, FP32 result. The call waits for its
+        # kernel (it reports non-finite results), so this time includes the wait and the flag read; the kernel's own
+        # duration is in the rocprofv3 trace (skinny_pb_kernel).
+        L.gen9blas_gemm_pb_skinny.argtypes = [ctypes.c_int, p, ctypes.c_int, p, p, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
+        nfv = ctypes.c_int(0)
+        for M in (1, 4, 16):
+            Af = to_dev(np.random.default_rng(1).standard_normal((M, K), dtype=np.float32))
+            Cf = torch.empty((M, N), dtype=torch.float32, device=dev)
+            state = {"j": 0}
+
+            def fn():
+                j = state["j"]
+                state["j"] = (j + 1) % ncopy
+                check(L.gen9blas_gemm_pb_skinny(M, p(Af.data_ptr()), K, p(packs[j]), p(Cf.data_ptr()), N,
+                                                ctypes.byref(nfv)))
+            ms = timed(fn, k=max(steps, 32) * 2, w=max(warm, 32))
+            byts = 2.0 * N * K + 4.0 * M * K + 4.0 * M * N
+            pk[f"pb_skinny_f32_M{M}"] = hbm_fracs({"us_per_call": round(ms * 1e3, 2),
+                                                   "GBs": round(byts / (ms * 1e-3) / 1e9, 1),
+                                                   "note": "synchronous call (waits, reads the non-finite flag)"})
+            log("packed_decode pb_skinny", M, pk[f"pb_skinny_f32_M{M}"])
         for h in packs:
             L.gen9blas_packed_b_free(p(h))
         res["packed_decode_fp16_4096x4096"] = pk

@@ -47,7 +47,7 @@ def _stale(target, deps):
 
 def build(force=False, jobs=None, verbose=True):
     os.makedirs(BUILD, exist_ok=True)
-    hdr = [os.path.join(CSRC, h) for h in HEADERS] + [os.path.join(INCLUDE, h) for h in ("gen9blas.h", "gen9blas_hip.h")]
+    hdr = [os.path.join(CSRC, h) for h in HEADERS] + [os.path.join(INCLUDE, h) for h in ("gen9blas.h", "gen9blas_hip.h", "gen9blas_ml.h")]
     objs, todo = [], []
     for s in HIP_SOURCES:
         src, obj = os.path.join(CSRC, s), os.path.join(BUILD, s.replace(".hip", ".o"))

@@ -13,6 +13,7 @@
 // with transB = 1 on that matrix. The reference's padded tile layouts, packing bands and spare-buffer pool answer
 // i915 constraints (page zeroing, preemption) that do not exist here.
 #include "internal.h"
+#include "gen9blas_ml.h"
 #include <new>
 
 struct gen9blas_packed_b {
@@ -45,6 +46,87 @@ __global__ void __launch_bounds__(256) pack_bt_kernel(const T *__restrict__ B, l
     for (int r = ty; r < 32; r += 8) {
         const long long n = n0 + r, k = k0 + tx;
         if (n < N && k < ld) P[n * ld + k] = tile[r][tx];
+    }
+}
+
+// ---------------- small batches on packed FP16 weights with FP32 activations ----------------
+// C (M×N) = A (M×K) · Bpᵀ for M ≤ 16 with FP32 activations, FP32 products and sums, FP32 result (reference:
+// lib/src/packed.c:307-329, lib/kernels/hgemm.cl:1392-1436). On the VALU every 16 bytes of weights would cost 8·M FP32
+// FMAs, more than the weight stream leaves time for at M = 16; the FP32 matrix cores take the product instead
+// (FP16 → FP32 is exact, products and sums are FP32). A workgroup of SPW waves owns 16 weight rows and its waves
+// split K in steps of 32. In a step lane l loads 16 bytes of weight row n0 + l%16 (8 k from 8·(l/16)) and the same 8 k
+// of activation row l%16 (zero past M or K); 8 v_mfma_f32_16x16x4_f32 add the step to
+// the wave's 16×16 accumulators, MFMA e taking k = 8·q + e from lane group q (each k of the step once) into chain
+// e % 4 (four independent chains keep the matrix cores busy). A lane then holds D[4·q + r][n0 + l%16], r = 0..3.
+// The chains are added, the waves' sums added in LDS in wave order, and wave 0 writes C, setting *flag for a
+// non-finite result.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4p __attribute__((ext_vector_type(4)));
+constexpr int SPW = 16;  // waves per workgroup
+constexpr int SPB = 8;   // steps per batch: all their loads are issued before the first MFMA
+__global__ void __launch_bounds__(SPW * 64) skinny_pb_kernel(int M, int N, int K, const float *__restrict__ A,
+                                                             long long lda, int avec, const _Float16 *__restrict__ W,
+                                                             long long ldw, int spw, float *__restrict__ C,
+                                                             long long ldc, int *flag) {
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int i = lane & 15, q = lane >> 4, n = blockIdx.x * 16 + i;
+    const bool wrow = n < N, arow = i < M;
+    const _Float16 *wr = W + (long long)(wrow ? n : 0) * ldw;
+    const float *ar = A + (long long)(arow ? i : 0) * lda;
+    floatx4 acc[4];   // four independent chains of MFMAs, added at the end
+#pragma unroll
+    for (int c = 0; c < 4; c++) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int s0 = w * spw;
+    for (int sb = s0; sb < s0 + spw; sb += SPB) {
+        u32x4p wq[SPB];
+        float av[SPB][8];
+#pragma unroll
+        for (int b = 0; b < SPB; b++) {
+            const int k = (sb + b) * 32 + 8 * q;
+            const u32x4p z = {0u, 0u, 0u, 0u};
+            // packed rows hold ldw ≥ K elements (zeros past K, ldw a multiple of 64): k < ldw keeps k + 7 inside
+            wq[b] = wrow && k < ldw ? *reinterpret_cast<const u32x4p *>(wr + k) : z;
+            if (avec && arow && k + 8 <= K) {
+                const u32x4p a0 = *reinterpret_cast<const u32x4p *>(ar + k);
+                const u32x4p a1 = *reinterpret_cast<const u32x4p *>(ar + k + 4);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const unsigned x0 = a0[e], x1 = a1[e];
+                    av[b][e] = __builtin_bit_cast(float, x0);
+                    av[b][e + 4] = __builtin_bit_cast(float, x1);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) av[b][e] = arow && k + e < K ? ar[k + e] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < SPB; b++) {
+            float we[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const unsigned h2 = wq[b][e / 2];
+                const unsigned short h = e % 2 ? (unsigned short)(h2 >> 16) : (unsigned short)(h2 & 0xffffu);
+                we[e] = (float)__builtin_bit_cast(_Float16, h);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[e % 4] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[b][e], we[e], acc[e % 4], 0, 0, 0);
+        }
+    }
+    __shared__ float part[SPW][4][64];
+#pragma unroll
+    for (int r = 0; r < 4; r++) part[w][r][lane] = (acc[0][r] + acc[1][r]) + (acc[2][r] + acc[3][r]);
+    __syncthreads();
+    if (w != 0 || !wrow) return;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int m = 4 * q + r;
+        if (m >= M) continue;
+        float t = part[0][r][lane];
+#pragma unroll
+        for (int v = 1; v < SPW; v++) t += part[v][r][lane];
+        C[(long long)m * ldc + n] = t;
+        if (!__builtin_isfinite(t)) *flag = 1;   // every writer stores the same value
     }
 }
 
@@ -121,6 +203,55 @@ int gen9blas_gemm_pb(int transA, int M, double alpha, const void *A, int lda, co
     G9_TRY(begin());
     if (!Bp) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "gemm_pb: no packed B");
     return gemm_impl(Bp->type, transA, 1, M, Bp->N, Bp->K, alpha, A, lda, 0, Bp->buf, (int)Bp->ld, 0, beta, C, ldc, 0, 1);
+}
+
+// Small batches on HS-packed weights (reference: lib/src/packed.c:307-329): DECLINED outside 1 ≤ M ≤ 16, a B not
+// packed as GEN9BLAS_HS is INVALID_ARG. Always waits: *nonfinite is known only after the kernel. The non-finite flag
+// is a word of pinned, coherent host memory that the kernel writes directly (only for a non-finite result); it is
+// zero at the start of every call (the host clears it after a call that set it), so no copy is needed to read it.
+int gen9blas_gemm_pb_skinny(int M, const float *A, int lda, const gen9blas_packed_b *Bp, float *C, int ldc,
+                            int *nonfinite) {
+    const double t0 = now_s();
+    G9_TRY(begin());
+    if (!Bp || Bp->type != GEN9BLAS_HS) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "gemm_pb_skinny: needs B packed as GEN9BLAS_HS");
+    if (M < 1 || M > 16) return GEN9BLAS_DECLINED;
+    if (!A || !C || !nonfinite) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "gemm_pb_skinny: NULL pointer");
+    const int K = Bp->K, N = Bp->N;
+    if (lda < K || ldc < N) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "gemm_pb_skinny: lda %d < K %d or ldc %d < N %d", lda, K, ldc, N);
+    *nonfinite = 0;
+    static volatile int *flag;
+    if (!flag) {
+        void *h = nullptr;
+        G9_HIP(hipHostMalloc(&h, 256, hipHostMallocCoherent));
+        flag = (volatile int *)h;
+        *flag = 0;
+    }
+    Operand o[2];
+    o[0].host = A; o[0].es = 4; o[0].rows = M; o[0].cols = K; o[0].caller_ld = lda;
+    o[1].host = C; o[1].es = 4; o[1].rows = M; o[1].cols = N; o[1].caller_ld = ldc;
+    G9_TRY(resolve(o[0], SLOT_A, true, false, true));
+    G9_TRY(resolve(o[1], SLOT_C, ldc != N, true, true));
+    const int steps = (K + 31) / 32;
+    int spw = (steps + SPW - 1) / SPW;
+    spw = (spw + SPB - 1) / SPB * SPB;
+    const bool avec = (uintptr_t)o[0].dev % 16 == 0 && o[0].ld % 4 == 0;
+    prof_begin();
+    hipLaunchKernelGGL(skinny_pb_kernel, dim3((unsigned)((N + 15) / 16)), dim3(SPW * 64), 0, stream, M, N, K,
+                       (const float *)o[0].dev, o[0].ld, (int)avec, (const _Float16 *)Bp->buf, Bp->ld, spw,
+                       (float *)o[1].dev, o[1].ld, (int *)flag);
+    G9_HIP(hipGetLastError());
+    prof_end();
+    const int saved = nowait;
+    nowait = 0;   // the flag is read after the kernel
+    const int r = finish(o, 2);
+    nowait = saved;
+    G9_TRY(r);
+    if (*flag) {
+        *nonfinite = 1;
+        *flag = 0;
+    }
+    prof_collect(t0);
+    return 0;
 }
 
 void gen9blas_packed_b_free(gen9blas_packed_b *Bp) {

@@ -260,8 +260,9 @@ int gen9blas_has(int f) {
     switch (f) {
     case GEN9BLAS_FEAT_FP16:
     case GEN9BLAS_FEAT_FP32:
-    case GEN9BLAS_FEAT_FP64: return 1;
-    default: return 0;   // the ML/packed-weight features of the reference are not part of this library
+    case GEN9BLAS_FEAT_FP64:
+    case GEN9BLAS_FEAT_SKINNY_PB: return 1;
+    default: return 0;   // the other ML features of the reference are not part of this library
     }
 }
 

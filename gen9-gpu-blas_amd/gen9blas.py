@@ -50,6 +50,7 @@ _lib.gen9blas_pack_b.argtypes = [_i, _i, _i, _i, _p, _i]
 _lib.gen9blas_pack_b.restype = _p
 _lib.gen9blas_gemm_pb.argtypes = [_i, _i, _d, _p, _i, _p, _d, _p, _i]
 _lib.gen9blas_packed_b_free.argtypes = [_p]
+_lib.gen9blas_gemm_pb_skinny.argtypes = [_i, _p, _i, _p, _p, _i, ctypes.POINTER(_i)]   # gen9blas_ml.h
 GEN9BLAS_H, GEN9BLAS_S, GEN9BLAS_HS, GEN9BLAS_D = 0, 1, 2, 3
 FEAT_FP16, FEAT_FP32, FEAT_FP64 = 0, 1, 2
 _lib.gen9blas_version.restype = ctypes.c_int

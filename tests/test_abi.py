@@ -16,7 +16,7 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.realpath(__file__)))
 LIB = os.path.join(ROOT, "gen9-gpu-blas_amd", "libgen9blas.so")
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("gen9blas.h", "gen9blas_hip.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("gen9blas.h", "gen9blas_hip.h", "gen9blas_ml.h")]
 
 
 def declared():
@@ -59,7 +59,8 @@ def test_header_declares_the_reference_surface():
               "gen9blas_has", "gen9blas_error", "gen9blas_last_status", "gen9blas_last_time_ms",
               "gen9blas_last_zero_copy", "gen9blas_alloc", "gen9blas_free", "gen9blas_is_usm"):
         assert f in names, f
-    assert len(names) == 59
+    assert "gen9blas_gemm_pb_skinny" in names   # the packed-weight decode entry of the reference's ML header
+    assert len(names) == 60
 
 
 def test_exports_exactly_the_header(lib):

@@ -122,3 +122,74 @@ def test_pack_b_arguments(g9):
     assert L.gen9blas_gemm_pb(0, 0, 1.0, b.ctypes.data, 8, P, 0.0, c.ctypes.data, 8) == 0   # M = 0: no-op
     assert (c == -1).all()
     L.gen9blas_packed_b_free(P)
+
+
+def _skinny_pb(L, M, A, P, N, C=None, ldc=None):
+    C = np.full((M, N), np.nan, np.float32) if C is None else C
+    nf = ctypes.c_int(-1)
+    rc = L.gen9blas_gemm_pb_skinny(M, A.ctypes.data, A.shape[1], P, C.ctypes.data, ldc or N, ctypes.byref(nf))
+    return rc, C, nf.value
+
+
+@pytest.mark.parametrize("N,K", [(1024, 1024), (256, 1024), (3072, 1024), (1024, 3072), (1000, 1000), (37, 96),
+                                 (4096, 4096)])
+def test_gemm_pb_skinny(g9, N, K):
+    """gen9blas_gemm_pb_skinny (reference: lib/test_skinny_pb.py:52-75): weights W[N][K] FP16 packed as GEN9BLAS_HS with
+    transB = 1, FP32 activations, M = 1..16; error against the float64 product relative to |A|·|Wᵀ| under 1e-5 (the
+    reference's bound), no non-finite result."""
+    L = g9._lib
+    assert L.gen9blas_has(3) == 1   # GEN9BLAS_FEAT_SKINNY_PB
+    rng = np.random.default_rng(11)
+    W = (rng.standard_normal((N, K)) * 0.05).astype(np.float16)
+    P, _, _ = _pack(L, HS, W, 1)
+    try:
+        W64 = W.astype(np.float64)
+        for M in (1, 2, 3, 4, 5, 8, 9, 12, 16):
+            A = rng.standard_normal((M, K)).astype(np.float32)
+            rc, C, nf = _skinny_pb(L, M, A, P, N)
+            assert rc == 0, L.gen9blas_error()
+            ref = A.astype(np.float64) @ W64.T
+            mag = np.abs(A.astype(np.float64)) @ np.abs(W64.T)
+            err = float(np.max(np.abs(C - ref) / mag))
+            assert err < 1e-5 and nf == 0 and np.isfinite(C).all(), f"M={M}: rel err {err:.1e}, nonfinite {nf}"
+    finally:
+        L.gen9blas_packed_b_free(P)
+
+
+def test_gemm_pb_skinny_flags_and_arguments(g9, torch_dev):
+    """A non-finite result sets *nonfinite and the next call starts clean; M outside 1..16 is DECLINED (1) with nothing
+    written; a B packed as another type is INVALID_ARG; device-resident A and C are used in place, with row strides."""
+    L = g9._lib
+    rng = np.random.default_rng(3)
+    N, K = 300, 520
+    W = (rng.standard_normal((N, K)) * 0.05).astype(np.float16)
+    P, _, _ = _pack(L, HS, W, 1)
+    Ph, _, _ = _pack(L, H, W, 1)
+    try:
+        A = rng.standard_normal((4, K)).astype(np.float32)
+        A[2, 17] = np.inf
+        rc, C, nf = _skinny_pb(L, 4, A, P, N)
+        assert rc == 0 and nf == 1 and not np.isfinite(C[2]).all() and np.isfinite(C[[0, 1, 3]]).all()
+        A[2, 17] = 1.0
+        rc, C, nf = _skinny_pb(L, 4, A, P, N)
+        assert rc == 0 and nf == 0 and np.isfinite(C).all()
+        for M in (0, 17):
+            Z = np.zeros((max(M, 1), K), np.float32)
+            rc, C, nf = _skinny_pb(L, M, Z, P, N, C=np.full((max(M, 1), N), 7.0, np.float32))
+            assert rc == 1 and (C == 7.0).all()
+        rc, _, _ = _skinny_pb(L, 4, A, Ph, N)
+        assert rc == -3
+        torch = torch_dev
+        Ab = rng.standard_normal((16, K + 12)).astype(np.float32)
+        Ad = torch.from_numpy(Ab).cuda()
+        Cd = torch.full((16, N + 5), 3.0, dtype=torch.float32, device="cuda")
+        nf = ctypes.c_int(-1)
+        assert L.gen9blas_gemm_pb_skinny(16, ctypes.c_void_p(Ad.data_ptr()), K + 12, P, ctypes.c_void_p(Cd.data_ptr()),
+                                         N + 5, ctypes.byref(nf)) == 0 and nf.value == 0
+        C = Cd.cpu().numpy()
+        ref = Ab[:, :K].astype(np.float64) @ W.astype(np.float64).T
+        mag = np.abs(Ab[:, :K].astype(np.float64)) @ np.abs(W.astype(np.float64)).T
+        assert float(np.max(np.abs(C[:, :N] - ref) / mag)) < 1e-5 and (C[:, N:] == 3.0).all()
+    finally:
+        L.gen9blas_packed_b_free(P)
+        L.gen9blas_packed_b_free(Ph)
