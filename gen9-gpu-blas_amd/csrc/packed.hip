@@ -14,6 +14,7 @@
 // i915 constraints (page zeroing, preemption) that do not exist here.
 #include "internal.h"
 #include "gen9blas_ml.h"
+#include "lds_dma.h"
 #include <new>
 
 struct gen9blas_packed_b {
@@ -130,6 +131,111 @@ __global__ void __launch_bounds__(SPW * 64) skinny_pb_kernel(int M, int N, int K
     }
 }
 
+// The same product with the weight and activation tiles streamed through LDS (K % 128 == 0, 16-byte aligned
+// activation rows): a workgroup of SKS waves owns 16 weight rows; its waves take groups of 128 k round robin, and
+// each wave streams its groups through a private NSP-stage LDS ring with global_load_lds_dwordx4: per group 4 copies
+// of 1 KiB bring 16 weight rows × 256 bytes (4 rows per copy, contiguous in memory) and MT/2 copies bring MT
+// activation rows × 512 bytes (2 rows per copy). Chunk c (16 bytes) of row r sits at position c ^ (r % 16) of the
+// row, so the 16 lanes that read one chunk of 16 rows hit distinct banks. Per 32 k, lane (i = l%16, q = l/16) reads
+// 8 FP16 weights of row n0 + i and 8 FP32 activations of row i at k = 8·q .. 8·q+7, and 8 v_mfma_f32_16x16x4_f32
+// add them (MFMA e takes k = 8·q + e from lane group q) into chain e % 4 of four independent chains. A wave reads only
+// what it copied itself, so no barrier is needed until the waves' 16×16 sums are added in LDS in wave order.
+template <int MT, int SKS, int NSP>
+__global__ void __launch_bounds__(SKS * 64) skinny_pb_lds_kernel(int M, int N, int K, const float *__restrict__ A,
+                                                                 long long lda, const _Float16 *__restrict__ W,
+                                                                 long long ldw, float *__restrict__ C, long long ldc,
+                                                                 int *flag) {
+    constexpr int GK = 128, WROW = GK * 2, AROW = GK * 4;   // bytes of a weight / activation row per group
+    constexpr int NWC = 16 * WROW / 1024, NAC = (MT + 1) / 2;   // copies per group
+    constexpr int WB = 16 * WROW, SB = WB + NAC * 1024, LPG = NWC + NAC;
+    static_assert((NSP - 1) * LPG < 64, "copies in flight must fit vmcnt");
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[SKS * NSP * SB];
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int i = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const unsigned lbase = (unsigned)(uintptr_t)smem + wv * NSP * SB;
+    const G9_LDS unsigned char *lds = (const G9_LDS unsigned char *)smem + wv * NSP * SB;
+    const int G = K / GK, ng = G > wv ? (G - wv + SKS - 1) / SKS : 0;
+    // weight copy c: rows 4c + L/16, position L % 16; activation copy c: rows 2c + L/32, position L % 32. Rows past N
+    // (M) load the last valid row: their results are not stored (activations: zeroed before use).
+    unsigned woff[NWC], aoff[NAC];
+#pragma unroll
+    for (int c = 0; c < NWC; c++) {
+        const int r = 4 * c + (lane >> 4), rr = min(n0 + r, N - 1) - n0;
+        woff[c] = (unsigned)((long long)rr * ldw * 2 + (((lane & 15) ^ r) << 4));
+    }
+#pragma unroll
+    for (int c = 0; c < NAC; c++) {
+        const int r = 2 * c + (lane >> 5), rr = min(r, M - 1);
+        aoff[c] = (unsigned)((long long)rr * lda * 4 + (((lane & 31) ^ (r & 15)) << 4));
+    }
+    const char *wb = reinterpret_cast<const char *>(W + (long long)n0 * ldw);
+    const char *ab = reinterpret_cast<const char *>(A);
+    auto issue = [&](int j, int st) {   // group wv + SKS·j into stage st
+        const int gg = wv + SKS * j;
+        const unsigned dst = lbase + st * SB;
+#pragma unroll
+        for (int c = 0; c < NWC; c++) lds_dma16(wb + (long long)gg * WROW, woff[c], dst + c * 1024);
+#pragma unroll
+        for (int c = 0; c < NAC; c++) lds_dma16(ab + (long long)gg * AROW, aoff[c], dst + WB + c * 1024);
+    };
+    floatx4 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // rows of D past M come from duplicated activation rows: they are computed and never stored
+    const int arow = i < MT ? i : 0;
+#pragma unroll
+    for (int st = 0; st < NSP; st++)
+        if (st < ng) issue(st, st);
+    int st = 0;
+    for (int j = 0; j < ng; j++) {
+        wait_vm_stages<NSP - 1, LPG>(min(NSP - 1, ng - 1 - j));   // group j has landed
+        const G9_LDS unsigned char *sg = lds + st * SB;
+        u32x4p wf[4], af0[4], af1[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int c = 4 * t + q;   // 16-byte weight chunk of the row; activation chunks 2c, 2c + 1
+            wf[t] = *reinterpret_cast<const G9_LDS u32x4p *>(sg + i * WROW + ((c ^ i) << 4));
+            af0[t] = *reinterpret_cast<const G9_LDS u32x4p *>(sg + WB + arow * AROW + (((2 * c) ^ arow) << 4));
+            af1[t] = *reinterpret_cast<const G9_LDS u32x4p *>(sg + WB + arow * AROW + (((2 * c + 1) ^ arow) << 4));
+        }
+        __builtin_amdgcn_sched_barrier(0);   // all fragment reads are issued before the first MFMA
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const unsigned h2 = wf[t][e / 2];
+                const unsigned short h = e % 2 ? (unsigned short)(h2 >> 16) : (unsigned short)(h2 & 0xffffu);
+                const unsigned ab32 = e < 4 ? af0[t][e] : af1[t][e - 4];
+                // consecutive MFMAs go to different chains, so none waits for the one before
+                acc[e % 4] = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, ab32),
+                                                                  (float)__builtin_bit_cast(_Float16, h), acc[e % 4], 0, 0, 0);
+            }
+        }
+        wait_lgkm0();   // the stage is refilled next: its reads must be done
+        if (j + NSP < ng) issue(j + NSP, st);
+        st = st + 1 == NSP ? 0 : st + 1;
+    }
+    // lane holds D[m = 4q + r][n0 + i]; sum the chains, then the waves' tiles in wave order
+    __syncthreads();
+    float *part = reinterpret_cast<float *>(smem);   // [SKS][4][64]
+#pragma unroll
+    for (int r = 0; r < 4; r++) part[(wv * 4 + r) * 64 + lane] = (acc[0][r] + acc[1][r]) + (acc[2][r] + acc[3][r]);
+    __syncthreads();
+    const int n = n0 + i;
+    if (wv != 0 || n >= N) return;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int m = 4 * q + r;
+        if (m >= M) continue;
+        float t = part[r * 64 + lane];
+#pragma unroll
+        for (int v = 1; v < SKS; v++) t += part[(v * 4 + r) * 64 + lane];
+        C[(long long)m * ldc + n] = t;
+        if (!__builtin_isfinite(t)) *flag = 1;
+    }
+}
+
 }  // namespace g9
 
 using namespace g9;
@@ -236,9 +342,20 @@ int gen9blas_gemm_pb_skinny(int M, const float *A, int lda, const gen9blas_packe
     spw = (spw + SPB - 1) / SPB * SPB;
     const bool avec = (uintptr_t)o[0].dev % 16 == 0 && o[0].ld % 4 == 0;
     prof_begin();
-    hipLaunchKernelGGL(skinny_pb_kernel, dim3((unsigned)((N + 15) / 16)), dim3(SPW * 64), 0, stream, M, N, K,
-                       (const float *)o[0].dev, o[0].ld, (int)avec, (const _Float16 *)Bp->buf, Bp->ld, spw,
-                       (float *)o[1].dev, o[1].ld, (int *)flag);
+    const dim3 grid((unsigned)((N + 15) / 16));
+    const float *ad = (const float *)o[0].dev;
+    const _Float16 *wd = (const _Float16 *)Bp->buf;
+    float *cd = (float *)o[1].dev;
+    // the LDS-streaming kernel: whole 128-k groups, 16-byte activation rows, 32-bit per-lane offsets
+    if (K % 128 == 0 && avec && 16LL * (Bp->ld * 2 + o[0].ld * 4) < (1LL << 32)) {
+        // three stages: deeper rings (6 at M <= 4) measured slower on MI355X
+        if (M <= 4) hipLaunchKernelGGL((skinny_pb_lds_kernel<4, 4, 3>), grid, dim3(4 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
+        else if (M <= 8) hipLaunchKernelGGL((skinny_pb_lds_kernel<8, 4, 3>), grid, dim3(4 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
+        else hipLaunchKernelGGL((skinny_pb_lds_kernel<16, 4, 3>), grid, dim3(4 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
+    } else {
+        hipLaunchKernelGGL(skinny_pb_kernel, grid, dim3(SPW * 64), 0, stream, M, N, K, ad, o[0].ld, (int)avec, wd, Bp->ld,
+                           spw, cd, o[1].ld, (int *)flag);
+    }
     G9_HIP(hipGetLastError());
     prof_end();
     const int saved = nowait;
