@@ -11,10 +11,12 @@ namespace g9 {
 
 // ---------------- host side ----------------
 // Tile configurations, per element type and layout, from a sweep on MI355X at n = 4096 (every variant checked against
-// a float64 reference). Big: the steady-state configuration. Small: 128-row tiles for products whose big tiles
+// a float64 reference). Big: the steady-state configuration. Small: smaller tiles for products whose big tiles
 // would leave most of the 256 CUs idle.
 //   FP16 256×256, 8 waves (4×2): NN 794, NT 950 TFLOP/s. FP32 256×128 (NN 117) / 128×128 (NT 127).
 //   FP64 256×128, 8 waves (4×2): 70.6 TFLOP/s.
+//   Small at n = 1024 (NN): FP32 64×64 (256 tiles, no split) 69 TFLOP/s against 62 for 128×128 split four ways;
+//   FP64 64×128 split two ways 43, 64×64 41.
 struct TileCfg { int BM, BN, WM, WN; };
 // Layouts whose staging needs more registers than a wave has at 2 waves per SIMD (transposed A, unaligned
 // operands) keep FP16 at 4 waves (512 registers per wave), which compiles without spills.
@@ -25,7 +27,7 @@ template <bool AK, bool BKC, bool VEC> struct Cfg<f16, AK, BKC, VEC> {
 };
 template <bool AK, bool BKC, bool VEC> struct Cfg<float, AK, BKC, VEC> {
     static constexpr TileCfg big = (AK && BKC) ? TileCfg{128, 128, 2, 2} : TileCfg{256, 128, 2, 2};
-    static constexpr TileCfg small{128, 128, 2, 2};
+    static constexpr TileCfg small{64, 64, 2, 2};
 };
 template <bool AK, bool BKC, bool VEC> struct Cfg<double, AK, BKC, VEC> {
     static constexpr TileCfg big{256, 128, 4, 2}, small{64, 128, 2, 2};

@@ -68,14 +68,16 @@ def test_status_codes(L):
     assert L.gen9blas_gemm(1, 0, 0, 8, 8, 8, 1.0, pa, 8, pb, 8, 0.0, pc, 8) == OK   # errors are not sticky
 
 
-def test_functions_outside_this_build_report_unsupported(L):
-    """Entry points of the reference ABI that this build exports without computing them return UNSUPPORTED (so the
-    BLAS shim falls back to the CPU), after the same type check as the reference."""
-    a = np.eye(8, dtype=np.float32)
-    x = np.ones(8, np.float32)
+def test_level23_type_check_and_host_operands(L):
+    """Level 2 / level 3 entry points check the type first, as the reference does (UNSUPPORTED, with the type in the
+    message), and compute on host memory like every other entry point (reference: lib/src/level12.c, level3.c)."""
+    a = np.eye(8, dtype=np.float32) * 2
+    x = np.arange(8, dtype=np.float32)
+    y = np.zeros(8, np.float32)
     d = ctypes.c_double
-    assert L.gen9blas_symv(1, 0, 8, d(1.0), a.ctypes.data, 8, x.ctypes.data, 1, d(0.0), x.ctypes.data, 1) == UNSUPPORTED
-    assert L.gen9blas_symv(9, 0, 8, d(1.0), a.ctypes.data, 8, x.ctypes.data, 1, d(0.0), x.ctypes.data, 1) == UNSUPPORTED
+    assert L.gen9blas_symv(1, 0, 8, d(1.0), a.ctypes.data, 8, x.ctypes.data, 1, d(0.0), y.ctypes.data, 1) == OK
+    assert np.array_equal(y, 2 * x)
+    assert L.gen9blas_symv(9, 0, 8, d(1.0), a.ctypes.data, 8, x.ctypes.data, 1, d(0.0), y.ctypes.data, 1) == UNSUPPORTED
     assert b"type 9" in L.gen9blas_error()
     assert L.gen9blas_symm(9, 0, 0, 8, 8, d(1.0), a.ctypes.data, 8, a.ctypes.data, 8, d(0.0), a.ctypes.data, 8) == UNSUPPORTED
     assert b"type 9" in L.gen9blas_error()
