@@ -19,12 +19,14 @@
 // fixed order and applies alpha / beta once, so results do not depend on scheduling. FP16 is computed in FP32 as in
 // the reference (level12.cl:1-3).
 //
-// Triangular solves run over diagonal blocks of 128 rows: one workgroup loads the block of op(A) into LDS and one
-// wave substitutes (lanes own rows, the solved value of each step is broadcast from its lane), then the rows after
-// the block are updated in parallel, two launches per block as in the reference (level12.c:303-347). The work
+// Triangular solves run over diagonal blocks of 128 rows, one launch per block: one workgroup applies the previous
+// block's update to this block's rows, loads the block of op(A) into LDS and one wave substitutes (lanes own rows,
+// the solved value of each step is broadcast from its lane), while the other workgroups apply the previous block's
+// update to the rows beyond (the reference alternates a solve and an update launch: level12.c:303-347). The work
 // vector is FP32 (FP64 for FP64), also for FP16 (level12.c:301).
 #include "internal.h"
 #include "wave.h"
+#include <algorithm>
 #include <type_traits>
 
 namespace g9 {
@@ -346,86 +348,148 @@ __device__ __forceinline__ double lane_value(double v, int k) {
 // (reference: level12.cl:493-548; the reference divides by the diagonal, here its reciprocal is taken once: the
 // solution differs by rounding only).
 template <class T, int FMT>
-__global__ void __launch_bounds__(NT) solve_block(Shape s, const T *__restrict__ a, int trans, int fwd, int p, int b,
-                                                  typename Comp<T>::R *xf) {
+struct Diag {
     using R = typename Comp<T>::R;
-    constexpr int RPT = SB * SB / NT;   // elements per thread
-    constexpr int KS = 8;               // steps per LDS read
-    __shared__ R Lt[SB][SB + 1];
-    __shared__ R dg[SB];
-    {
-        // column of A in the block; first row (uniform across a wave: row bounds and offsets are scalar)
+    static constexpr int RPT = SB * SB / NT;   // elements per thread
+    static constexpr int KS = 8;               // steps per LDS read
+    T e[RPT];
+
+    // Column w of A in the block; first row q0 (uniform across a wave: row offsets are scalar). Element (q, w),
+    // A(p + q, p + w), is needed where it lies in A's stored triangle (the solve uses no other entry) and, for a
+    // band, inside the band; elsewhere the value is zero. Every lane loads, without a branch, from an address
+    // clamped into storage: rows past the block re-read its last row, and outside full storage the column is
+    // clamped into the row's stored entries (the diagonal is always among them: a unit diagonal that is not
+    // referenced is still in storage). The values that are not needed are replaced by zero when placed.
+    __device__ __forceinline__ void load(const Shape &s, const T *__restrict__ a, int p, int b) {
         const int w = threadIdx.x % SB, q0 = __builtin_amdgcn_readfirstlane(threadIdx.x / SB);
-        R v[RPT];
+        const bool lowA = s.tri == TRI_LOWER;
+        const int bw = lowA ? s.KL : s.KU;   // band width on the stored side
 #pragma unroll
         for (int u = 0; u < RPT; u++) {
-            const int q = u * (NT / SB) + q0;
-            int lo, hi;
-            stored_range(s, FMT == F_BAND, p + q, lo, hi);
-            v[u] = q < b && w < b && p + w >= lo && p + w <= hi ? (R)a[row_start<FMT>(s, p + q) + p + w] : R(0);
+            const int q = min(u * (NT / SB) + q0, b - 1);
+            int c = min(w, b - 1);
+            if constexpr (FMT != F_FULL) {
+                c = lowA ? min(c, q) : max(c, q);
+                if constexpr (FMT == F_BAND) c = lowA ? max(c, q - bw) : min(c, q + bw);
+            }
+            e[u] = a[row_start<FMT>(s, p + q) + p + c];
         }
+    }
+
+    // (q, w): element of A in the block; (r, c): the same element in op(A); (r2, c2): in solve order. The four
+    // (transpose, direction) cases are separate loops, so each index is a register or a constant offset. Indices at
+    // or past b (a partial block) wrap to [b, SB) under backward order: a column there is never read and a row there
+    // belongs to a lane whose value is dropped, and the zero stored there meets no entry in use.
+    template <bool TR, bool FW>
+    __device__ __forceinline__ void place(const Shape &s, int b, R (*Lt)[SB + 1], R *dg) const {
+        constexpr bool LOW = TR != FW;   // A's stored triangle: op(A) is lower (forward) iff A lower xor transposed
+        const int w = threadIdx.x % SB, q0 = __builtin_amdgcn_readfirstlane(threadIdx.x / SB);
+        const int bw = LOW ? s.KL : s.KU;
 #pragma unroll
         for (int u = 0; u < RPT; u++) {
             const int q = u * (NT / SB) + q0;
-            // (q, w): element of A in the block; (r, c): the same element in op(A); (r2, c2): in solve order
-            const int r = trans ? w : q, c = trans ? q : w;
-            const int r2 = fwd ? r : b - 1 - r, c2 = fwd ? c : b - 1 - c;
-            if (q < b && w < b) {
-                Lt[c2][r2] = c2 < r2 ? v[u] : R(0);
-                if (c2 == r2) dg[r2] = v[u];
+            const int d = LOW ? q - w : w - q;   // distance from the diagonal into the stored triangle
+            const bool need = q < b && w < b && d >= 0 && (FMT != F_BAND || d <= bw);
+            const R vu = need ? (R)e[u] : R(0);
+            const int r = TR ? w : q, c = TR ? q : w;
+            const int r2 = FW ? r : (b - 1 - r) & (SB - 1), c2 = FW ? c : (b - 1 - c) & (SB - 1);
+            Lt[c2][r2] = c2 < r2 ? vu : R(0);
+            if (c2 == r2) dg[r2] = vu;
+        }
+    }
+
+    // Places the loaded block in LDS, then wave 0 substitutes, starting from the block's right-hand side rhs[0 .. b)
+    // (in A's row order, in LDS), and writes x of the block to xf. Called by the whole workgroup; the barrier orders
+    // the writes of rhs before wave 0 reads it.
+    __device__ __forceinline__ void solve(const Shape &s, int trans, int fwd, int p, int b, const R *rhs, R *xf,
+                                          R (*Lt)[SB + 1], R *dg) const {
+        if (trans) {
+            if (fwd) place<true, true>(s, b, Lt, dg);
+            else place<true, false>(s, b, Lt, dg);
+        } else {
+            if (fwd) place<false, true>(s, b, Lt, dg);
+            else place<false, false>(s, b, Lt, dg);
+        }
+        __syncthreads();
+        if (threadIdx.x >= 64) return;
+        const int l = threadIdx.x, n0 = b < 64 ? b : 64;
+        const auto idx = [&](int r) { return fwd ? r : b - 1 - r; };   // row of the block in A's order
+        const bool has1 = l + 64 < b;
+        R v0 = l < b ? rhs[idx(l)] : R(0), v1 = has1 ? rhs[idx(l + 64)] : R(0);
+        const R r0 = s.unit || l >= b ? R(1) : R(1) / dg[l], r1 = s.unit || !has1 ? R(1) : R(1) / dg[l + 64];
+        // rows at or past b read stale LDS: they belong to lanes whose values are never written back
+        const auto col = [&](int k, int row) { return Lt[k][row]; };
+        int k = 0;
+        for (; k + KS <= n0; k += KS) {
+            R c0[KS], c1[KS];
+#pragma unroll
+            for (int u = 0; u < KS; u++) {
+                c0[u] = col(k + u, l);
+                c1[u] = col(k + u, l + 64);
+            }
+#pragma unroll
+            for (int u = 0; u < KS; u++) {
+                const R xk = lane_value(v0 * r0, k + u);
+                v0 = fma_r(-c0[u], xk, v0);
+                v1 = fma_r(-c1[u], xk, v1);
             }
         }
-    }
-    __syncthreads();
-    if (threadIdx.x >= 64) return;
-    const int l = threadIdx.x, n0 = b < 64 ? b : 64;
-    const auto idx = [&](int r) { return p + (fwd ? r : b - 1 - r); };
-    const bool has1 = l + 64 < b;
-    R v0 = l < b ? xf[idx(l)] : R(0), v1 = has1 ? xf[idx(l + 64)] : R(0);
-    const R r0 = s.unit || l >= b ? R(1) : R(1) / dg[l], r1 = s.unit || !has1 ? R(1) : R(1) / dg[l + 64];
-    // rows at or past b read stale LDS: they belong to lanes whose values are never written back
-    const auto col = [&](int k, int row) { return Lt[k][row]; };
-    int k = 0;
-    for (; k + KS <= n0; k += KS) {
-        R c0[KS], c1[KS];
-#pragma unroll
-        for (int u = 0; u < KS; u++) {
-            c0[u] = col(k + u, l);
-            c1[u] = col(k + u, l + 64);
+        for (; k < n0; k++) {
+            const R xk = lane_value(v0 * r0, k);
+            v0 = fma_r(-col(k, l), xk, v0);
+            v1 = fma_r(-col(k, l + 64), xk, v1);
         }
+        for (; k + KS <= b; k += KS) {
+            R c1[KS];
 #pragma unroll
-        for (int u = 0; u < KS; u++) {
-            const R xk = lane_value(v0 * r0, k + u);
-            v0 = fma_r(-c0[u], xk, v0);
-            v1 = fma_r(-c1[u], xk, v1);
+            for (int u = 0; u < KS; u++) c1[u] = col(k + u, l + 64);
+#pragma unroll
+            for (int u = 0; u < KS; u++) v1 = fma_r(-c1[u], lane_value(v1 * r1, k + u - 64), v1);
         }
+        for (; k < b; k++) v1 = fma_r(-col(k, l + 64), lane_value(v1 * r1, k - 64), v1);
+        if (l < b) xf[p + idx(l)] = v0 * r0;
+        if (has1) xf[p + idx(l + 64)] = v1 * r1;
     }
-    for (; k < n0; k++) {
-        const R xk = lane_value(v0 * r0, k);
-        v0 = fma_r(-col(k, l), xk, v0);
-        v1 = fma_r(-col(k, l + 64), xk, v1);
-    }
-    for (; k + KS <= b; k += KS) {
-        R c1[KS];
+};
+
+// The region of A at rows [R0, R0 + br), columns [C0, C0 + bc) (br, bc ≤ SB) into e[], laid out as the diagonal block
+// (thread: column w = t % SB, rows q0 + 2u). Every lane loads, without a branch, from an address inside its row's
+// storage (rows past br re-read the last row; outside full storage the column is clamped into the row's stored
+// entries); `needed` tells which values are elements of A in the region.
+template <class T, int FMT>
+__device__ __forceinline__ void load_region(const Shape &s, const T *__restrict__ a, int R0, int br, int C0, int bc,
+                                            T (&e)[SB * SB / NT]) {
+    const int w = threadIdx.x % SB, q0 = __builtin_amdgcn_readfirstlane(threadIdx.x / SB);
 #pragma unroll
-        for (int u = 0; u < KS; u++) c1[u] = col(k + u, l + 64);
-#pragma unroll
-        for (int u = 0; u < KS; u++) v1 = fma_r(-c1[u], lane_value(v1 * r1, k + u - 64), v1);
+    for (int u = 0; u < SB * SB / NT; u++) {
+        const int i = R0 + min(u * (NT / SB) + q0, br - 1);
+        int j = C0 + min(w, bc - 1);
+        if constexpr (FMT == F_PACKL) j = min(j, i);
+        else if constexpr (FMT == F_PACKU) j = max(j, i);
+        else if constexpr (FMT == F_BAND) j = max(min(j, i + s.KU), i - s.KL);
+        e[u] = a[row_start<FMT>(s, i) + j];
     }
-    for (; k < b; k++) v1 = fma_r(-col(k, l + 64), lane_value(v1 * r1, k - 64), v1);
-    if (l < b) xf[idx(l)] = v0 * r0;
-    if (has1) xf[idx(l + 64)] = v1 * r1;
+}
+// Whether value u of load_region is an element of A, for a region that couples two different diagonal blocks: such a
+// region lies strictly inside A's stored triangle (the solve runs over the triangle's blocks in order), so only the
+// region's bounds and, for a band, the band decide.
+template <int FMT>
+__device__ __forceinline__ bool needed(const Shape &s, int R0, int br, int C0, int bc, int u) {
+    const int w = threadIdx.x % SB, q = u * (NT / SB) + __builtin_amdgcn_readfirstlane(threadIdx.x / SB);
+    const int dj = (C0 + w) - (R0 + q);   // column minus row
+    return q < br && w < bc && (FMT != F_BAND || (dj >= -s.KL && dj <= s.KU));
 }
 
-// x_r -= Σ_{c in [p, p+b)} A(r, c)·x_c for r in [r0, r1) (op(A) = A): a wave takes 8 rows, its lanes the block's
-// columns (b ≤ 128: two per lane), then the butterfly sums the 8 rows.
+// x_r -= Σ_{c in [p, p+b)} A(r, c)·x_c for rows r of [r0, r1) (op(A) = A), 32 rows per part: in part vb a wave takes
+// 8 rows, its lanes the block's columns (b ≤ 128: two per lane), then the butterfly sums the 8 rows.
+constexpr int UPD_ROWS = 8 * (NT / 64), UPD_COLS = 64;   // rows per part of the two updates
 template <class T, int FMT>
-__global__ void __launch_bounds__(NT) update_rows(Shape s, const T *__restrict__ a, int p, int b, int r0, int r1,
-                                                  typename Comp<T>::R *xf) {
+__device__ __forceinline__ void update_rows(const Shape &s, const T *__restrict__ a, int p, int b, int r0, int r1,
+                                            typename Comp<T>::R *xf, int vb) {
     using R = typename Comp<T>::R;
     constexpr int RW = 8;
     const int lane = threadIdx.x & 63;
-    const int rbase = r0 + (blockIdx.x * (NT / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * RW;
+    const int rbase = r0 + (vb * (NT / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * RW;
     if (rbase >= r1) return;
     const int ca = p + lane, cb = p + 64 + lane;
     const R x0 = lane < b ? xf[ca] : R(0), x1 = lane + 64 < b ? xf[cb] : R(0);
@@ -446,16 +510,17 @@ __global__ void __launch_bounds__(NT) update_rows(Shape s, const T *__restrict__
     if ((lane & (64 / RW - 1)) == 0 && rbase + base < r1) xf[rbase + base] -= t[0];
 }
 
-// x_r -= Σ_{c in [p, p+b)} A(c, r)·x_c for r in [r0, r1) (op(A) = Aᵀ): a workgroup takes 64 consecutive r, each
-// of its waves 32 of the block's rows c (all 32 loads in flight; neighbouring lanes read neighbouring elements of a
-// row of A), then wave 0 adds the 4 sums in wave order.
+// x_r -= Σ_{c in [p, p+b)} A(c, r)·x_c for rows r of [r0, r1) (op(A) = Aᵀ), 64 consecutive r per part: each wave
+// takes 32 of the block's rows c (all 32 loads in flight; neighbouring lanes read neighbouring elements of a row of
+// A), then wave 0 adds the 4 sums in wave order. Called by the whole workgroup (two barriers; `red` is free again
+// on return).
 template <class T, int FMT>
-__global__ void __launch_bounds__(NT) update_cols(Shape s, const T *__restrict__ a, int p, int b, int r0, int r1,
-                                                  typename Comp<T>::R *xf) {
+__device__ __forceinline__ void update_cols(const Shape &s, const T *__restrict__ a, int p, int b, int r0, int r1,
+                                            typename Comp<T>::R *xf, int vb, typename Comp<T>::R (*red)[64]) {
     using R = typename Comp<T>::R;
     constexpr int G = NT / 64, CW = SB / G;
     const int lane = threadIdx.x & 63, q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r = r0 + blockIdx.x * 64 + lane;
+    const int r = r0 + vb * UPD_COLS + lane;
     R t = 0;
     if (r < r1) {
         R v[CW];
@@ -470,14 +535,78 @@ __global__ void __launch_bounds__(NT) update_cols(Shape s, const T *__restrict__
         for (int u = 0; u < CW; u++)
             if (q * CW + u < b) t = fma_r(v[u], xf[p + q * CW + u], t);
     }
-    __shared__ R red[G][64];
     red[q][lane] = t;
     __syncthreads();
-    if (q != 0 || r >= r1) return;
-    R u = red[0][lane];
+    if (q == 0 && r < r1) {
+        R sum = red[0][lane];
 #pragma unroll
-    for (int w = 1; w < G; w++) u += red[w][lane];
-    xf[r] -= u;
+        for (int w = 1; w < G; w++) sum += red[w][lane];
+        xf[r] -= sum;
+    }
+    __syncthreads();
+}
+
+// One step of the blocked solve: block [p, p + b) in solve order, after block [pp, pp + pb) (pb = 0: the first step).
+// The previous block's solution is final (the previous launch wrote it), and its update reaches rows [t0, t1) of
+// this block and rows [o0, o1) beyond it. Workgroups 1.. apply the update to [o0, o1), one part each. Workgroup 0
+// issues the loads of this block's diagonal part and of the 128×128 region of A that couples the two blocks
+// (op(A) = A: this block's rows × the previous block's columns; op(A) = Aᵀ: the previous block's rows × this block's
+// columns) at once, forms this block's right-hand side x_r − Σ_c op(A)(r, c)·x_c in LDS (row sums: transposing
+// butterfly over each wave's 64 columns, then the two waves of a row set; column sums: per thread, then the two row
+// sets), and substitutes. The two sides read only the previous block's solution and write disjoint rows, so one
+// launch per block suffices (the update of block q and the solve of block q + 1 in one launch: a one-block
+// look-ahead).
+template <class T, int FMT>
+__global__ void __launch_bounds__(NT) solve_step(Shape s, const T *__restrict__ a, int trans, int fwd, int pp, int pb, int p,
+                                                 int b, int t0, int t1, int o0, int o1, typename Comp<T>::R *xf) {
+    using R = typename Comp<T>::R;
+    constexpr int RPT = SB * SB / NT;
+    __shared__ R Lt[SB][SB + 1];
+    __shared__ R dg[SB];
+    __shared__ R red[NT / 64][64];
+    __shared__ R xp[SB], rhs[SB];
+    if (blockIdx.x > 0) {
+        if (trans) update_cols<T, FMT>(s, a, pp, pb, o0, o1, xf, blockIdx.x - 1, red);
+        else update_rows<T, FMT>(s, a, pp, pb, o0, o1, xf, blockIdx.x - 1);
+        return;
+    }
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int w = tid % SB, q0 = __builtin_amdgcn_readfirstlane(tid / SB);
+    const bool upd = t1 > t0;
+    // coupling region: rows [R0, R0 + br), columns [C0, C0 + bc) of A
+    const int R0 = trans ? pp : p, br = trans ? pb : b, C0 = trans ? p : pp, bc = trans ? b : pb;
+    Diag<T, FMT> d;
+    d.load(s, a, p, b);
+    T eo[RPT];
+    if (upd) load_region<T, FMT>(s, a, R0, br, C0, bc, eo);
+    const R own = tid < b ? xf[p + tid] : R(0);
+    if (tid < SB) xp[tid] = upd && tid < pb ? xf[pp + tid] : R(0);
+    __syncthreads();
+    R sum = 0;   // thread tid < b: Σ_c op(A)(p + tid, c)·x_c over the previous block
+    if (upd) {
+        if (!trans) {
+            const R xw = xp[w];
+            R t[RPT];
+#pragma unroll
+            for (int u = 0; u < RPT; u++) t[u] = needed<FMT>(s, R0, br, C0, bc, u) ? (R)eo[u] * xw : R(0);
+            int base = 0;
+            butterfly<0, RPT>(t, lane, base);   // lane l: the wave's sum for u = l, row q0 + 2l
+            red[wave][lane] = t[0];
+            __syncthreads();
+            if (tid < b) sum = red[2 * (tid & 1)][tid >> 1] + red[2 * (tid & 1) + 1][tid >> 1];
+        } else {
+            R t = 0;
+#pragma unroll
+            for (int u = 0; u < RPT; u++)
+                if (needed<FMT>(s, R0, br, C0, bc, u)) t = fma_r((R)eo[u], xp[u * (NT / SB) + q0], t);
+            R *half = &red[0][0];   // [2][SB]: the column sums of row sets q0 = 0 and 1
+            half[q0 * SB + w] = t;
+            __syncthreads();
+            if (tid < b) sum = half[tid] + half[SB + tid];
+        }
+    }
+    if (tid < b) rhs[tid] = own - sum;
+    d.solve(s, trans, fwd, p, b, rhs, xf, Lt, dg);
 }
 
 // ---------------- launchers ----------------
@@ -586,25 +715,30 @@ static int launch_solve(int es, int fmt, const Shape &s, const void *a, int tran
         const int nb = (n + SB - 1) / SB;
         G9_TRY(by_fmt(fmt, [&](auto fc) -> int {
             constexpr int FMT = decltype(fc)::value;
+            const int per = trans ? UPD_COLS : UPD_ROWS;
             for (int q = 0; q < nb; q++) {
                 const int p = (lower ? q : nb - 1 - q) * SB, b = n - p < SB ? n - p : SB;
-                hipLaunchKernelGGL((solve_block<T, FMT>), dim3(1), dim3(NT), 0, stream, s, (const T *)a, trans, lower, p, b, xf);
-                G9_HIP(hipGetLastError());
-                int r0, r1;
-                if (lower) {
-                    r0 = p + b;
-                    r1 = (ll)p + b + kb < n ? p + b + kb : n;
-                } else {
-                    r0 = p - kb > 0 ? p - kb : 0;
-                    r1 = p;
+                int pp = 0, pb = 0, t0 = 0, t1 = 0, o0 = 0, o1 = 0;
+                if (q > 0) {
+                    // rows [r0, r1) reached by the previous block (after it in solve order), split at this block
+                    pp = (lower ? q - 1 : nb - q) * SB;
+                    pb = n - pp < SB ? n - pp : SB;
+                    int r0, r1;
+                    if (lower) {
+                        r0 = pp + pb;
+                        r1 = (ll)pp + pb + kb < n ? pp + pb + kb : n;
+                    } else {
+                        r0 = pp - kb > 0 ? pp - kb : 0;
+                        r1 = pp;
+                    }
+                    t0 = std::max(r0, p);
+                    t1 = std::min(r1, p + b);
+                    o0 = lower ? std::max(r0, p + b) : r0;
+                    o1 = lower ? r1 : std::min(r1, p);
                 }
-                if (r1 <= r0) continue;
-                if (trans)
-                    hipLaunchKernelGGL((update_cols<T, FMT>), dim3(blocks(r1 - r0, 64)), dim3(NT), 0, stream, s, (const T *)a,
-                                       p, b, r0, r1, xf);
-                else
-                    hipLaunchKernelGGL((update_rows<T, FMT>), dim3(blocks(r1 - r0, 8 * (NT / 64))), dim3(NT), 0, stream, s,
-                                       (const T *)a, p, b, r0, r1, xf);
+                const unsigned grid = 1 + (o1 > o0 ? (unsigned)blocks(o1 - o0, per) : 0u);
+                hipLaunchKernelGGL((solve_step<T, FMT>), dim3(grid), dim3(NT), 0, stream, s, (const T *)a, trans, lower, pp, pb,
+                                   p, b, t0, t1, o0, o1, xf);
                 G9_HIP(hipGetLastError());
             }
             return 0;
