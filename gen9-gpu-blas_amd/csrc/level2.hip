@@ -77,8 +77,9 @@ __device__ __forceinline__ void stored_range(const Shape &s, bool band, int i, i
 
 // ---------------- products ----------------
 constexpr int NT = 256;
-// Rows per batch: 16 (V > 1: 16 bytes per lane, a wave has 16 KiB of loads outstanding).
-template <int V> constexpr int UB = 16;
+// Rows per batch: 8 with 16 bytes per lane (V > 1: a wave has 8 KiB of loads outstanding), 16 with one element per
+// lane. From a sweep at n = 16384 FP32 (SYMV / TRMV / SPMV): 8 and 16 rows, 8 to 128 workgroups per CU.
+template <int V> constexpr int UB = V > 1 ? 8 : 16;
 template <class T, int V, int FMT>
 __global__ void __launch_bounds__(NT) mv_kernel(Shape s, const T *__restrict__ a, const T *__restrict__ x, ll ix, int rpp, int dirs,
                                                 int skipdiag, typename Comp<T>::R *P, typename Comp<T>::R *Q) {
@@ -632,11 +633,12 @@ static int launch_mv(int es, int fmt, const Shape &s, const void *a, const void 
         const bool vec = fmt == F_FULL && (uintptr_t)a % 16 == 0 && (s.ld * (ll)sizeof(T)) % 16 == 0;
         const int V = vec ? VW<T> : 1, gw = 64 * V;
         const ll groups = (s.ncols + gw - 1) / gw;
-        // a workgroup per (column group, band of rows), its 4 waves on quarters of the band; about 16 workgroups per
-        // CU, so the dispatcher balances the uneven work of a triangle (about half the workgroups find no rows)
-        constexpr int RU = 16 * (NT / 64);   // a band is whole batches for each wave
+        // a workgroup per (column group, band of rows), its 4 waves on quarters of the band; about 64 workgroups per
+        // CU, so the dispatcher balances the uneven work of a triangle (about half the workgroups find no rows). At
+        // n = 16384 FP32 this is 113 µs for SYMV against 136 with 16 workgroups per CU and 16-row batches.
+        const int RU = (V > 1 ? UB<2> : UB<1>) * (NT / 64);   // a band is whole batches for each wave
         const int cus = num_cus > 0 ? num_cus : 256;
-        ll parts = (16LL * cus + groups - 1) / groups;
+        ll parts = (64LL * cus + groups - 1) / groups;
         const ll maxparts = (s.nrows + RU - 1) / RU;
         if (parts > maxparts) parts = maxparts;
         if (parts < 1) parts = 1;
