@@ -274,46 +274,97 @@ __global__ void __launch_bounds__(NT) mv_finish(Shape s, int band, int ny, int d
 }
 
 // ---------------- rank-1 / rank-2 updates of the stored elements ----------------
-// A = alpha·x·yᵀ + A (SYR, SPR: y = x) or alpha·(x·yᵀ + y·xᵀ) + A (SYR2, SPR2) on the stored triangle
-// (reference: level12.cl:466-476, 622-630: fma(alpha·x_i, y_j, a), then fma(alpha·y_i, x_j, ·)). V > 1: full
-// storage with 16-byte rows and contiguous x, y: a thread updates 16 bytes of a row at a time, element by element
-// only in the chunks the triangle cuts.
+// Rank updates A += alpha·x·yᵀ (+ alpha·y·xᵀ) on the stored elements: fma(alpha·x_i, y_j, a), then
+// fma(alpha·y_i, x_j, ·) (reference: level12.cl:466-476), each element read and written once. The grid and the row
+// classification are those of mv_kernel: a workgroup owns a group of 64·V columns and a band of rows, its waves a
+// quarter of the band each; a lane loads its columns' y_j (and x_j) once. Rows that store the whole group take
+// batches of U rows with every load issued before the first store; rows near the diagonal or the band's edges are
+// checked per element.
 template <class T, int V, int FMT>
 __global__ void __launch_bounds__(NT) rank_kernel(Shape s, typename Comp<T>::R alpha, const T *x, ll ix, const T *y,
-                                                  ll iy, int two, T *a) {
+                                                  ll iy, int two, int rpp, T *a) {
     using R = typename Comp<T>::R;
-    for (int i = blockIdx.y; i < s.nrows; i += gridDim.y) {
-        int lo, hi;
-        stored_range(s, FMT == F_BAND, i, lo, hi);
-        const R xi = alpha * (R)x[(ll)i * ix];
-        const R yi = two ? alpha * (R)y[(ll)i * iy] : R(0);
-        T *ar = a + row_start<FMT>(s, i);
-        const int step = gridDim.x * NT * V;
-        for (int c = lo / V * V + (blockIdx.x * NT + threadIdx.x) * V; c <= hi; c += step) {
-            if (V > 1 && c >= lo && c + V - 1 <= hi) {
-                Vec<T> av, xv, yv;
-                av.u = *reinterpret_cast<const u32x4 *>(ar + c);
-                yv.u = *reinterpret_cast<const u32x4 *>(y + c);
-                if (two) xv.u = *reinterpret_cast<const u32x4 *>(x + c);
+    constexpr bool band = FMT == F_BAND;
+    constexpr int U = UB<V>;
+    const int lane = threadIdx.x & 63;
+    const int g = blockIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g0 = g * 64 * V, g1 = min(g0 + 64 * V, s.ncols) - 1, c0 = g0 + lane * V;
+    const int rpw = rpp / (NT / 64);
+    int rb = blockIdx.y * rpp + w * rpw, re = min(s.nrows, rb + rpw);
+    if (s.tri == TRI_LOWER) rb = max(rb, g0);
+    if (s.tri == TRI_UPPER) re = min(re, g1 + 1);
+    if (band) {
+        rb = max(rb, g0 - s.KU);
+        re = min(re, g1 + s.KL + 1);
+    }
+    R yc[V], xc[V];
 #pragma unroll
-                for (int e = 0; e < V; e++) {
-                    R v = fma_r(xi, (R)yv.e[e], (R)av.e[e]);
-                    if (two) v = fma_r(yi, (R)xv.e[e], v);
-                    av.e[e] = (T)v;
-                }
-                *reinterpret_cast<u32x4 *>(ar + c) = av.u;
-            } else {
+    for (int e = 0; e < V; e++) {
+        yc[e] = c0 + e < s.ncols ? (R)y[(ll)(c0 + e) * iy] : R(0);
+        xc[e] = two && c0 + e < s.ncols ? (R)x[(ll)(c0 + e) * ix] : R(0);
+    }
+    int fa = rb, fb = re;   // rows [fa, fb) store every column of the group (as in mv_kernel)
+    if (g0 + 64 * V > s.ncols) {
+        fb = fa;
+    } else {
+        if (band) {
+            fa = max(fa, g1 - s.KU);
+            fb = min(fb, g0 + s.KL + 1);
+        }
+        if (s.tri == TRI_LOWER) fa = max(fa, g1 + 1);
+        if (s.tri == TRI_UPPER) fb = min(fb, g0);
+    }
+    fa = min(fa, re);
+    fb = max(fa, min(fb, re));
+    fb = fa + (fb - fa) / U * U;
+    auto update = [&](R (&v)[V], R xi, R yi) {
 #pragma unroll
-                for (int e = 0; e < V; e++) {
-                    const int j = c + e;
-                    if (j < lo || j > hi) continue;
-                    R v = fma_r(xi, (R)y[(ll)j * iy], (R)ar[j]);
-                    if (two) v = fma_r(yi, (R)x[(ll)j * ix], v);
-                    ar[j] = (T)v;
-                }
-            }
+        for (int e = 0; e < V; e++) {
+            v[e] = fma_r(xi, yc[e], v[e]);
+            if (two) v[e] = fma_r(yi, xc[e], v[e]);
+        }
+    };
+    auto checked = [&](int r0, int r1) {
+        for (int i = r0; i < r1; i++) {
+            int lo, hi;
+            stored_range(s, band, i, lo, hi);
+            const R xi = alpha * (R)x[(ll)i * ix], yi = two ? alpha * (R)y[(ll)i * iy] : R(0);
+            T *ar = a + row_start<FMT>(s, i);
+            R v[V];
+#pragma unroll
+            for (int e = 0; e < V; e++) v[e] = c0 + e >= lo && c0 + e <= hi ? (R)ar[c0 + e] : R(0);
+            update(v, xi, yi);
+#pragma unroll
+            for (int e = 0; e < V; e++)
+                if (c0 + e >= lo && c0 + e <= hi) ar[c0 + e] = (T)v[e];
+        }
+    };
+    checked(rb, fa);
+    for (int i = fa; i < fb; i += U) {
+        Vec<T> el[U];
+        R xi[U], yi[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const T *ar = a + row_start<FMT>(s, i + u) + c0;
+            if constexpr (V > 1) el[u].u = *reinterpret_cast<const u32x4 *>(ar);
+            else el[u].e[0] = *ar;
+            xi[u] = alpha * (R)x[(ll)(i + u) * ix];
+            yi[u] = two ? alpha * (R)y[(ll)(i + u) * iy] : R(0);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            R v[V];
+#pragma unroll
+            for (int e = 0; e < V; e++) v[e] = (R)el[u].e[e];
+            update(v, xi[u], yi[u]);
+#pragma unroll
+            for (int e = 0; e < V; e++) el[u].e[e] = (T)v[e];
+            T *ar = a + row_start<FMT>(s, i + u) + c0;
+            if constexpr (V > 1) *reinterpret_cast<u32x4 *>(ar) = el[u].u;
+            else *ar = el[u].e[0];
         }
     }
+    checked(fb, re);
 }
 
 // ---------------- triangular solves ----------------
@@ -625,6 +676,25 @@ template <class F> static int by_fmt(int fmt, F f) {
 static unsigned blocks(ll n, int per) { return (unsigned)((n + per - 1) / per); }
 
 // y = alpha·(sums over the stored elements in the directions `dirs`) + beta·y (+ x for add_x); ny outputs.
+// Grid of mv_kernel and rank_kernel: a workgroup per (column group of 64·V columns, band of rpp rows), its 4 waves on
+// quarters of the band; about 64 workgroups per CU, so the dispatcher balances the uneven work of a triangle (about
+// half the workgroups find no rows). At n = 16384 FP32 this is 113 µs for SYMV against 136 with 16 workgroups per CU
+// and 16-row batches. Returns the number of column groups.
+static ll grid_2d(const Shape &s, int V, ll &parts, ll &rpp) {
+    const ll gw = 64LL * V, groups = (s.ncols + gw - 1) / gw;
+    const int RU = (V > 1 ? UB<2> : UB<1>) * (NT / 64);   // a band is whole batches for each wave
+    const int cus = num_cus > 0 ? num_cus : 256;
+    parts = (64LL * cus + groups - 1) / groups;
+    const ll maxparts = (s.nrows + RU - 1) / RU;
+    if (parts > maxparts) parts = maxparts;
+    if (parts < 1) parts = 1;
+    if (parts > 65535) parts = 65535;
+    rpp = (s.nrows + parts - 1) / parts;
+    rpp = (rpp + RU - 1) / RU * RU;
+    parts = (s.nrows + rpp - 1) / rpp;
+    return groups;
+}
+
 static int launch_mv(int es, int fmt, const Shape &s, const void *a, const void *x, ll ix, int dirs, int skipdiag,
                      double alpha, double beta, int add_x, void *y, ll iy, int ny) {
     return by_type(es, [&](auto *tag) -> int {
@@ -632,20 +702,8 @@ static int launch_mv(int es, int fmt, const Shape &s, const void *a, const void 
         using R = typename Comp<T>::R;
         const bool vec = fmt == F_FULL && (uintptr_t)a % 16 == 0 && (s.ld * (ll)sizeof(T)) % 16 == 0;
         const int V = vec ? VW<T> : 1, gw = 64 * V;
-        const ll groups = (s.ncols + gw - 1) / gw;
-        // a workgroup per (column group, band of rows), its 4 waves on quarters of the band; about 64 workgroups per
-        // CU, so the dispatcher balances the uneven work of a triangle (about half the workgroups find no rows). At
-        // n = 16384 FP32 this is 113 µs for SYMV against 136 with 16 workgroups per CU and 16-row batches.
-        const int RU = (V > 1 ? UB<2> : UB<1>) * (NT / 64);   // a band is whole batches for each wave
-        const int cus = num_cus > 0 ? num_cus : 256;
-        ll parts = (64LL * cus + groups - 1) / groups;
-        const ll maxparts = (s.nrows + RU - 1) / RU;
-        if (parts > maxparts) parts = maxparts;
-        if (parts < 1) parts = 1;
-        if (parts > 65535) parts = 65535;
-        ll rpp = (s.nrows + parts - 1) / parts;
-        rpp = (rpp + RU - 1) / RU * RU;
-        parts = (s.nrows + rpp - 1) / rpp;
+        ll parts, rpp;
+        const ll groups = grid_2d(s, V, parts, rpp);
         if (groups > 0x7fffffffLL) G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "level 2: %lld column groups", groups);
         void *pp = nullptr, *qq = nullptr;
         if (dirs & DIR_COL) G9_TRY(scratch(SLOT_P, (size_t)parts * s.ncols * sizeof(R), &pp));
@@ -679,22 +737,22 @@ static int launch_rank(int es, int fmt, const Shape &s, double alpha, const void
     return by_type(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
         using R = typename Comp<T>::R;
-        const auto al = [](const void *q) { return (uintptr_t)q % 16 == 0; };
-        const bool vec = fmt == F_FULL && al(a) && (s.ld * (ll)sizeof(T)) % 16 == 0 && ix == 1 && iy == 1 && al(x) && al(y);
+        const bool vec = fmt == F_FULL && (uintptr_t)a % 16 == 0 && (s.ld * (ll)sizeof(T)) % 16 == 0;
         const int V = vec ? VW<T> : 1;
-        const unsigned gx = blocks(s.ncols, NT * V) < 8 ? blocks(s.ncols, NT * V) : 8;
-        const dim3 grid(gx, s.nrows < 65535 ? (unsigned)s.nrows : 65535u);
+        ll parts, rpp;
+        const ll groups = grid_2d(s, V, parts, rpp);
+        const dim3 grid((unsigned)groups, (unsigned)parts);
         G9_TRY(by_fmt(fmt, [&](auto fc) -> int {
             constexpr int FMT = decltype(fc)::value;
             if constexpr (FMT == F_FULL) {
                 if (vec) {
                     hipLaunchKernelGGL((rank_kernel<T, VW<T>, FMT>), grid, dim3(NT), 0, stream, s, (R)alpha, (const T *)x, ix,
-                                       (const T *)y, iy, two, (T *)a);
+                                       (const T *)y, iy, two, (int)rpp, (T *)a);
                     return 0;
                 }
             }
             hipLaunchKernelGGL((rank_kernel<T, 1, FMT>), grid, dim3(NT), 0, stream, s, (R)alpha, (const T *)x, ix,
-                               (const T *)y, iy, two, (T *)a);
+                               (const T *)y, iy, two, (int)rpp, (T *)a);
             return 0;
         }));
         G9_HIP(hipGetLastError());
