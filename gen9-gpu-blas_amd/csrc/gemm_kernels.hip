@@ -97,8 +97,11 @@ static int launch_layout(const GemmParams<typename Mma<T>::Sum> &p, int count) {
 
 // ---------------- FP16 whole-tile kernel ----------------
 // Configurations from sweeps on MI355X with N(0,1) FP16 inputs: n = 4096, 256×256 tiles, 8 waves (4×2), KB = 64,
-// two stages: 1130-1180 TFLOP/s (NN; hipBLASLt on the same inputs: 1180-1210); n = 2048 and 1024, 128×128 tiles,
-// 4 waves, KB = 32, four stages: 721 and 191. Products with fewer 256×256 tiles than CUs take the 128×128 tile.
+// two stages: 1130-1180 TFLOP/s (NN; hipBLASLt on the same inputs: 1180-1210); n = 2048, 128×128 tiles, 4 waves,
+// KB = 32, four stages: 780 (32×128 or 64×128 tiles: 430-690). Products with fewer 256×256 tiles than CUs take the
+// 128×128 tile, and with fewer 128×128 tiles than CUs (n = 1024: 64) a 32×128 tile, 4 waves of 32×32, KB = 64, three
+// stages: 322 TFLOP/s at n = 1024 against 208 for 128×128 (two or four stages: 290, 312; 64×128: 268). The 32-row
+// tile needs A k-contiguous (the transposed-A loader reads 128-row tiles).
 template <int BM, int BN, int WM, int WN, int KB, int NS, bool AK, bool BKC>
 static int launch_hg(const hg::Params &p0, int count) {
     hg::Params p = p0;
@@ -113,6 +116,8 @@ template <bool AK, bool BKC>
 static int launch_hg_layout(const hg::Params &p, int count) {
     if ((long long)(p.M / 256) * (p.N / 256) * count >= num_cus && p.M % 256 == 0 && p.N % 256 == 0)
         return launch_hg<256, 256, 4, 2, 64, 2, AK, BKC>(p, count);
+    if constexpr (AK)
+        if ((long long)(p.M / 128) * (p.N / 128) * count < num_cus) return launch_hg<32, 128, 1, 4, 64, 3, AK, BKC>(p, count);
     return launch_hg<128, 128, 2, 2, 32, 4, AK, BKC>(p, count);
 }
 // The whole-tile FP16 kernel applies when every operand is 16-byte aligned with 16-byte row strides, M and N are

@@ -197,12 +197,14 @@ def test_gemm_exact_small_integers(g9, torch_dev):
                     assert np.array_equal(W.astype(np.int64), ref), f"{dt} {M}x{N}x{K} tA={ta} tB={tb}"
 
 
-@pytest.mark.parametrize("M,N,K,count", [(256, 384, 320, 1), (128, 256, 2112, 1), (1024, 1024, 192, 16)])
+@pytest.mark.parametrize("M,N,K,count", [(256, 384, 320, 1), (128, 256, 2112, 1), (1024, 1024, 64, 4),
+                                         (1024, 1024, 192, 16)])
 def test_hgemm_whole_tile_kernel(g9, torch_dev, M, N, K, count):
-    """Shapes served by the whole-tile FP16 kernel (M, N multiples of 128, K of 64, 16-byte aligned operands): 128×128
-    tiles with two and with four LDS stages, and 256×256 tiles over a batch of 16, in every transpose layout, through
-    the C ABI on device memory. Small-integer inputs make every result exact, so a misplaced 16-byte chunk, k row or
-    tile shows up bit-exactly; alpha/beta are then checked against float64 with the HGEMM bound."""
+    """Shapes served by the whole-tile FP16 kernel (M, N multiples of 128, K of 64, 16-byte aligned operands): fewer
+    128×128 tiles than CUs (32×128 tiles, three LDS stages, with A k-contiguous; 128×128, four stages, with A
+    transposed), 256 tiles of 128×128 over a batch of 4, and 256×256 tiles over a batch of 16, in every transpose
+    layout, through the C ABI on device memory. Small-integer inputs make every result exact, so a misplaced 16-byte
+    chunk, k row or tile shows up bit-exactly; alpha/beta are then checked against float64 with the HGEMM bound."""
     import ctypes
     torch = torch_dev
     rng = np.random.default_rng(21)
@@ -214,7 +216,7 @@ def test_hgemm_whole_tile_kernel(g9, torch_dev, M, N, K, count):
             A = np.ascontiguousarray(a.transpose(0, 2, 1)) if ta else a      # stored K×M when transposed
             B = np.ascontiguousarray(b.transpose(0, 2, 1)) if tb else b      # stored N×K when transposed
             Ad, Bd = _to_dev(torch, A), _to_dev(torch, B)
-            ref = np.einsum("bmk,bkn->bmn", a.astype(np.int64), b.astype(np.int64))
+            ref = np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.int64)   # exact: |sums| < 2^53
             assert np.abs(ref).max() <= 2048
             for al, be in ((1.0, 0.0), (0.5, -1.5)):
                 Cd = _to_dev(torch, c0 if be else np.zeros_like(c0))
