@@ -14,8 +14,9 @@
 //   X·Yᵀ = op(A)·op(B)ᵀ + op(B)·op(A)ᵀ is one accumulation (level3.c:109-125);
 // - TRSM: op(A)·X = alpha·B (left) or X·op(A) = alpha·B (right), X overwrites B. As the reference (level3.c:127-215)
 //   the problem is brought to L·Y = alpha·R with L lower triangular (an upper matrix by reversing the index order,
-//   the right side by transposition), the diagonal blocks of L are inverted in FP64, and for each block row
-//   Y_i -= L[i, <i]·Y[<i] and Y_i = inv(L_ii)·Y_i run on the GEMM kernels. Blocks are 128 rows (the MFMA tile).
+//   the right side by transposition) and the diagonal blocks of L are inverted in FP64; the substitution then runs on
+//   the GEMM kernels by recursive halving (the reference's per-block-row updates Y_i -= L[i, <i]·X[<i] grouped into a
+//   few large products), each 128-row block finished by X_i = inv(L_ii)·Y_i.
 // Products of the element type round as a GEMM does; the merge / copy passes round once more, as the reference's
 // separate epilogues do.
 #include "internal.h"
@@ -136,7 +137,15 @@ __global__ void __launch_bounds__(TRSM_NB) trsm_inv_kernel(const T *L, int n, T 
         for (int i = j + 1; i < b; i++) {
             const T *li = L + (ll)(r0 + i) * n + r0;
             double s = 0.0;
-            for (int k = j; k < i; k++) s = __builtin_fma((double)li[k], X[k][j], s);
+            int k = j;
+            for (; k + 8 <= i; k += 8) {   // 8 loads in flight, then the FMAs in k order
+                T lv[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) lv[u] = li[k + u];
+#pragma unroll
+                for (int u = 0; u < 8; u++) s = __builtin_fma((double)lv[u], X[k + u][j], s);
+            }
+            for (; k < i; k++) s = __builtin_fma((double)li[k], X[k][j], s);
             X[i][j] = -s / (double)li[i];
         }
     }
@@ -160,6 +169,31 @@ static int dgemm_dev(int type, int tA, int tB, int M, int N, int K, double alpha
     g.C = C; g.ldc = ldc; g.sC = 0;
     return launch_gemm(g);
 }
+
+// Blocked forward substitution L·X = Y (L n×n lower, Y and X n×m, row strides n and m) over 128-row diagonal blocks,
+// by recursive halving: the first half of a block range is solved, one GEMM then subtracts its contribution from the
+// right-hand side of the second half, Y[i1..i2) -= L[i1..i2, i0..i1)·X[i0..i1), and the second half is solved. A
+// single block is X_i = inv(L_ii)·Y_i with the block's FP64-computed inverse. The reference updates one block row at
+// a time, Y_i -= L[i, <i]·X[<i] (level3.c:127-215): the same products, grouped so that most of the flops run in a few
+// large GEMMs instead of n/128 products of 128 rows; the sums differ only in rounding (each GEMM rounds once).
+struct TrsmSolve {
+    int type, n, m, es;
+    const char *L, *Iv;
+    char *Y, *X;
+    int solve(int b0, int nb) const {   // blocks [b0, b0 + nb)
+        if (nb == 1) {
+            const int i0 = b0 * TRSM_NB, b = n - i0 < TRSM_NB ? n - i0 : TRSM_NB;
+            return dgemm_dev(type, 0, 0, b, m, b, 1.0, Iv + (ll)b0 * TRSM_NB * TRSM_NB * es, b, Y + (ll)i0 * m * es, m, 0.0,
+                             X + (ll)i0 * m * es, m);
+        }
+        const int h = nb / 2;
+        G9_TRY(solve(b0, h));
+        const int i0 = b0 * TRSM_NB, i1 = (b0 + h) * TRSM_NB, i2 = n < (b0 + nb) * TRSM_NB ? n : (b0 + nb) * TRSM_NB;
+        G9_TRY(dgemm_dev(type, 0, 0, i2 - i1, m, i1 - i0, -1.0, L + ((ll)i1 * n + i0) * es, n, X + (ll)i0 * m * es, m, 1.0,
+                         Y + (ll)i1 * m * es, m));
+        return solve(b0 + h, nb - h);
+    }
+};
 
 static int bands(int n) { return n >= 512 ? 4 : 1; }
 static int band_rows(int n) {
@@ -359,7 +393,7 @@ int gen9blas_trsm(int type, int side, int uplo, int transA, int diag, int M, int
     G9_TRY(scratch(SLOT_T, (size_t)n * n * es, &Ld));
     G9_TRY(scratch(SLOT_X, (size_t)n * m * es, &Yd));
     G9_TRY(scratch(SLOT_Y, (size_t)nbl * TRSM_NB * TRSM_NB * es, &Iv));
-    G9_TRY(scratch(SLOT_W, (size_t)TRSM_NB * m * es, &Zd));
+    G9_TRY(scratch(SLOT_W, (size_t)n * m * es, &Zd));
     G9_TRY(by_es(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
         using S = typename Acc<T>::S;
@@ -371,18 +405,11 @@ int gen9blas_trsm(int type, int side, int uplo, int transA, int diag, int M, int
         G9_HIP(hipGetLastError());
         return 0;
     }));
-    for (int bi = 0; bi < nbl; bi++) {
-        const int i0 = bi * TRSM_NB, b = n - i0 < TRSM_NB ? n - i0 : TRSM_NB;
-        char *Yi = (char *)Yd + (ll)i0 * m * es;
-        if (i0 > 0)   // Y_i -= L[i0.., 0..i0]·Y[0..i0]
-            G9_TRY(dgemm_dev(type, 0, 0, b, m, i0, -1.0, (const char *)Ld + (ll)i0 * n * es, n, Yd, m, 1.0, Yi, m));
-        // Y_i = inv(L_ii)·Y_i (through Z: the product may not overwrite its input)
-        G9_TRY(dgemm_dev(type, 0, 0, b, m, b, 1.0, (const char *)Iv + (ll)bi * TRSM_NB * TRSM_NB * es, b, Yi, m, 0.0, Zd, m));
-        G9_HIP(hipMemcpyAsync(Yi, Zd, (size_t)b * m * es, hipMemcpyDeviceToDevice, stream));
-    }
+    TrsmSolve rec{type, n, m, es, (const char *)Ld, (const char *)Iv, (char *)Yd, (char *)Zd};
+    G9_TRY(rec.solve(0, nbl));
     G9_TRY(by_es(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
-        hipLaunchKernelGGL((trsm_store_kernel<T>), dim3(grid_for((ll)n * m)), dim3(256), 0, stream, (const T *)Yd,
+        hipLaunchKernelGGL((trsm_store_kernel<T>), dim3(grid_for((ll)n * m)), dim3(256), 0, stream, (const T *)Zd,
                            (T *)ops[1].dev, ops[1].ld, n, m, left, rev);
         G9_HIP(hipGetLastError());
         return 0;
