@@ -125,20 +125,29 @@ __global__ void __launch_bounds__(256) trsm_store_kernel(const T *Y, T *B, ll ld
 
 constexpr int TRSM_NB = 128;
 // Inverse of the diagonal block bi of L (rows and columns r0 .. r0+b-1, b ≤ TRSM_NB), in FP64, stored in the element
-// type as a b×b lower matrix at Inv + bi·NB². Thread j forms column j by forward substitution:
-// X[j][j] = 1 / L[j][j], X[i][j] = −(Σ_{k=j}^{i-1} L[i][k]·X[k][j]) / L[i][i]. The columns live in LDS (128 KiB).
+// type as a b×b lower matrix at Inv + bi·NB². The block is split into 32×32 sub-blocks: the four diagonal sub-blocks
+// are inverted first, thread j forming column j of its sub-block by substitution (X[j][j] = 1 / L[j][j],
+// X[i][j] = −(Σ_{k=j}^{i-1} L[i][k]·X[k][j]) / L[i][i], 8 loads of L in flight per step); the off-diagonal sub-blocks
+// then follow by distance d from the diagonal, X_ij = −inv(L_ii)·Σ_{k=j}^{i-1} L_ik·X_kj (i − j = d), one element per
+// thread at a time. The work per thread is balanced (a single column chain of the whole block would be 8128 FMAs
+// long); the sums differ from plain column substitution in FP64 rounding only. X and the sums live in LDS (154 KiB).
 template <class T>
-__global__ void __launch_bounds__(TRSM_NB) trsm_inv_kernel(const T *L, int n, T *Inv) {
-    __shared__ double X[TRSM_NB][TRSM_NB];
-    const int bi = blockIdx.x, r0 = bi * TRSM_NB, b = min(TRSM_NB, n - r0), j = threadIdx.x;
-    if (j < b) {
-        for (int i = 0; i < j; i++) X[i][j] = 0.0;
-        X[j][j] = 1.0 / (double)L[(ll)(r0 + j) * n + r0 + j];
-        for (int i = j + 1; i < b; i++) {
-            const T *li = L + (ll)(r0 + i) * n + r0;
+__global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, int n, T *Inv) {
+    constexpr int S = 32, NSB = TRSM_NB / S;
+    __shared__ double X[TRSM_NB][TRSM_NB + 1];
+    __shared__ double Sb[NSB - 1][S][S + 1];
+    const int bi = blockIdx.x, r0 = bi * TRSM_NB, b = min(TRSM_NB, n - r0), t = threadIdx.x;
+    const T *Lb = L + (ll)r0 * n + r0;   // element (i, j) of the block
+    for (int e = t; e < TRSM_NB * TRSM_NB; e += 256) X[e / TRSM_NB][e % TRSM_NB] = 0.0;
+    __syncthreads();
+    if (t < TRSM_NB && t < b) {
+        const int j = t, e = min(b, (j / S + 1) * S);   // column j of its diagonal sub-block, rows up to e
+        X[j][j] = 1.0 / (double)Lb[(ll)j * n + j];
+        for (int i = j + 1; i < e; i++) {
+            const T *li = Lb + (ll)i * n;
             double s = 0.0;
             int k = j;
-            for (; k + 8 <= i; k += 8) {   // 8 loads in flight, then the FMAs in k order
+            for (; k + 8 <= i; k += 8) {
                 T lv[8];
 #pragma unroll
                 for (int u = 0; u < 8; u++) lv[u] = li[k + u];
@@ -150,8 +159,37 @@ __global__ void __launch_bounds__(TRSM_NB) trsm_inv_kernel(const T *L, int n, T 
         }
     }
     __syncthreads();
+    for (int d = 1; d < NSB; d++) {
+        const int nblk = NSB - d;   // sub-blocks (j + d, j), j = 0 .. nblk - 1
+        for (int q = t; q < nblk * S * S; q += 256) {
+            const int j = q / (S * S), rr = (q / S) % S, cc = q % S;
+            const int row = (j + d) * S + rr, col = j * S + cc;
+            double s = 0.0;
+            if (row < b && col < b) {
+                const T *li = Lb + (ll)row * n;
+                for (int k = j * S; k < (j + d) * S; k += 8) {
+                    T lv[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) lv[u] = li[k + u];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) s = __builtin_fma((double)lv[u], X[k + u][col], s);
+                }
+            }
+            Sb[j][rr][cc] = s;
+        }
+        __syncthreads();
+        for (int q = t; q < nblk * S * S; q += 256) {
+            const int j = q / (S * S), rr = (q / S) % S, cc = q % S, i = j + d;
+            const int row = i * S + rr, col = j * S + cc;
+            double x = 0.0;
+#pragma unroll 8
+            for (int m = 0; m < S; m++) x = __builtin_fma(X[row][i * S + m], Sb[j][m][cc], x);
+            if (row < b && col < b) X[row][col] = -x;
+        }
+        __syncthreads();
+    }
     T *out = Inv + (ll)bi * TRSM_NB * TRSM_NB;
-    for (int e = threadIdx.x; e < b * b; e += TRSM_NB) out[e] = (T)X[e / b][e % b];
+    for (int e = t; e < b * b; e += 256) out[e] = (T)X[e / b][e % b];
 }
 
 // One GEMM on device operands (no staging, no wait): C = alpha·op(A)·op(B) + beta·C.
@@ -401,7 +439,7 @@ int gen9blas_trsm(int type, int side, int uplo, int transA, int diag, int M, int
                            ops[0].ld, (T *)Ld, n, uplo == GEN9BLAS_LOWER, tr, diag != 0, rev);
         hipLaunchKernelGGL((trsm_y_kernel<T>), dim3(grid_for((ll)n * m)), dim3(256), 0, stream, (const T *)ops[1].dev,
                            ops[1].ld, (T *)Yd, n, m, left, rev, (S)alpha);
-        hipLaunchKernelGGL((trsm_inv_kernel<T>), dim3(nbl), dim3(TRSM_NB), 0, stream, (const T *)Ld, n, (T *)Iv);
+        hipLaunchKernelGGL((trsm_inv_kernel<T>), dim3(nbl), dim3(256), 0, stream, (const T *)Ld, n, (T *)Iv);
         G9_HIP(hipGetLastError());
         return 0;
     }));
