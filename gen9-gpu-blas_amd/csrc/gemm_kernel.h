@@ -194,7 +194,10 @@ template <class T, class S> __device__ __forceinline__ void store4(T *c, const S
 // Instruction-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100, SG_DS_WRITE = 0x200;
 
-template <class T, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool VEC, bool SCHED = true, bool SPLIT = false>
+// TRI (1: lower, 2: upper): C is square and only its lower (upper) triangle is written, alpha·sum + beta·C as
+// elsewhere; the grid holds only the tiles that meet the triangle (square tiles, one product, no split).
+template <class T, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool VEC, bool SCHED = true, bool SPLIT = false,
+          int TRI = 0>
 __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename Mma<T>::Sum> p) {
     using MM = Mma<T>;
     using S = typename MM::Sum;
@@ -206,6 +209,7 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
     constexpr int QG = KRB / 16;                    // 16-byte groups per lane group and row
     constexpr int SPG = 16 / ((int)sizeof(T) * MM::E);   // MFMA steps per 16-byte group
     static_assert(TM * MI == WTM && TN * MI == WTN, "wave tile must be a multiple of the MFMA tile");
+    static_assert(TRI == 0 || (BM == BN && !SPLIT), "triangle mode: square tiles, no split");
     __shared__ __attribute__((aligned(16))) unsigned char lds[2][(BM + BN) * ROWB];
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -214,13 +218,28 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
 
     // tile of this workgroup
     int bid = blockIdx.x;
-    const int nt = p.tiles_m * p.tiles_n, nt8 = nt & ~7;
+    const int nt = TRI ? p.tiles_m * (p.tiles_m + 1) / 2 : p.tiles_m * p.tiles_n, nt8 = nt & ~7;
     if (bid < nt8) bid = (bid & 7) * (nt8 >> 3) + (bid >> 3);
-    constexpr int GM = 4;
-    const int group = bid / (GM * p.tiles_n), first_m = group * GM;
-    const int gsz = min(p.tiles_m - first_m, GM);
-    const int in_group = bid % (GM * p.tiles_n);
-    const int m0 = (first_m + in_group % gsz) * BM, n0 = (in_group / gsz) * BN;
+    int m0, n0;
+    if constexpr (TRI != 0) {
+        // tile bid of the lower triangle of tiles, row by row: (tr, tc) with tc ≤ tr; the upper triangle transposes it
+        int tr = (int)((__builtin_sqrtf(8.f * (float)bid + 1.f) - 1.f) * 0.5f);
+        while ((tr + 1) * (tr + 2) / 2 <= bid) tr++;
+        while (tr * (tr + 1) / 2 > bid) tr--;
+        const int tc = bid - tr * (tr + 1) / 2;
+        m0 = (TRI == 1 ? tr : tc) * BM;
+        n0 = (TRI == 1 ? tc : tr) * BN;
+    } else {
+        constexpr int GM = 4;
+        const int group = bid / (GM * p.tiles_n), first_m = group * GM;
+        const int gsz = min(p.tiles_m - first_m, GM);
+        const int in_group = bid % (GM * p.tiles_n);
+        m0 = (first_m + in_group % gsz) * BM;
+        n0 = (in_group / gsz) * BN;
+    }
+    // elements of a tile on the diagonal are written only inside the triangle
+    const bool diag = TRI != 0 && m0 == n0;
+    const auto in_tri = [&](int m, int n) { return TRI == 1 ? n <= m : n >= m; };
 
     const long long z = blockIdx.y;
     const T *A = reinterpret_cast<const T *>(p.A);
@@ -370,6 +389,17 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
                     const int n = n0 + wn * WTN + i * MI + MM::row(4 * q, lane);
                     if (n >= p.N) continue;
                     const S v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                    if (diag) {
+                        T *c = C + (long long)m * p.ldc + n;
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            if (n + e < p.N && in_tri(m, n + e)) {
+                                S r = p.alpha * v[e];
+                                if (p.beta != S(0)) r = fma_s(p.beta, (S)c[e], r);
+                                c[e] = (T)r;
+                            }
+                        continue;
+                    }
                     if constexpr (SPLIT)
                         store4<S, S>(p.P + z * p.M * (long long)p.N + (long long)m * p.N + n, v, S(1), S(0), p.vec_p, p.N - n);
                     else
@@ -387,7 +417,7 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
 #pragma unroll
                 for (int r = 0; r < MM::NACC; r++) {
                     const int m = m0 + wm * WTM + i * MI + MM::row(r, lane);
-                    if (m >= p.M) continue;
+                    if (m >= p.M || (diag && !in_tri(m, n))) continue;
                     if constexpr (SPLIT) {
                         p.P[z * p.M * (long long)p.N + (long long)m * p.N + n] = acc[i][j][r];
                         continue;

@@ -186,6 +186,58 @@ static int launch_typed(const GemmCall &c) {
     }
 }
 
+// Triangle of a square product (SYRK, SYR2K): alpha·op(A)·op(B) + beta·C written on the lower (upper) triangle of C
+// only. One launch over the T(T+1)/2 square tiles that meet the triangle (T tiles per side), diagonal tiles masked per
+// element, each C element rounded once; the two layouts those routines use: A and B both k-contiguous, or both
+// mn-contiguous.
+template <class T, int TRI, bool AK, bool BKC, bool VEC>
+static int launch_tri_t(GemmParams<typename Mma<T>::Sum> p) {
+    constexpr TileCfg C = sizeof(T) == 8 ? TileCfg{128, 128, 4, 2} : TileCfg{128, 128, 2, 2};
+    p.tiles_m = p.tiles_n = (p.M + C.BM - 1) / C.BM;
+    const long long tiles = (long long)p.tiles_m * (p.tiles_m + 1) / 2;
+    if (tiles > 0x7fffffffLL) G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "triangle product too large (%d tiles per side)", p.tiles_m);
+    hipLaunchKernelGGL((gemm_kernel<T, C.BM, C.BN, C.WM, C.WN, AK, BKC, VEC, true, false, TRI>), dim3((unsigned)tiles),
+                       dim3(C.WM * C.WN * 64), 0, stream, p);
+    G9_HIP(hipGetLastError());
+    return 0;
+}
+template <class T, bool AK, bool BKC>
+static int launch_tri_layout(const GemmParams<typename Mma<T>::Sum> &p, bool vec, bool lower) {
+    if (vec) return lower ? launch_tri_t<T, 1, AK, BKC, true>(p) : launch_tri_t<T, 2, AK, BKC, true>(p);
+    return lower ? launch_tri_t<T, 1, AK, BKC, false>(p) : launch_tri_t<T, 2, AK, BKC, false>(p);
+}
+template <class T>
+static int launch_tri_typed(const GemmCall &c, bool lower) {
+    using S = typename Mma<T>::Sum;
+    GemmParams<S> p;
+    p.A = c.A; p.B = c.B; p.C = c.C;
+    p.lda = c.lda; p.ldb = c.ldb; p.ldc = c.ldc;
+    p.sA = p.sB = p.sC = 0;
+    p.M = c.M; p.N = c.N; p.K = c.K;
+    p.alpha = (S)c.alpha;
+    p.beta = (S)c.beta;
+    p.tiles_m = p.tiles_n = 0;
+    p.P = nullptr;
+    p.kper = p.vec_p = 0;
+    const long long es = sizeof(T);
+    const long long cal = es * 4 < 16 ? es * 4 : 16;
+    p.vec_c = ((uintptr_t)c.C % cal == 0) && (c.ldc * es) % cal == 0;
+    const bool vec = ((uintptr_t)c.A % 16 == 0) && ((uintptr_t)c.B % 16 == 0) && (c.lda * es) % 16 == 0 && (c.ldb * es) % 16 == 0;
+    if (!c.tA && c.tB) return launch_tri_layout<T, true, true>(p, vec, lower);
+    if (c.tA && !c.tB) return launch_tri_layout<T, false, false>(p, vec, lower);
+    G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "triangle product: layout tA=%d tB=%d", c.tA, c.tB);
+}
+int launch_gemm_tri(const GemmCall &c, bool lower) {
+    if (c.M != c.N || c.count != 1) G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "triangle product: %d×%d, batch %d", c.M, c.N, c.count);
+    switch (c.type) {
+    case GEN9BLAS_H:
+    case GEN9BLAS_HS: return launch_tri_typed<f16>(c, lower);
+    case GEN9BLAS_S: return launch_tri_typed<float>(c, lower);
+    case GEN9BLAS_D: return launch_tri_typed<double>(c, lower);
+    }
+    G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "type %d unavailable", c.type);
+}
+
 int launch_gemm(const GemmCall &c) {
     switch (c.type) {
     case GEN9BLAS_H:

@@ -8,17 +8,18 @@
 // - TRMM: B = alpha·op(A)·B (left) or alpha·B·op(A) (right). op(A) is made explicit with zeros outside its triangle;
 //   the product runs in row (left) or column (right) bands, each over only the k range where op(A) is non-zero
 //   (4 bands from n = 512: about 62 % of the full work, as level3.c:28-49), into a work buffer copied back to B;
-// - SYRK / SYR2K: only the uplo triangle of C changes. The product runs in row bands over the columns the triangle
-//   needs (level3.c:76-97) into a work buffer, then a merge kernel writes alpha·product + beta·C on the triangle
-//   (C not read when beta = 0). SYR2K joins X = [op(A) | op(B)] and Y = [op(B) | op(A)] so that
+// - SYRK / SYR2K: only the uplo triangle of C changes. One launch of the GEMM kernel in triangle mode covers the
+//   tiles that meet the triangle and writes alpha·product + beta·C there (C not read when beta = 0), each element
+//   rounded once; the reference runs row bands over the columns the triangle needs (level3.c:76-97) into a work
+//   buffer that is merged afterwards. SYR2K joins X = [op(A) | op(B)] and Y = [op(B) | op(A)] so that
 //   X·Yᵀ = op(A)·op(B)ᵀ + op(B)·op(A)ᵀ is one accumulation (level3.c:109-125);
 // - TRSM: op(A)·X = alpha·B (left) or X·op(A) = alpha·B (right), X overwrites B. As the reference (level3.c:127-215)
 //   the problem is brought to L·Y = alpha·R with L lower triangular (an upper matrix by reversing the index order,
 //   the right side by transposition) and the diagonal blocks of L are inverted in FP64; the substitution then runs on
 //   the GEMM kernels by recursive halving (the reference's per-block-row updates Y_i -= L[i, <i]·X[<i] grouped into a
 //   few large products), each 128-row block finished by X_i = inv(L_ii)·Y_i.
-// Products of the element type round as a GEMM does; the merge / copy passes round once more, as the reference's
-// separate epilogues do.
+// Products of the element type round as a GEMM does; the TRMM copy pass and SYMM's explicit matrix add no rounding
+// (they copy elements of the element type).
 #include "internal.h"
 #include <type_traits>
 
@@ -248,25 +249,24 @@ static int check_type(int type) {
 static int tri_product(int type, int lower, int trans, int N, int K, double alpha, const void *X, ll ldx, const void *Y,
                        ll ldy, double beta, void *C, ll ldc) {
     const int es = elem_size(type);
-    void *P = nullptr;
     if (K > 0 && alpha != 0.0) {
-        G9_TRY(scratch(SLOT_T, (size_t)N * N * es, &P));
-        const int nb = band_rows(N);
-        for (int i0 = 0; i0 < N; i0 += nb) {
-            const int b = N - i0 < nb ? N - i0 : nb;
-            const int c0 = lower ? 0 : i0, c1 = lower ? i0 + b : N;
-            // rows i0.. of op(X) times columns c0..c1 of op(Y)ᵀ
-            const char *xa = (const char *)X + (trans ? (ll)i0 : (ll)i0 * ldx) * es;
-            const char *yb = (const char *)Y + (trans ? (ll)c0 : (ll)c0 * ldy) * es;
-            G9_TRY(dgemm_dev(type, trans, !trans, b, c1 - c0, K, alpha, xa, ldx, yb, ldy, 0.0,
-                             (char *)P + ((ll)i0 * N + c0) * es, N));
-        }
+        // one launch over the tiles of the triangle: C = alpha·op(X)·op(Y)ᵀ + beta·C there, rounded once
+        GemmCall g;
+        g.type = type;
+        g.tA = trans; g.tB = !trans;
+        g.M = N; g.N = N; g.K = K;
+        g.count = 1;
+        g.alpha = alpha; g.beta = beta;
+        g.A = X; g.lda = ldx; g.sA = 0;
+        g.B = Y; g.ldb = ldy; g.sB = 0;
+        g.C = C; g.ldc = ldc; g.sC = 0;
+        return launch_gemm_tri(g, lower != 0);
     }
     return by_es(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
         using S = typename Acc<T>::S;
-        hipLaunchKernelGGL((merge_kernel<T>), dim3(grid_for((ll)N * N)), dim3(256), 0, stream, (const T *)P, (ll)N, (T *)C,
-                           ldc, N, lower, (S)beta);
+        hipLaunchKernelGGL((merge_kernel<T>), dim3(grid_for((ll)N * N)), dim3(256), 0, stream, (const T *)nullptr, (ll)N,
+                           (T *)C, ldc, N, lower, (S)beta);
         G9_HIP(hipGetLastError());
         return 0;
     });
