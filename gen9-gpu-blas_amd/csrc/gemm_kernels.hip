@@ -13,24 +13,31 @@ namespace g9 {
 // Tile configurations, per element type and layout, from a sweep on MI355X at n = 4096 (every variant checked against
 // a float64 reference). Big: the steady-state configuration. Small: smaller tiles for products whose big tiles
 // would leave most of the 256 CUs idle.
-//   FP16 256×256, 8 waves (4×2): NN 794, NT 950 TFLOP/s. FP32 256×128 (NN 117) / 128×128 (NT 127).
-//   FP64 256×128, 8 waves (4×2): 70.6 TFLOP/s.
+//   FP16 256×256, 8 waves (4×2): NN 794, NT 950 TFLOP/s. FP64 256×128, 8 waves (4×2): 70.6 TFLOP/s.
+//   FP32 with A k-contiguous: small tiles with 4 waves, many workgroups per CU. NN 64×128: 123 TFLOP/s at n = 4096,
+//   117 at n = 2048 (256×128: 117 / 105; 128×128, 64×64, 128×64, 64×256 and 2- or 8-wave variants: 74-118). NT
+//   64×64: 126 at n = 4096, 119 on the odd shape 3000×11008×4096 (128×128: 128 / 97, the odd shape's 2064 tiles
+//   being four rounds of 512 workgroups and a nearly empty fifth). Transposed A: 256×128 (TN, TT).
 //   Small at n = 1024 (NN): FP32 64×64 (256 tiles, no split) 69 TFLOP/s against 62 for 128×128 split four ways;
 //   FP64 64×128 split two ways 43, 64×64 41.
 struct TileCfg { int BM, BN, WM, WN; };
 // Layouts whose staging needs more registers than a wave has at 2 waves per SIMD (transposed A, unaligned
 // operands) keep FP16 at 4 waves (512 registers per wave), which compiles without spills.
 template <class T, bool AK, bool BKC, bool VEC> struct Cfg;
+// small_div: the small tile is taken when the big tiles times small_div are fewer than the CUs.
 template <bool AK, bool BKC, bool VEC> struct Cfg<f16, AK, BKC, VEC> {
     static constexpr TileCfg big = (AK && VEC) ? TileCfg{256, 256, 4, 2} : TileCfg{256, 256, 2, 2};
     static constexpr TileCfg small{128, 128, 2, 2};
+    static constexpr int small_div = 2;
 };
 template <bool AK, bool BKC, bool VEC> struct Cfg<float, AK, BKC, VEC> {
-    static constexpr TileCfg big = (AK && BKC) ? TileCfg{128, 128, 2, 2} : TileCfg{256, 128, 2, 2};
+    static constexpr TileCfg big = !AK ? TileCfg{256, 128, 2, 2} : BKC ? TileCfg{64, 64, 2, 2} : TileCfg{64, 128, 2, 2};
     static constexpr TileCfg small{64, 64, 2, 2};
+    static constexpr int small_div = 1;
 };
 template <bool AK, bool BKC, bool VEC> struct Cfg<double, AK, BKC, VEC> {
     static constexpr TileCfg big{256, 128, 4, 2}, small{64, 128, 2, 2};
+    static constexpr int small_div = 2;
 };
 
 // Split-K slices for a single product of `tiles` tiles: doubled while the slices still leave at most one workgroup
@@ -91,7 +98,7 @@ template <class T, bool AK, bool BKC, bool VEC>
 static int launch_layout(const GemmParams<typename Mma<T>::Sum> &p, int count) {
     using CF = Cfg<T, AK, BKC, VEC>;
     const long long big_tiles = (long long)((p.M + CF::big.BM - 1) / CF::big.BM) * ((p.N + CF::big.BN - 1) / CF::big.BN) * count;
-    if (big_tiles * 2 < num_cus) return launch_t<T, CF::small, AK, BKC, VEC>(p, count);
+    if (big_tiles * CF::small_div < num_cus) return launch_t<T, CF::small, AK, BKC, VEC>(p, count);
     return launch_t<T, CF::big, AK, BKC, VEC>(p, count);
 }
 
