@@ -17,7 +17,8 @@ namespace g9 {
 //   FP32 with A k-contiguous: small tiles with 4 waves, many workgroups per CU. NN 64×128: 123 TFLOP/s at n = 4096,
 //   117 at n = 2048 (256×128: 117 / 105; 128×128, 64×64, 128×64, 64×256 and 2- or 8-wave variants: 74-118). NT
 //   64×64: 126 at n = 4096, 119 on the odd shape 3000×11008×4096 (128×128: 128 / 97, the odd shape's 2064 tiles
-//   being four rounds of 512 workgroups and a nearly empty fifth). Transposed A: 256×128 (TN, TT).
+//   being four rounds of 512 workgroups and a nearly empty fifth). Transposed A: TN 128×128 125 (256×128: 117),
+//   TT 128×64 120 (256×128: 117).
 //   Small at n = 1024 (NN): FP32 64×64 (256 tiles, no split) 69 TFLOP/s against 62 for 128×128 split four ways;
 //   FP64 64×128 split two ways 43, 64×64 41.
 struct TileCfg { int BM, BN, WM, WN; };
@@ -31,7 +32,8 @@ template <bool AK, bool BKC, bool VEC> struct Cfg<f16, AK, BKC, VEC> {
     static constexpr int small_div = 2;
 };
 template <bool AK, bool BKC, bool VEC> struct Cfg<float, AK, BKC, VEC> {
-    static constexpr TileCfg big = !AK ? TileCfg{256, 128, 2, 2} : BKC ? TileCfg{64, 64, 2, 2} : TileCfg{64, 128, 2, 2};
+    static constexpr TileCfg big = !AK ? (BKC ? TileCfg{128, 64, 2, 2} : TileCfg{128, 128, 2, 2})
+                                       : (BKC ? TileCfg{64, 64, 2, 2} : TileCfg{64, 128, 2, 2});
     static constexpr TileCfg small{64, 64, 2, 2};
     static constexpr int small_div = 1;
 };
