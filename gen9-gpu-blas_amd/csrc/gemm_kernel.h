@@ -196,8 +196,11 @@ constexpr int SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100, SG_DS_W
 
 // TRI (1: lower, 2: upper): C is square and only its lower (upper) triangle is written, alpha·sum + beta·C as
 // elsewhere; the grid holds only the tiles that meet the triangle (square tiles, one product, no split).
+// KLIM: the k range of a tile is cut to where a triangular operand is non-zero (one product, no split):
+//   1: op(A) lower, k < m0 + BM; 2: op(A) upper, k ≥ m0; 3: op(B) lower, k ≥ n0; 4: op(B) upper, k < n0 + BN.
+//   Tiles are dispatched longest range first, spread over the XCDs.
 template <class T, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool VEC, bool SCHED = true, bool SPLIT = false,
-          int TRI = 0>
+          int TRI = 0, int KLIM = 0>
 __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename Mma<T>::Sum> p) {
     using MM = Mma<T>;
     using S = typename MM::Sum;
@@ -210,6 +213,7 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
     constexpr int SPG = 16 / ((int)sizeof(T) * MM::E);   // MFMA steps per 16-byte group
     static_assert(TM * MI == WTM && TN * MI == WTN, "wave tile must be a multiple of the MFMA tile");
     static_assert(TRI == 0 || (BM == BN && !SPLIT), "triangle mode: square tiles, no split");
+    static_assert(KLIM == 0 || (!SPLIT && TRI == 0), "k-limited tiles: one product, no split");
     __shared__ __attribute__((aligned(16))) unsigned char lds[2][(BM + BN) * ROWB];
 
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -229,6 +233,20 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
         const int tc = bid - tr * (tr + 1) / 2;
         m0 = (TRI == 1 ? tr : tc) * BM;
         n0 = (TRI == 1 ? tc : tr) * BN;
+    } else if constexpr (KLIM != 0) {
+        // Tiles in dispatch order, longest k range first, without the XCD remap: consecutive workgroups go to
+        // different XCDs, so every XCD gets long and short tiles alike (a contiguous range per XCD would give one XCD
+        // all the longest tiles)
+        const int b = blockIdx.x;
+        if constexpr (KLIM <= 2) {   // the range depends on the tile row
+            const int tr = b / p.tiles_n;
+            m0 = (KLIM == 1 ? p.tiles_m - 1 - tr : tr) * BM;
+            n0 = (b % p.tiles_n) * BN;
+        } else {                     // on the tile column
+            const int tc = b / p.tiles_m;
+            n0 = (KLIM == 4 ? p.tiles_n - 1 - tc : tc) * BN;
+            m0 = (b % p.tiles_m) * BM;
+        }
     } else {
         constexpr int GM = 4;
         const int group = bid / (GM * p.tiles_n), first_m = group * GM;
@@ -246,9 +264,16 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
     const T *B = reinterpret_cast<const T *>(p.B);
     T *C = reinterpret_cast<T *>(p.C);
     int K = p.K;
-    if constexpr (SPLIT) {
-        const int k0 = (int)z * p.kper;
-        K = min(p.K - k0, p.kper);
+    if constexpr (SPLIT || KLIM != 0) {
+        int k0, k1;
+        if constexpr (SPLIT) {
+            k0 = (int)z * p.kper;
+            k1 = min(p.K, k0 + p.kper);
+        } else {
+            k0 = KLIM == 2 ? m0 : KLIM == 3 ? n0 : 0;
+            k1 = KLIM == 1 ? min(p.K, m0 + BM) : KLIM == 4 ? min(p.K, n0 + BN) : p.K;
+        }
+        K = max(k1 - k0, 0);
         A += AK ? k0 : (long long)k0 * p.lda;
         B += BKC ? k0 : (long long)k0 * p.ldb;
     } else {

@@ -248,6 +248,61 @@ int launch_gemm_tri(const GemmCall &c, bool lower) {
     G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "type %d unavailable", c.type);
 }
 
+// Product with a triangular operand (TRMM on the explicit triangular matrix): each tile's k range is cut to where the
+// triangle is non-zero (klim as gemm_kernel's KLIM), one launch over every tile of C, longest ranges dispatched first.
+// Layout NN only (both operands as stored), one product.
+template <class T, int KLIM, bool VEC>
+static int launch_klim_t(GemmParams<typename Mma<T>::Sum> p) {
+    constexpr TileCfg C = Cfg<T, true, false, VEC>::big;
+    p.tiles_m = (p.M + C.BM - 1) / C.BM;
+    p.tiles_n = (p.N + C.BN - 1) / C.BN;
+    const long long tiles = (long long)p.tiles_m * p.tiles_n;
+    if (tiles > 0x7fffffffLL) G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "gemm grid too large (%d × %d tiles)", p.tiles_m, p.tiles_n);
+    hipLaunchKernelGGL((gemm_kernel<T, C.BM, C.BN, C.WM, C.WN, true, false, VEC, true, false, 0, KLIM>), dim3((unsigned)tiles),
+                       dim3(C.WM * C.WN * 64), 0, stream, p);
+    G9_HIP(hipGetLastError());
+    return 0;
+}
+template <class T>
+static int launch_klim_typed(const GemmCall &c, int klim) {
+    using S = typename Mma<T>::Sum;
+    GemmParams<S> p;
+    p.A = c.A; p.B = c.B; p.C = c.C;
+    p.lda = c.lda; p.ldb = c.ldb; p.ldc = c.ldc;
+    p.sA = p.sB = p.sC = 0;
+    p.M = c.M; p.N = c.N; p.K = c.K;
+    p.alpha = (S)c.alpha;
+    p.beta = (S)c.beta;
+    p.tiles_m = p.tiles_n = 0;
+    p.P = nullptr;
+    p.kper = p.vec_p = 0;
+    const long long es = sizeof(T);
+    const long long cal = es * 4 < 16 ? es * 4 : 16;
+    p.vec_c = ((uintptr_t)c.C % cal == 0) && (c.ldc * es) % cal == 0;
+    const bool vec = ((uintptr_t)c.A % 16 == 0) && ((uintptr_t)c.B % 16 == 0) && (c.lda * es) % 16 == 0 && (c.ldb * es) % 16 == 0;
+    switch (klim * 2 + (vec ? 1 : 0)) {
+    case 2: return launch_klim_t<T, 1, false>(p);
+    case 3: return launch_klim_t<T, 1, true>(p);
+    case 4: return launch_klim_t<T, 2, false>(p);
+    case 5: return launch_klim_t<T, 2, true>(p);
+    case 6: return launch_klim_t<T, 3, false>(p);
+    case 7: return launch_klim_t<T, 3, true>(p);
+    case 8: return launch_klim_t<T, 4, false>(p);
+    case 9: return launch_klim_t<T, 4, true>(p);
+    }
+    G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "k-limited product: mode %d", klim);
+}
+int launch_gemm_klim(const GemmCall &c, int klim) {
+    if (c.tA || c.tB || c.count != 1) G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "k-limited product: layout tA=%d tB=%d, batch %d", c.tA, c.tB, c.count);
+    switch (c.type) {
+    case GEN9BLAS_H:
+    case GEN9BLAS_HS: return launch_klim_typed<f16>(c, klim);
+    case GEN9BLAS_S: return launch_klim_typed<float>(c, klim);
+    case GEN9BLAS_D: return launch_klim_typed<double>(c, klim);
+    }
+    G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "type %d unavailable", c.type);
+}
+
 int launch_gemm(const GemmCall &c) {
     switch (c.type) {
     case GEN9BLAS_H:

@@ -92,6 +92,9 @@ struct GemmCall {
 G9_HIDDEN int launch_gemm(const GemmCall &c);
 // Lower (upper) triangle only of a square product, C = alpha·op(A)·op(B) + beta·C there (tA != tB, count 1).
 G9_HIDDEN int launch_gemm_tri(const GemmCall &c, bool lower);
+// NN product whose tiles take only the k range where a triangular operand is non-zero: klim 1 op(A) lower, 2 op(A)
+// upper, 3 op(B) lower, 4 op(B) upper (count 1).
+G9_HIDDEN int launch_gemm_klim(const GemmCall &c, int klim);
 // The whole gen9blas_gemm_batched call: checks, operand resolution, skinny / MFMA dispatch, wait (gemm.hip).
 G9_HIDDEN int gemm_impl(int type, int tA, int tB, int M, int N, int K, double alpha, const void *A, int lda, long long sA,
                         const void *B, int ldb, long long sB, double beta, void *C, int ldc, long long sC, int count);

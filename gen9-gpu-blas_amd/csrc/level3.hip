@@ -6,8 +6,8 @@
 //   13-60), the symmetric matrix is first made explicit from its triangle (here into a device work buffer), then one
 //   GEMM runs;
 // - TRMM: B = alpha·op(A)·B (left) or alpha·B·op(A) (right). op(A) is made explicit with zeros outside its triangle;
-//   the product runs in row (left) or column (right) bands, each over only the k range where op(A) is non-zero
-//   (4 bands from n = 512: about 62 % of the full work, as level3.c:28-49), into a work buffer copied back to B;
+//   one product then runs with each tile over only the k range where op(A) is non-zero (about half of the full work;
+//   the reference uses 4 row or column bands, level3.c:28-49: 62 %), into a work buffer copied back to B;
 // - SYRK / SYR2K: only the uplo triangle of C changes. One launch of the GEMM kernel in triangle mode covers the
 //   tiles that meet the triangle and writes alpha·product + beta·C there (C not read when beta = 0), each element
 //   rounded once; the reference runs row bands over the columns the triangle needs (level3.c:76-97) into a work
@@ -234,12 +234,6 @@ struct TrsmSolve {
     }
 };
 
-static int bands(int n) { return n >= 512 ? 4 : 1; }
-static int band_rows(int n) {
-    const int p = bands(n);
-    return ((n + p - 1) / p + 127) / 128 * 128;
-}
-
 static int check_type(int type) {
     if (type < 0 || type > 3) G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "type %d unavailable", type);
     return 0;
@@ -331,20 +325,17 @@ int gen9blas_trmm(int type, int side, int uplo, int transA, int diag, int M, int
         return 0;
     }));
     const ll ldB = ops[1].ld;
-    const char *Bd = (const char *)ops[1].dev;
-    const int nb = band_rows(n);
-    for (int i0 = 0; i0 < n; i0 += nb) {
-        const int b = n - i0 < nb ? n - i0 : nb;
-        if (left) {   // Z rows i0..i0+b = alpha·F[i0.., k0..k1]·B[k0..k1, :]
-            const int k0 = lower ? 0 : i0, k1 = lower ? i0 + b : n;
-            G9_TRY(dgemm_dev(type, 0, 0, b, N, k1 - k0, alpha, (const char *)F + ((ll)i0 * n + k0) * es, n,
-                             Bd + (ll)k0 * ldB * es, ldB, 0.0, (char *)Z + (ll)i0 * N * es, N));
-        } else {      // Z columns i0..i0+b = alpha·B[:, k0..k1]·F[k0..k1, i0..]
-            const int k0 = lower ? i0 : 0, k1 = lower ? n : i0 + b;
-            G9_TRY(dgemm_dev(type, 0, 0, M, b, k1 - k0, alpha, Bd + (ll)k0 * es, ldB,
-                             (const char *)F + ((ll)k0 * n + i0) * es, n, 0.0, (char *)Z + (ll)i0 * es, N));
-        }
-    }
+    // Z = alpha·F·B (left) or alpha·B·F (right) in one launch, each tile over the k range where F is non-zero
+    GemmCall g;
+    g.type = type;
+    g.tA = g.tB = 0;
+    g.M = M; g.N = N; g.K = n;
+    g.count = 1;
+    g.alpha = alpha; g.beta = 0.0;
+    g.A = left ? F : ops[1].dev; g.lda = left ? n : ldB; g.sA = 0;
+    g.B = left ? ops[1].dev : F; g.ldb = left ? ldB : n; g.sB = 0;
+    g.C = Z; g.ldc = N; g.sC = 0;
+    G9_TRY(launch_gemm_klim(g, left ? (lower ? 1 : 2) : (lower ? 3 : 4)));
     G9_HIP(hipMemcpy2DAsync(ops[1].dev, (size_t)ldB * es, Z, (size_t)N * es, (size_t)N * es, (size_t)M,
                             hipMemcpyDeviceToDevice, stream));
     return finish(ops, 2);
