@@ -93,7 +93,9 @@ __global__ void __launch_bounds__(NT) mv_kernel(Shape s, const T *__restrict__ a
     const int g0 = g * 64 * V, g1 = min(g0 + 64 * V, s.ncols) - 1, c0 = g0 + lane * V;
     const int rpw = rpp / (NT / 64);
     // rows whose stored range can reach the group's columns, within this wave's quarter of the band
-    int rb = blockIdx.y * rpp + w * rpw, re = min(s.nrows, rb + rpw);
+    // an upper triangle's long row bands come first in the matrix: they are dispatched last, as a lower triangle's
+    const int bandi = s.tri == TRI_UPPER ? (int)gridDim.y - 1 - (int)blockIdx.y : (int)blockIdx.y;
+    int rb = bandi * rpp + w * rpw, re = min(s.nrows, rb + rpw);
     if (s.tri == TRI_LOWER) rb = max(rb, g0);
     if (s.tri == TRI_UPPER) re = min(re, g1 + 1);
     if (band) {
@@ -222,7 +224,7 @@ __global__ void __launch_bounds__(NT) mv_kernel(Shape s, const T *__restrict__ a
                 R t = red[0][lane * V + e];
 #pragma unroll
                 for (int q = 1; q < NT / 64; q++) t += red[q][lane * V + e];
-                if (c0 + e < s.ncols) P[(ll)blockIdx.y * s.ncols + c0 + e] = t;
+                if (c0 + e < s.ncols) P[(ll)bandi * s.ncols + c0 + e] = t;
             }
         }
     }
@@ -290,7 +292,8 @@ __global__ void __launch_bounds__(NT) rank_kernel(Shape s, typename Comp<T>::R a
     const int g = blockIdx.x, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g0 = g * 64 * V, g1 = min(g0 + 64 * V, s.ncols) - 1, c0 = g0 + lane * V;
     const int rpw = rpp / (NT / 64);
-    int rb = blockIdx.y * rpp + w * rpw, re = min(s.nrows, rb + rpw);
+    const int bandi = s.tri == TRI_UPPER ? (int)gridDim.y - 1 - (int)blockIdx.y : (int)blockIdx.y;   // as mv_kernel
+    int rb = bandi * rpp + w * rpw, re = min(s.nrows, rb + rpw);
     if (s.tri == TRI_LOWER) rb = max(rb, g0);
     if (s.tri == TRI_UPPER) re = min(re, g1 + 1);
     if (band) {
