@@ -392,16 +392,8 @@ __device__ __forceinline__ double lane_value(double v, int k) {
     return __builtin_bit_cast(double, (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
 }
 
-// Diagonal block [p, p + b) of op(A), b ≤ SB. In solve order (r' = r, c' = c for forward substitution, op(A)
-// lower; both reversed for backward substitution, so the solve below is always forward) the entries below the
-// diagonal, op(A)(p + r, p + c) with c' < r', go to Lt[c'][r'] (column-major, padded rows against bank conflicts);
-// the diagonal goes to dg[r'] and Lt holds zeros on and above it. The block is read along rows of A, a thread's 64
-// loads all in flight at once. The substitution runs in one wave: lane l owns rows l and l + 64 and the reciprocals of
-// their diagonal entries. At step k, x_k = v_k·(1/d_k) is read from lane k and every row subtracts Lt[k][row]·x_k: a
-// row's value stops changing once its own step is past, since its column entries there are zero. Columns are read from
-// LDS 8 steps at a time, so the sequential chain per step is a multiply, a lane read and a fused multiply-add
-// (reference: level12.cl:493-548; the reference divides by the diagonal, here its reciprocal is taken once: the
-// solution differs by rounding only).
+// Diagonal block [p, p + b) of op(A), b ≤ SB: loaded by the whole workgroup (a thread's 64 loads all in flight at
+// once), stored in LDS as it lies in A, and substituted by one wave (see solve).
 template <class T, int FMT>
 struct Diag {
     using R = typename Comp<T>::R;
@@ -431,79 +423,102 @@ struct Diag {
         }
     }
 
-    // (q, w): element of A in the block; (r, c): the same element in op(A); (r2, c2): in solve order. The four
-    // (transpose, direction) cases are separate loops, so each index is a register or a constant offset. Indices at
-    // or past b (a partial block) wrap to [b, SB) under backward order: a column there is never read and a row there
-    // belongs to a lane whose value is dropped, and the zero stored there meets no entry in use.
-    template <bool TR, bool FW>
-    __device__ __forceinline__ void place(const Shape &s, int b, R (*Lt)[SB + 1], R *dg) const {
-        constexpr bool LOW = TR != FW;   // A's stored triangle: op(A) is lower (forward) iff A lower xor transposed
+    // The loaded block goes to LDS as it lies in A: raw[q][w] = A(p + q, p + w), rows padded to SB + 1 elements, so a
+    // thread's stores are constant offsets from one address. A band's entries outside the band (read from a clamped
+    // address) are stored as zeros; every other entry outside the solve's triangle is left as loaded: the
+    // substitution never lets it reach a live value (see solve).
+    __device__ __forceinline__ void place(const Shape &s, R (*raw)[SB + 1]) const {
         const int w = threadIdx.x % SB, q0 = __builtin_amdgcn_readfirstlane(threadIdx.x / SB);
-        const int bw = LOW ? s.KL : s.KU;
+        const bool lowA = s.tri == TRI_LOWER;
+        const int bw = lowA ? s.KL : s.KU;
 #pragma unroll
         for (int u = 0; u < RPT; u++) {
             const int q = u * (NT / SB) + q0;
-            const int d = LOW ? q - w : w - q;   // distance from the diagonal into the stored triangle
-            const bool need = q < b && w < b && d >= 0 && (FMT != F_BAND || d <= bw);
-            const R vu = need ? (R)e[u] : R(0);
-            const int r = TR ? w : q, c = TR ? q : w;
-            const int r2 = FW ? r : (b - 1 - r) & (SB - 1), c2 = FW ? c : (b - 1 - c) & (SB - 1);
-            Lt[c2][r2] = c2 < r2 ? vu : R(0);
-            if (c2 == r2) dg[r2] = vu;
+            R v = (R)e[u];
+            if constexpr (FMT == F_BAND) {
+                const int d = lowA ? q - w : w - q;
+                if (d > bw) v = R(0);
+            }
+            raw[q][w] = v;
         }
     }
 
     // Places the loaded block in LDS, then wave 0 substitutes, starting from the block's right-hand side rhs[0 .. b)
     // (in A's row order, in LDS), and writes x of the block to xf. Called by the whole workgroup; the barrier orders
     // the writes of rhs before wave 0 reads it.
+    // In solve order (r' = r, c' = c forward; both reversed backward, so the solve is always forward) step k takes
+    // x_k = v_k·(1/d_k) from lane k and subtracts op(A)(r', k)·x_k from every row r'. Lane l owns rows l and l + 64.
+    // Rows below k receive their true entries (they lie in the stored triangle); rows at or above k receive whatever
+    // the block holds there, possibly not even finite, but a row's value is final at its own step: each lane keeps
+    // x of its row from that step (rows l at steps k < 64, rows l + 64 at steps k ≥ 64) and v_k at step k has only
+    // received entries of rows below earlier steps. Columns are read from LDS 8 steps at a time, so the sequential
+    // chain per step is a multiply, a lane read and a fused multiply-add (reference: level12.cl:493-548; the
+    // reference divides by the diagonal, here its reciprocal is taken once: the solution differs by rounding only).
     __device__ __forceinline__ void solve(const Shape &s, int trans, int fwd, int p, int b, const R *rhs, R *xf,
-                                          R (*Lt)[SB + 1], R *dg) const {
-        if (trans) {
-            if (fwd) place<true, true>(s, b, Lt, dg);
-            else place<true, false>(s, b, Lt, dg);
-        } else {
-            if (fwd) place<false, true>(s, b, Lt, dg);
-            else place<false, false>(s, b, Lt, dg);
-        }
+                                          R (*raw)[SB + 1]) const {
+        place(s, raw);
         __syncthreads();
         if (threadIdx.x >= 64) return;
+        if (trans) {
+            if (fwd) substitute<true, true>(s, p, b, rhs, xf, raw);
+            else substitute<true, false>(s, p, b, rhs, xf, raw);
+        } else {
+            if (fwd) substitute<false, true>(s, p, b, rhs, xf, raw);
+            else substitute<false, false>(s, p, b, rhs, xf, raw);
+        }
+    }
+    template <bool TR, bool FW>
+    __device__ __forceinline__ void substitute(const Shape &s, int p, int b, const R *rhs, R *xf, R (*raw)[SB + 1]) const {
         const int l = threadIdx.x, n0 = b < 64 ? b : 64;
-        const auto idx = [&](int r) { return fwd ? r : b - 1 - r; };   // row of the block in A's order
+        // row of the block in A's order for solve-order index x; lanes past b wrap into the block (values dropped)
+        const auto idx = [&](int x) { return (FW ? x : b - 1 - x) & (SB - 1); };
         const bool has1 = l + 64 < b;
-        R v0 = l < b ? rhs[idx(l)] : R(0), v1 = has1 ? rhs[idx(l + 64)] : R(0);
-        const R r0 = s.unit || l >= b ? R(1) : R(1) / dg[l], r1 = s.unit || !has1 ? R(1) : R(1) / dg[l + 64];
-        // rows at or past b read stale LDS: they belong to lanes whose values are never written back
-        const auto col = [&](int k, int row) { return Lt[k][row]; };
+        const int i0 = idx(l), i1 = idx(l + 64);
+        R v0 = l < b ? rhs[i0] : R(0), v1 = has1 ? rhs[i1] : R(0);
+        const R r0 = s.unit || l >= b ? R(1) : R(1) / raw[i0][i0], r1 = s.unit || !has1 ? R(1) : R(1) / raw[i1][i1];
+        // op(A) in solve order at (row of A i, step k); k < b, so the column index needs no wrap
+        const auto col = [&](int k, int i) { const int j = FW ? k : b - 1 - k; return TR ? raw[j][i] : raw[i][j]; };
+        R x0 = 0, x1 = 0;
         int k = 0;
         for (; k + KS <= n0; k += KS) {
             R c0[KS], c1[KS];
 #pragma unroll
             for (int u = 0; u < KS; u++) {
-                c0[u] = col(k + u, l);
-                c1[u] = col(k + u, l + 64);
+                c0[u] = col(k + u, i0);
+                c1[u] = col(k + u, i1);
             }
 #pragma unroll
             for (int u = 0; u < KS; u++) {
-                const R xk = lane_value(v0 * r0, k + u);
+                const R y = v0 * r0, xk = lane_value(y, k + u);
+                if (l == k + u) x0 = y;
                 v0 = fma_r(-c0[u], xk, v0);
                 v1 = fma_r(-c1[u], xk, v1);
             }
         }
         for (; k < n0; k++) {
-            const R xk = lane_value(v0 * r0, k);
-            v0 = fma_r(-col(k, l), xk, v0);
-            v1 = fma_r(-col(k, l + 64), xk, v1);
+            const R y = v0 * r0, xk = lane_value(y, k);
+            if (l == k) x0 = y;
+            v0 = fma_r(-col(k, i0), xk, v0);
+            v1 = fma_r(-col(k, i1), xk, v1);
         }
         for (; k + KS <= b; k += KS) {
             R c1[KS];
 #pragma unroll
-            for (int u = 0; u < KS; u++) c1[u] = col(k + u, l + 64);
+            for (int u = 0; u < KS; u++) c1[u] = col(k + u, i1);
 #pragma unroll
-            for (int u = 0; u < KS; u++) v1 = fma_r(-c1[u], lane_value(v1 * r1, k + u - 64), v1);
+            for (int u = 0; u < KS; u++) {
+                const R y = v1 * r1, xk = lane_value(y, k + u - 64);
+                if (l == k + u - 64) x1 = y;
+                v1 = fma_r(-c1[u], xk, v1);
+            }
         }
-        for (; k < b; k++) v1 = fma_r(-col(k, l + 64), lane_value(v1 * r1, k - 64), v1);
-        if (l < b) xf[p + idx(l)] = v0 * r0;
-        if (has1) xf[p + idx(l + 64)] = v1 * r1;
+        for (; k < b; k++) {
+            const R y = v1 * r1, xk = lane_value(y, k - 64);
+            if (l == k - 64) x1 = y;
+            v1 = fma_r(-col(k, i1), xk, v1);
+        }
+        if (l < b) xf[p + i0] = x0;
+        if (has1) xf[p + i1] = x1;
     }
 };
 
@@ -616,8 +631,7 @@ __global__ void __launch_bounds__(NT) solve_step(Shape s, const T *__restrict__ 
                                                  int b, int t0, int t1, int o0, int o1, typename Comp<T>::R *xf) {
     using R = typename Comp<T>::R;
     constexpr int RPT = SB * SB / NT;
-    __shared__ R Lt[SB][SB + 1];
-    __shared__ R dg[SB];
+    __shared__ R raw[SB][SB + 1];
     __shared__ R red[NT / 64][64];
     __shared__ R xp[SB], rhs[SB];
     if (blockIdx.x > 0) {
@@ -661,7 +675,7 @@ __global__ void __launch_bounds__(NT) solve_step(Shape s, const T *__restrict__ 
         }
     }
     if (tid < b) rhs[tid] = own - sum;
-    d.solve(s, trans, fwd, p, b, rhs, xf, Lt, dg);
+    d.solve(s, trans, fwd, p, b, rhs, xf, raw);
 }
 
 // ---------------- launchers ----------------
