@@ -400,6 +400,7 @@ struct Diag {
     static constexpr int RPT = SB * SB / NT;   // elements per thread
     static constexpr int KS = 8;               // steps per LDS read
     T e[RPT];
+    T d0, d1;   // wave 0: the diagonal entries of lane l's rows (see substitute)
 
     // Column w of A in the block; first row q0 (uniform across a wave: row offsets are scalar). Element (q, w),
     // A(p + q, p + w), is needed where it lies in A's stored triangle (the solve uses no other entry) and, for a
@@ -407,7 +408,14 @@ struct Diag {
     // clamped into storage: rows past the block re-read its last row, and outside full storage the column is
     // clamped into the row's stored entries (the diagonal is always among them: a unit diagonal that is not
     // referenced is still in storage). The values that are not needed are replaced by zero when placed.
-    __device__ __forceinline__ void load(const Shape &s, const T *__restrict__ a, int p, int b) {
+    __device__ __forceinline__ void load(const Shape &s, const T *__restrict__ a, int p, int b, int fwd) {
+        if (threadIdx.x < 64) {   // the diagonal of the rows lane l substitutes (clamped into the block)
+            const int l = threadIdx.x;
+            const int i0 = min(fwd ? l : b - 1 - l, b - 1), i1 = min(fwd ? l + 64 : b - 1 - (l + 64), b - 1);
+            const int j0 = max(i0, 0), j1 = max(i1, 0);
+            d0 = a[row_start<FMT>(s, p + j0) + p + j0];
+            d1 = a[row_start<FMT>(s, p + j1) + p + j1];
+        }
         const int w = threadIdx.x % SB, q0 = __builtin_amdgcn_readfirstlane(threadIdx.x / SB);
         const bool lowA = s.tri == TRI_LOWER;
         const int bw = lowA ? s.KL : s.KU;   // band width on the stored side
@@ -424,9 +432,9 @@ struct Diag {
     }
 
     // The loaded block goes to LDS as it lies in A: raw[q][w] = A(p + q, p + w), rows padded to SB + 1 elements, so a
-    // thread's stores are constant offsets from one address. A band's entries outside the band (read from a clamped
-    // address) are stored as zeros; every other entry outside the solve's triangle is left as loaded: the
-    // substitution never lets it reach a live value (see solve).
+    // thread's stores are constant offsets from one address. Only the strict stored triangle is kept (and, for a
+    // band, the band): the diagonal and the other triangle are stored as zeros, so a row stops changing once its own
+    // step is past. The substitution order (transpose, direction) is applied when the block is read.
     __device__ __forceinline__ void place(const Shape &s, R (*raw)[SB + 1]) const {
         const int w = threadIdx.x % SB, q0 = __builtin_amdgcn_readfirstlane(threadIdx.x / SB);
         const bool lowA = s.tri == TRI_LOWER;
@@ -434,12 +442,8 @@ struct Diag {
 #pragma unroll
         for (int u = 0; u < RPT; u++) {
             const int q = u * (NT / SB) + q0;
-            R v = (R)e[u];
-            if constexpr (FMT == F_BAND) {
-                const int d = lowA ? q - w : w - q;
-                if (d > bw) v = R(0);
-            }
-            raw[q][w] = v;
+            const int d = lowA ? q - w : w - q;   // distance from the diagonal into the stored triangle
+            raw[q][w] = d > 0 && (FMT != F_BAND || d <= bw) ? (R)e[u] : R(0);
         }
     }
 
@@ -447,13 +451,12 @@ struct Diag {
     // (in A's row order, in LDS), and writes x of the block to xf. Called by the whole workgroup; the barrier orders
     // the writes of rhs before wave 0 reads it.
     // In solve order (r' = r, c' = c forward; both reversed backward, so the solve is always forward) step k takes
-    // x_k = v_k·(1/d_k) from lane k and subtracts op(A)(r', k)·x_k from every row r'. Lane l owns rows l and l + 64.
-    // Rows below k receive their true entries (they lie in the stored triangle); rows at or above k receive whatever
-    // the block holds there, possibly not even finite, but a row's value is final at its own step: each lane keeps
-    // x of its row from that step (rows l at steps k < 64, rows l + 64 at steps k ≥ 64) and v_k at step k has only
-    // received entries of rows below earlier steps. Columns are read from LDS 8 steps at a time, so the sequential
-    // chain per step is a multiply, a lane read and a fused multiply-add (reference: level12.cl:493-548; the
-    // reference divides by the diagonal, here its reciprocal is taken once: the solution differs by rounding only).
+    // x_k = v_k·(1/d_k) from lane k and subtracts op(A)(r', k)·x_k from every row r'. Lane l owns rows l and l + 64
+    // and the reciprocals of their diagonal entries; a row's entries on and above the diagonal are zero in LDS, so
+    // its value stops changing once its own step is past. Columns are read from LDS 8 steps at a time, so the
+    // sequential chain per step is a multiply, a lane read and a fused multiply-add (reference: level12.cl:493-548;
+    // the reference divides by the diagonal, here its reciprocal is taken once: the solution differs by rounding
+    // only).
     __device__ __forceinline__ void solve(const Shape &s, int trans, int fwd, int p, int b, const R *rhs, R *xf,
                                           R (*raw)[SB + 1]) const {
         place(s, raw);
@@ -475,10 +478,9 @@ struct Diag {
         const bool has1 = l + 64 < b;
         const int i0 = idx(l), i1 = idx(l + 64);
         R v0 = l < b ? rhs[i0] : R(0), v1 = has1 ? rhs[i1] : R(0);
-        const R r0 = s.unit || l >= b ? R(1) : R(1) / raw[i0][i0], r1 = s.unit || !has1 ? R(1) : R(1) / raw[i1][i1];
+        const R r0 = s.unit || l >= b ? R(1) : R(1) / (R)d0, r1 = s.unit || !has1 ? R(1) : R(1) / (R)d1;
         // op(A) in solve order at (row of A i, step k); k < b, so the column index needs no wrap
         const auto col = [&](int k, int i) { const int j = FW ? k : b - 1 - k; return TR ? raw[j][i] : raw[i][j]; };
-        R x0 = 0, x1 = 0;
         int k = 0;
         for (; k + KS <= n0; k += KS) {
             R c0[KS], c1[KS];
@@ -489,15 +491,13 @@ struct Diag {
             }
 #pragma unroll
             for (int u = 0; u < KS; u++) {
-                const R y = v0 * r0, xk = lane_value(y, k + u);
-                if (l == k + u) x0 = y;
+                const R xk = lane_value(v0 * r0, k + u);
                 v0 = fma_r(-c0[u], xk, v0);
                 v1 = fma_r(-c1[u], xk, v1);
             }
         }
         for (; k < n0; k++) {
-            const R y = v0 * r0, xk = lane_value(y, k);
-            if (l == k) x0 = y;
+            const R xk = lane_value(v0 * r0, k);
             v0 = fma_r(-col(k, i0), xk, v0);
             v1 = fma_r(-col(k, i1), xk, v1);
         }
@@ -506,19 +506,11 @@ struct Diag {
 #pragma unroll
             for (int u = 0; u < KS; u++) c1[u] = col(k + u, i1);
 #pragma unroll
-            for (int u = 0; u < KS; u++) {
-                const R y = v1 * r1, xk = lane_value(y, k + u - 64);
-                if (l == k + u - 64) x1 = y;
-                v1 = fma_r(-c1[u], xk, v1);
-            }
+            for (int u = 0; u < KS; u++) v1 = fma_r(-c1[u], lane_value(v1 * r1, k + u - 64), v1);
         }
-        for (; k < b; k++) {
-            const R y = v1 * r1, xk = lane_value(y, k - 64);
-            if (l == k - 64) x1 = y;
-            v1 = fma_r(-col(k, i1), xk, v1);
-        }
-        if (l < b) xf[p + i0] = x0;
-        if (has1) xf[p + i1] = x1;
+        for (; k < b; k++) v1 = fma_r(-col(k, i1), lane_value(v1 * r1, k - 64), v1);
+        if (l < b) xf[p + i0] = v0 * r0;
+        if (has1) xf[p + i1] = v1 * r1;
     }
 };
 
@@ -645,7 +637,7 @@ __global__ void __launch_bounds__(NT) solve_step(Shape s, const T *__restrict__ 
     // coupling region: rows [R0, R0 + br), columns [C0, C0 + bc) of A
     const int R0 = trans ? pp : p, br = trans ? pb : b, C0 = trans ? p : pp, bc = trans ? b : pb;
     Diag<T, FMT> d;
-    d.load(s, a, p, b);
+    d.load(s, a, p, b, fwd);
     T eo[RPT];
     if (upd) load_region<T, FMT>(s, a, R0, br, C0, bc, eo);
     const R own = tid < b ? xf[p + tid] : R(0);
