@@ -167,6 +167,32 @@ def test_gemm_nothing_outside_c(g9, torch_dev):
                                    rtol=0, atol=2e-3 if dt == np.float16 else 1e-5)
 
 
+def test_host_operands_staged(g9):
+    """Host (pageable NumPy) operands of 4 MiB and more move through the pinned staging ring in chunks: whole spans
+    (A, B, C 18-36 MB, several 8 MiB chunks each way) and re-pitched rows (A and C column slices of arrays three times
+    wider, so their row gaps exceed half the span: 2D copies chunked by rows, C copied back row by row). Small-integer
+    inputs make every result exact; nothing outside the C slice changes."""
+    rng = np.random.default_rng(31)
+    A = rng.integers(-2, 3, (3000, 1500)).astype(np.float32)
+    B = rng.integers(-2, 3, (1500, 3000)).astype(np.float32)
+    C0 = rng.integers(-2, 3, (3000, 3000)).astype(np.float32)
+    C = C0.copy()
+    g9.gemm(A, B, 1.0, 2.0, C)
+    ref = A.astype(np.int64) @ B.astype(np.int64) + 2 * C0.astype(np.int64)
+    assert np.array_equal(C.astype(np.int64), ref), "whole spans"
+    big_a = rng.integers(-2, 3, (3000, 3000)).astype(np.float32)
+    big_c = rng.integers(-2, 3, (3000, 3000)).astype(np.float32)
+    keep = big_c.copy()
+    A2, C2 = big_a[:, 1000:2000], big_c[:, 500:1500]
+    B2 = B[:1000, :1000].copy()
+    g9.gemm(A2, B2, 1.0, 2.0, C2)
+    ref = A2.astype(np.int64) @ B2.astype(np.int64) + 2 * keep[:, 500:1500].astype(np.int64)
+    assert np.array_equal(big_c[:, 500:1500].astype(np.int64), ref), "re-pitched rows"
+    mask = np.ones(big_c.shape, bool)
+    mask[:, 500:1500] = False
+    assert np.array_equal(big_c[mask], keep[mask]), "write outside the C slice"
+
+
 def test_gemm_beta_zero_does_not_read_c(g9, torch_dev):
     """beta = 0: C is not read, NaN in C does not propagate (reference: lib/gen9blas.h:133 semantics for C)."""
     for dt in (np.float16, np.float32, np.float64):
