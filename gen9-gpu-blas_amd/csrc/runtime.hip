@@ -16,6 +16,7 @@
 #include <stdlib.h>
 #include <string.h>
 #include <time.h>
+#include <unistd.h>
 #include <condition_variable>
 #include <functional>
 #include <map>
@@ -209,8 +210,14 @@ struct Pool {
     }
 };
 static Pool *pool;
+static pid_t pool_pid;   // a forked child has none of the parent's copy threads: it starts its own
 
 static bool on() {
+    if (state > 0 && pool_pid != getpid()) {
+        pool = new Pool;
+        pool_pid = getpid();
+        for (int t = 1; t < NTHREADS; t++) std::thread([] { pool->worker(); }).detach();
+    }
     if (state == 0) {
         const char *e = getenv("GEN9BLAS_STAGE");
         state = e && !strcmp(e, "0") ? -1 : 1;
@@ -223,6 +230,7 @@ static bool on() {
         }
         if (state > 0) {
             pool = new Pool;
+            pool_pid = getpid();
             for (int t = 1; t < NTHREADS; t++) std::thread([] { pool->worker(); }).detach();
         }
     }
