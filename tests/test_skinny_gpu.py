@@ -92,10 +92,11 @@ def test_skinny_oracle_parity_small(g9, orc):
         assert (d <= 2 * ulp).all(), f"M={M}: GPU and oracle differ by more than 2 FP16 ulp"
 
 
-@pytest.mark.parametrize("M,N,K", [(5, 100, 256), (8, 4099, 512), (12, 333, 768), (16, 64, 4096), (16, 3000, 2560)])
+@pytest.mark.parametrize("M,N,K", [(3, 77, 512), (4, 2050, 1024), (5, 100, 256), (8, 4099, 512), (12, 333, 768),
+                                   (16, 64, 4096), (16, 3000, 2560)])
 def test_skinny_matrix_core_kernel(g9, torch_dev, M, N, K):
-    """FP16 shapes that take the matrix-core skinny kernel (4 < M ≤ 16, K a multiple of 256, aligned rows): fewer
-    K groups than waves, N not a multiple of 16, both M tiles, host and device memory. Small-integer inputs give exact
+    """FP16 shapes that take the matrix-core skinny kernel (2 < M ≤ 16, K a multiple of 256, aligned rows): fewer
+    K groups than waves, N not a multiple of 16, all three M tiles (4, 8, 16), host and device memory. Small-integer inputs give exact
     products and sums, so every result must be bit-exact; then alpha/beta on a C slice, and the role swap (small N)
     that stores through swapped strides."""
     rng = np.random.default_rng(31)
