@@ -200,8 +200,8 @@ constexpr int SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100, SG_DS_W
 //   1: op(A) lower, k < m0 + BM; 2: op(A) upper, k ≥ m0; 3: op(B) lower, k ≥ n0; 4: op(B) upper, k < n0 + BN.
 //   Tiles are dispatched longest range first, spread over the XCDs.
 template <class T, int BM, int BN, int WM, int WN, bool AK, bool BKC, bool VEC, bool SCHED = true, bool SPLIT = false,
-          int TRI = 0, int KLIM = 0>
-__global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename Mma<T>::Sum> p) {
+          int TRI = 0, int KLIM = 0, int KG = 1>
+__global__ void __launch_bounds__(WM *WN * 64 * KG) gemm_kernel(GemmParams<typename Mma<T>::Sum> p) {
     using MM = Mma<T>;
     using S = typename MM::Sum;
     constexpr int NT = WM * WN * 64;
@@ -214,9 +214,13 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
     static_assert(TM * MI == WTM && TN * MI == WTN, "wave tile must be a multiple of the MFMA tile");
     static_assert(TRI == 0 || (BM == BN && !SPLIT), "triangle mode: square tiles, no split");
     static_assert(KLIM == 0 || (!SPLIT && TRI == 0), "k-limited tiles: one product, no split");
-    __shared__ __attribute__((aligned(16))) unsigned char lds[2][(BM + BN) * ROWB];
+    static_assert(KG == 1 || (!SPLIT && TRI == 0 && KLIM == 0), "k groups: plain tiles only");
+    __shared__ __attribute__((aligned(16))) unsigned char lds[2 * KG][(BM + BN) * ROWB];
 
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    // KG > 1: the workgroup holds KG groups of WM × WN waves; group kh takes the block tiles kh, kh + KG, ... of the
+    // k range into LDS buffers of its own, and the groups' sums are added in group order at the end
+    const int kh = KG > 1 ? (int)threadIdx.x / NT : 0;
+    const int tid = KG > 1 ? (int)threadIdx.x % NT : (int)threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int wm = wid % WM, wn = wid / WM;
     const int g = lane / MI, lr = lane % MI;
 
@@ -296,8 +300,8 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
     // MFMAs of one block tile held in LDS buffer `cur`. Fragments live in two register sets: group q+1 is read from
     // LDS while the MFMAs of group q run.
     auto compute = [&](int cur) {
-        const unsigned char *As = lds[cur] + (wm * WTM + lr) * ROWB + g * KRB;
-        const unsigned char *Bs = lds[cur] + BM * ROWB + (wn * WTN + lr) * ROWB + g * KRB;
+        const unsigned char *As = lds[cur * KG + kh] + (wm * WTM + lr) * ROWB + g * KRB;
+        const unsigned char *Bs = lds[cur * KG + kh] + BM * ROWB + (wn * WTN + lr) * ROWB + g * KRB;
         typename MM::Acc part[MM::BLOCKED ? TI : 1][MM::BLOCKED ? TJ : 1];
         if constexpr (MM::BLOCKED) {
 #pragma unroll
@@ -337,24 +341,27 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
         }
     };
 
-    const int nk = (K + BK - 1) / BK;
+    // block tiles per k group (a group's tiles past K load as zeros)
+    const int nk = ((K + BK - 1) / BK + KG - 1) / KG;
+    const int kofs = kh * BK;
+    auto buf = [&](int b) { return lds[b * KG + kh]; };
     // Interior tiles with whole k-steps load without bounds tests: the steady-state loop is then one basic block,
     // whose instruction order is pinned below so the LDS reads, global loads and LDS writes of a k-step run between
     // its MFMAs.
-    const bool fast = VEC && m0 + BM <= p.M && n0 + BN <= p.N && K % BK == 0;
+    const bool fast = VEC && m0 + BM <= p.M && n0 + BN <= p.N && K % (BK * KG) == 0;
     if (fast) {
-        sa.template load<false>(A, p.lda, p.M, K, m0, 0, tid);
-        sb.template load<false>(B, p.ldb, p.N, K, n0, 0, tid);
-        sa.store(lds[0], tid);
-        sb.store(lds[0] + BM * ROWB, tid);
+        sa.template load<false>(A, p.lda, p.M, K, m0, kofs, tid);
+        sb.template load<false>(B, p.ldb, p.N, K, n0, kofs, tid);
+        sa.store(buf(0), tid);
+        sb.store(buf(0) + BM * ROWB, tid);
         __syncthreads();
         for (int kt = 0; kt + 1 < nk; kt++) {
             const int cur = kt & 1;
-            sa.template load<false>(A, p.lda, p.M, K, m0, (kt + 1) * BK, tid);
-            sb.template load<false>(B, p.ldb, p.N, K, n0, (kt + 1) * BK, tid);
+            sa.template load<false>(A, p.lda, p.M, K, m0, (kt + 1) * KG * BK + kofs, tid);
+            sb.template load<false>(B, p.ldb, p.N, K, n0, (kt + 1) * KG * BK + kofs, tid);
             compute(cur);
-            sa.store(lds[cur ^ 1], tid);
-            sb.store(lds[cur ^ 1] + BM * ROWB, tid);
+            sa.store(buf(cur ^ 1), tid);
+            sb.store(buf(cur ^ 1) + BM * ROWB, tid);
             if constexpr (SCHED) {
                 constexpr int NRD = TM + TN;                         // LDS fragment reads per group
                 constexpr int NMF = SPG * TI * TJ;                   // MFMAs per group
@@ -385,20 +392,49 @@ __global__ void __launch_bounds__(WM *WN * 64) gemm_kernel(GemmParams<typename M
             sa.template load<true>(A, p.lda, p.M, K, m0, k0, tid);
             sb.template load<true>(B, p.ldb, p.N, K, n0, k0, tid);
         };
-        load_tile(0);
-        sa.store(lds[0], tid);
-        sb.store(lds[0] + BM * ROWB, tid);
+        load_tile(kofs);
+        sa.store(buf(0), tid);
+        sb.store(buf(0) + BM * ROWB, tid);
         __syncthreads();
         for (int kt = 0; kt < nk; kt++) {
             const int cur = kt & 1;
-            if (kt + 1 < nk) load_tile((kt + 1) * BK);
+            if (kt + 1 < nk) load_tile((kt + 1) * KG * BK + kofs);
             compute(cur);
             if (kt + 1 < nk) {
-                sa.store(lds[cur ^ 1], tid);
-                sb.store(lds[cur ^ 1] + BM * ROWB, tid);
+                sa.store(buf(cur ^ 1), tid);
+                sb.store(buf(cur ^ 1) + BM * ROWB, tid);
             }
             __syncthreads();
         }
+    }
+
+    if constexpr (KG > 1) {
+        // groups 1 .. KG-1 leave their sums in LDS (value-major, so a wave's 64 lanes write 256 consecutive bytes);
+        // group 0 adds them in group order and stores C
+        constexpr int NV = TI * TJ * MM::NACC;
+        static_assert((KG - 1) * NV * NT * sizeof(S) <= sizeof(lds), "k-group sums must fit in LDS");
+        S *red = reinterpret_cast<S *>(&lds[0][0]);
+        __syncthreads();   // the last block tile of every group has been read
+        if (kh > 0) {
+#pragma unroll
+            for (int i = 0; i < TI; i++)
+#pragma unroll
+                for (int j = 0; j < TJ; j++)
+#pragma unroll
+                    for (int r = 0; r < MM::NACC; r++)
+                        red[((kh - 1) * NV + (i * TJ + j) * MM::NACC + r) * NT + tid] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (kh > 0) return;
+#pragma unroll
+        for (int h = 1; h < KG; h++)
+#pragma unroll
+            for (int i = 0; i < TI; i++)
+#pragma unroll
+                for (int j = 0; j < TJ; j++)
+#pragma unroll
+                    for (int r = 0; r < MM::NACC; r++)
+                        acc[i][j][r] += red[((h - 1) * NV + (i * TJ + j) * MM::NACC + r) * NT + tid];
     }
 
     if constexpr (MM::SWAP) {

@@ -20,7 +20,7 @@ namespace g9 {
 //   being four rounds of 512 workgroups and a nearly empty fifth). Transposed A: TN 128×128 125 (256×128: 117),
 //   TT 128×64 120 (256×128: 117).
 //   Small at n = 1024 (NN): FP32 64×64 (256 tiles, no split) 69 TFLOP/s against 62 for 128×128 split four ways;
-//   FP64 64×128 split two ways 43, 64×64 41.
+//   FP64 64×128 split two ways 43, 64×64 41. Both are beaten by 64×64 tiles with two k groups (launch_layout).
 struct TileCfg { int BM, BN, WM, WN; };
 // Layouts whose staging needs more registers than a wave has at 2 waves per SIMD (transposed A, unaligned
 // operands) keep FP16 at 4 waves (512 registers per wave), which compiles without spills.
@@ -42,16 +42,23 @@ template <bool AK, bool BKC, bool VEC> struct Cfg<double, AK, BKC, VEC> {
     static constexpr int small_div = 2;
 };
 
-// Split-K slices for a single product of `tiles` tiles: doubled while the slices still leave at most one workgroup
-// per CU and each slice keeps at least 4 k-steps, up to 8. GEN9BLAS_SPLITK=n forces n slices (0 or 1: none).
-// Splitting changes only the FP32 (FP64) summation order: each slice sums its k-range, the slices are then added in
-// order, and alpha/beta and the rounding to the element type are applied once.
-static int splitk_slices(long long tiles, int K, int BK, int count) {
+// GEN9BLAS_SPLITK=n forces n split-K slices (0 or 1: none) and turns the two-k-group tiles off, so that the
+// summation order no longer depends on the shape; -1 when unset.
+static int splitk_forced() {
     static int forced = -2;
     if (forced == -2) {
         const char *e = getenv("GEN9BLAS_SPLITK");
-        forced = e ? atoi(e) : -1;
+        forced = e ? std::max(atoi(e), 0) : -1;
     }
+    return forced;
+}
+
+// Split-K slices for a single product of `tiles` tiles: doubled while the slices still leave at most one workgroup
+// per CU and each slice keeps at least 4 k-steps, up to 8.
+// Splitting changes only the FP32 (FP64) summation order: each slice sums its k-range, the slices are then added in
+// order, and alpha/beta and the rounding to the element type are applied once.
+static int splitk_slices(long long tiles, int K, int BK, int count) {
+    const int forced = splitk_forced();
     if (count != 1) return 1;
     if (forced >= 0) return forced < 1 ? 1 : forced > 64 ? 64 : forced;
     int s = 1;
@@ -59,7 +66,7 @@ static int splitk_slices(long long tiles, int K, int BK, int count) {
     return s;
 }
 
-template <class T, TileCfg C, bool AK, bool BKC, bool VEC>
+template <class T, TileCfg C, bool AK, bool BKC, bool VEC, int KG = 1>
 static int launch_t(GemmParams<typename Mma<T>::Sum> p, int count) {
     using S = typename Mma<T>::Sum;
     constexpr int BK = 128 / (int)sizeof(T);
@@ -68,8 +75,8 @@ static int launch_t(GemmParams<typename Mma<T>::Sum> p, int count) {
     if ((long long)p.tiles_m * p.tiles_n > 0x7fffffffLL || count > 65535)
         G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "gemm grid too large (%d × %d tiles, batch %d)", p.tiles_m, p.tiles_n, count);
     const long long tiles = (long long)p.tiles_m * p.tiles_n;
-    const int split = splitk_slices(tiles, p.K, BK, count);
-    const dim3 block(C.WM * C.WN * 64);
+    const int split = KG > 1 ? 1 : splitk_slices(tiles, p.K, BK, count);
+    const dim3 block(C.WM * C.WN * 64 * KG);
     if (split > 1) {
         p.kper = ((p.K + split - 1) / split + BK - 1) / BK * BK;
         const int ns = (p.K + p.kper - 1) / p.kper;
@@ -91,7 +98,7 @@ static int launch_t(GemmParams<typename Mma<T>::Sum> p, int count) {
         return 0;
     }
     const dim3 grid((unsigned)tiles, (unsigned)count);
-    hipLaunchKernelGGL((gemm_kernel<T, C.BM, C.BN, C.WM, C.WN, AK, BKC, VEC, true>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((gemm_kernel<T, C.BM, C.BN, C.WM, C.WN, AK, BKC, VEC, true, false, 0, 0, KG>), grid, block, 0, stream, p);
     G9_HIP(hipGetLastError());
     return 0;
 }
@@ -100,7 +107,19 @@ template <class T, bool AK, bool BKC, bool VEC>
 static int launch_layout(const GemmParams<typename Mma<T>::Sum> &p, int count) {
     using CF = Cfg<T, AK, BKC, VEC>;
     const long long big_tiles = (long long)((p.M + CF::big.BM - 1) / CF::big.BM) * ((p.N + CF::big.BN - 1) / CF::big.BN) * count;
-    if (big_tiles * CF::small_div < num_cus) return launch_t<T, CF::small, AK, BKC, VEC>(p, count);
+    if (big_tiles * CF::small_div < num_cus) {
+        // 64×64 tiles with two k groups of 4 waves (8 waves per workgroup, the groups' sums added through LDS), when
+        // they give more than num_cus / 2 tiles: two waves per SIMD hide each other's barrier and load waits without a
+        // split-K pass. Measured (TFLOP/s, against the small tiles with split-K): FP32 NN n = 1024 71 → 82, TN 68 → 77,
+        // n = 1000 38 → 56, 1024² × K 4096 81 → 98; FP64 n = 1024 44 → 52, n = 1536 38 → 48. FP32 above num_cus tiles
+        // loses (n = 1280: 74 → 70), FP64 does not.
+        if constexpr (sizeof(T) >= 4) {
+            const long long t64 = (long long)((p.M + 63) / 64) * ((p.N + 63) / 64) * count;
+            if (splitk_forced() < 0 && t64 * 2 > num_cus && (sizeof(T) == 8 || t64 <= num_cus))
+                return launch_t<T, TileCfg{64, 64, 2, 2}, AK, BKC, VEC, 2>(p, count);
+        }
+        return launch_t<T, CF::small, AK, BKC, VEC>(p, count);
+    }
     return launch_t<T, CF::big, AK, BKC, VEC>(p, count);
 }
 

@@ -28,7 +28,10 @@ def case_bounds(kind, K):
         return (4.9e-4, 5e-3) if K < 256 else (1e-4, 1e-3)
     return MEAN_E[kind], MAX_E[kind]
 SIZES = [(1, 1, 1, 1.0, 0.0), (17, 33, 15, 1.0, 0.0), (100, 70, 300, 2.0, 0.0), (64, 96, 48, 0.5, 1.0),
-         (333, 129, 1000, 1.0, -1.0), (1000, 1024, 777, 1.0, 0.5)]
+         (333, 129, 1000, 1.0, -1.0), (1000, 1024, 777, 1.0, 0.5),
+         # FP32/FP64 two-k-group tiles: the second group's only block tile lies past K (K = 20), and one whole block
+         # tile per group (K = 64)
+         (1024, 960, 20, 1.0, 0.0), (960, 1024, 64, -1.0, 0.25)]
 
 
 def _to_dev(torch, x):
@@ -265,8 +268,8 @@ def test_hgemm_whole_tile_kernel(g9, torch_dev, M, N, K, count):
 
 def test_banded_launch(tmp_path):
     """GEN9BLAS_MAX_LAUNCH_MS splits a long product into row bands, each its own launch (reference:
-    lib/src/gemm.c:119-164): results equal the unbanded call's (with split-K off: it picks its slices from the shape,
-    so a band may sum in another order). The variable is read once per process, so the banded call runs in a child
+    lib/src/gemm.c:119-164): results equal the unbanded call's (with GEN9BLAS_SPLITK=0: split-K slices and the
+    two-k-group tiles are picked from the shape, so a band may sum in another order). The variable is read once per process, so the banded call runs in a child
     process (one extra GPU process, sequential)."""
     import os
     import subprocess
