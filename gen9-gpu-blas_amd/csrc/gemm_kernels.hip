@@ -109,13 +109,14 @@ static int launch_layout(const GemmParams<typename Mma<T>::Sum> &p, int count) {
     const long long big_tiles = (long long)((p.M + CF::big.BM - 1) / CF::big.BM) * ((p.N + CF::big.BN - 1) / CF::big.BN) * count;
     if (big_tiles * CF::small_div < num_cus) {
         // 64×64 tiles with two k groups of 4 waves (8 waves per workgroup, the groups' sums added through LDS), when
-        // they give more than num_cus / 2 tiles: two waves per SIMD hide each other's barrier and load waits without a
+        // they give at least num_cus / 2 tiles: two waves per SIMD hide each other's barrier and load waits without a
         // split-K pass. Measured (TFLOP/s, against the small tiles with split-K): FP32 NN n = 1024 71 → 82, TN 68 → 77,
-        // n = 1000 38 → 56, 1024² × K 4096 81 → 98; FP64 n = 1024 44 → 52, n = 1536 38 → 48. FP32 above num_cus tiles
-        // loses (n = 1280: 74 → 70), FP64 does not.
+        // n = 1000 38 → 56, 1024² × K 4096 81 → 98; FP64 n = 1024 44 → 52, n = 1536 38 → 48, 128×4096×128 (the
+        // triangular solve's block products) 8.6 → 15.8. FP32 above num_cus tiles loses (n = 1280: 74 → 70), FP64
+        // does not.
         if constexpr (sizeof(T) >= 4) {
             const long long t64 = (long long)((p.M + 63) / 64) * ((p.N + 63) / 64) * count;
-            if (splitk_forced() < 0 && t64 * 2 > num_cus && (sizeof(T) == 8 || t64 <= num_cus))
+            if (splitk_forced() < 0 && t64 * 2 >= num_cus && (sizeof(T) == 8 || t64 <= num_cus))
                 return launch_t<T, TileCfg{64, 64, 2, 2}, AK, BKC, VEC, 2>(p, count);
         }
         return launch_t<T, CF::small, AK, BKC, VEC>(p, count);
