@@ -126,14 +126,16 @@ __global__ void __launch_bounds__(256) trsm_store_kernel(const T *Y, T *B, ll ld
 
 constexpr int TRSM_NB = 128;
 // Inverse of the diagonal block bi of L (rows and columns r0 .. r0+b-1, b ≤ TRSM_NB), in FP64, stored in the element
-// type as a b×b lower matrix at Inv + bi·NB². The block is split into 32×32 sub-blocks: the four diagonal sub-blocks
+// type into the inverted diagonal block of lb rows (lb = TRSM_NB or 2·TRSM_NB) that holds it: leaf p = r0 / lb at
+// Inv + p·lb², row stride lb, at row and column offset o = r0 − p·lb. The first 128-block of a leaf also writes zeros
+// right of itself (columns b .. lb−1 of its rows), the leaf's upper-right quadrant. The block is split into 32×32 sub-blocks: the four diagonal sub-blocks
 // are inverted first, thread j forming column j of its sub-block by substitution (X[j][j] = 1 / L[j][j],
 // X[i][j] = −(Σ_{k=j}^{i-1} L[i][k]·X[k][j]) / L[i][i], 8 loads of L in flight per step); the off-diagonal sub-blocks
 // then follow by distance d from the diagonal, X_ij = −inv(L_ii)·Σ_{k=j}^{i-1} L_ik·X_kj (i − j = d), one element per
 // thread at a time. The work per thread is balanced (a single column chain of the whole block would be 8128 FMAs
 // long); the sums differ from plain column substitution in FP64 rounding only. X and the sums live in LDS (154 KiB).
 template <class T>
-__global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, int n, T *Inv) {
+__global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, int n, T *Inv, int lb) {
     constexpr int S = 32, NSB = TRSM_NB / S;
     __shared__ double X[TRSM_NB][TRSM_NB + 1];
     __shared__ double Sb[NSB - 1][S][S + 1];
@@ -189,45 +191,54 @@ __global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, int n, T *Inv
         }
         __syncthreads();
     }
-    T *out = Inv + (ll)bi * TRSM_NB * TRSM_NB;
-    for (int e = t; e < b * b; e += 256) out[e] = (T)X[e / b][e % b];
+    const int p = r0 / lb, o = r0 - p * lb, w = o == 0 ? lb : b;
+    T *out = Inv + (ll)p * lb * lb + (ll)o * lb + o;
+    for (int e = t; e < b * w; e += 256) {
+        const int i = e / w, j = e % w;
+        out[(ll)i * lb + j] = j < b ? (T)X[i][j] : T(0);
+    }
 }
 
-// One GEMM on device operands (no staging, no wait): C = alpha·op(A)·op(B) + beta·C.
-static int dgemm_dev(int type, int tA, int tB, int M, int N, int K, double alpha, const void *A, ll lda, const void *B,
-                     ll ldb, double beta, void *C, ll ldc) {
-    if (M <= 0 || N <= 0 || K <= 0) return 0;
+// count GEMMs on device operands (no staging, no wait): C_z = alpha·op(A_z)·op(B_z) + beta·C_z, X_z = X + z·sX.
+static int dgemm_dev_batched(int type, int tA, int tB, int M, int N, int K, double alpha, const void *A, ll lda, ll sA,
+                             const void *B, ll ldb, ll sB, double beta, void *C, ll ldc, ll sC, int count) {
+    if (M <= 0 || N <= 0 || K <= 0 || count <= 0) return 0;
     GemmCall g;
     g.type = type;
     g.tA = tA; g.tB = tB;
     g.M = M; g.N = N; g.K = K;
-    g.count = 1;
+    g.count = count;
     g.alpha = alpha; g.beta = beta;
-    g.A = A; g.lda = lda; g.sA = 0;
-    g.B = B; g.ldb = ldb; g.sB = 0;
-    g.C = C; g.ldc = ldc; g.sC = 0;
+    g.A = A; g.lda = lda; g.sA = sA;
+    g.B = B; g.ldb = ldb; g.sB = sB;
+    g.C = C; g.ldc = ldc; g.sC = sC;
     return launch_gemm(g);
 }
+static int dgemm_dev(int type, int tA, int tB, int M, int N, int K, double alpha, const void *A, ll lda, const void *B,
+                     ll ldb, double beta, void *C, ll ldc) {
+    return dgemm_dev_batched(type, tA, tB, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1);
+}
 
-// Blocked forward substitution L·X = Y (L n×n lower, Y and X n×m, row strides n and m) over 128-row diagonal blocks,
-// by recursive halving: the first half of a block range is solved, one GEMM then subtracts its contribution from the
-// right-hand side of the second half, Y[i1..i2) -= L[i1..i2, i0..i1)·X[i0..i1), and the second half is solved. A
-// single block is X_i = inv(L_ii)·Y_i with the block's FP64-computed inverse. The reference updates one block row at
-// a time, Y_i -= L[i, <i]·X[<i] (level3.c:127-215): the same products, grouped so that most of the flops run in a few
-// large GEMMs instead of n/128 products of 128 rows; the sums differ only in rounding (each GEMM rounds once).
+// Blocked forward substitution L·X = Y (L n×n lower, Y and X n×m, row strides n and m) over diagonal blocks of lb
+// rows (256 for FP32 / FP64, 128 for FP16), by recursive halving: the first half of a block range is solved, one GEMM
+// then subtracts its contribution from the right-hand side of the second half, Y[i1..i2) -= L[i1..i2, i0..i1)·X[i0..i1),
+// and the second half is solved. A single block is X_i = inv(L_ii)·Y_i with the block's inverse (128-row inverses
+// computed in FP64; a 256-row inverse composed from two of them). The reference updates one block row at a time,
+// Y_i -= L[i, <i]·X[<i] (level3.c:127-215): the same products, grouped so that most of the flops run in a few large
+// GEMMs instead of n/128 products of 128 rows; the sums differ only in rounding (each GEMM rounds once).
 struct TrsmSolve {
-    int type, n, m, es;
+    int type, n, m, es, lb;   // lb: rows of an inverted diagonal block (leaf)
     const char *L, *Iv;
     char *Y, *X;
-    int solve(int b0, int nb) const {   // blocks [b0, b0 + nb)
+    int solve(int b0, int nb) const {   // leaves [b0, b0 + nb)
         if (nb == 1) {
-            const int i0 = b0 * TRSM_NB, b = n - i0 < TRSM_NB ? n - i0 : TRSM_NB;
-            return dgemm_dev(type, 0, 0, b, m, b, 1.0, Iv + (ll)b0 * TRSM_NB * TRSM_NB * es, b, Y + (ll)i0 * m * es, m, 0.0,
+            const int i0 = b0 * lb, b = n - i0 < lb ? n - i0 : lb;
+            return dgemm_dev(type, 0, 0, b, m, b, 1.0, Iv + (ll)b0 * lb * lb * es, lb, Y + (ll)i0 * m * es, m, 0.0,
                              X + (ll)i0 * m * es, m);
         }
         const int h = nb / 2;
         G9_TRY(solve(b0, h));
-        const int i0 = b0 * TRSM_NB, i1 = (b0 + h) * TRSM_NB, i2 = n < (b0 + nb) * TRSM_NB ? n : (b0 + nb) * TRSM_NB;
+        const int i0 = b0 * lb, i1 = (b0 + h) * lb, i2 = n < (b0 + nb) * lb ? n : (b0 + nb) * lb;
         G9_TRY(dgemm_dev(type, 0, 0, i2 - i1, m, i1 - i0, -1.0, L + ((ll)i1 * n + i0) * es, n, X + (ll)i0 * m * es, m, 1.0,
                          Y + (ll)i1 * m * es, m));
         return solve(b0 + h, nb - h);
@@ -417,11 +428,15 @@ int gen9blas_trsm(int type, int side, int uplo, int transA, int diag, int M, int
     // L·Y = alpha·R: op'(A) = left ? op(A) : op(A)ᵀ; lower when the triangle of A, transposed or not, is lower
     const int tr = left ? transA != 0 : transA == 0;
     const int lower = (uplo == GEN9BLAS_LOWER) != (tr != 0), rev = !lower;
-    const int nbl = (n + TRSM_NB - 1) / TRSM_NB;
+    // Leaves of 256 rows for FP32 / FP64: each leaf inverse is composed from two 128-row FP64 inverses (below); FP16
+    // keeps 128-row leaves (the composition would round once more in FP16)
+    const int nbl = (n + TRSM_NB - 1) / TRSM_NB, lb = es >= 4 ? 2 * TRSM_NB : TRSM_NB, nleaf = (n + lb - 1) / lb;
     void *Ld, *Yd, *Iv, *Zd;
     G9_TRY(scratch(SLOT_T, (size_t)n * n * es, &Ld));
     G9_TRY(scratch(SLOT_X, (size_t)n * m * es, &Yd));
-    G9_TRY(scratch(SLOT_Y, (size_t)nbl * TRSM_NB * TRSM_NB * es, &Iv));
+    // the leaf inverses, then (lb > TRSM_NB) the products C·I1 of the composition, TRSM_NB² per leaf
+    const size_t inv_bytes = (size_t)nleaf * lb * lb * es;
+    G9_TRY(scratch(SLOT_Y, inv_bytes + (lb > TRSM_NB ? (size_t)nleaf * TRSM_NB * TRSM_NB * es : 0), &Iv));
     G9_TRY(scratch(SLOT_W, (size_t)n * m * es, &Zd));
     G9_TRY(by_es(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
@@ -430,12 +445,33 @@ int gen9blas_trsm(int type, int side, int uplo, int transA, int diag, int M, int
                            ops[0].ld, (T *)Ld, n, uplo == GEN9BLAS_LOWER, tr, diag != 0, rev);
         hipLaunchKernelGGL((trsm_y_kernel<T>), dim3(grid_for((ll)n * m)), dim3(256), 0, stream, (const T *)ops[1].dev,
                            ops[1].ld, (T *)Yd, n, m, left, rev, (S)alpha);
-        hipLaunchKernelGGL((trsm_inv_kernel<T>), dim3(nbl), dim3(256), 0, stream, (const T *)Ld, n, (T *)Iv);
+        hipLaunchKernelGGL((trsm_inv_kernel<T>), dim3(nbl), dim3(256), 0, stream, (const T *)Ld, n, (T *)Iv, lb);
         G9_HIP(hipGetLastError());
         return 0;
     }));
-    TrsmSolve rec{type, n, m, es, (const char *)Ld, (const char *)Iv, (char *)Yd, (char *)Zd};
-    G9_TRY(rec.solve(0, nbl));
+    if (lb > TRSM_NB) {
+        // A leaf [I1 0; C I2]⁻¹ = [inv(I1) 0; −inv(I2)·C·inv(I1) inv(I2)]: the kernel above left inv(I1), inv(I2) and
+        // the zero quadrant; two GEMMs form the lower-left quadrant, batched over the leaves with two whole halves
+        // (leaf p: C at L + p·lb·(n+1) + TRSM_NB·n, inv(I1) at Inv_p, inv(I2) at Inv_p + TRSM_NB·(lb+1)), then once
+        // for a last leaf whose second half has b2 < TRSM_NB rows.
+        const ll NB = TRSM_NB;
+        const char *L0 = (const char *)Ld;
+        char *I0 = (char *)Iv, *Tm = I0 + inv_bytes;
+        const int full = n / lb;
+        G9_TRY(dgemm_dev_batched(type, 0, 0, TRSM_NB, TRSM_NB, TRSM_NB, 1.0, L0 + NB * n * es, n, (ll)lb * (n + 1), I0, lb,
+                                 (ll)lb * lb, 0.0, Tm, NB, NB * NB, full));
+        G9_TRY(dgemm_dev_batched(type, 0, 0, TRSM_NB, TRSM_NB, TRSM_NB, -1.0, I0 + NB * (lb + 1) * es, lb, (ll)lb * lb, Tm,
+                                 NB, NB * NB, 0.0, I0 + NB * lb * es, lb, (ll)lb * lb, full));
+        const ll i0 = (ll)full * lb;
+        const int b2 = n - (int)i0 - TRSM_NB;
+        if (b2 > 0) {
+            char *Ip = I0 + i0 * lb * es;
+            G9_TRY(dgemm_dev(type, 0, 0, b2, TRSM_NB, TRSM_NB, 1.0, L0 + ((i0 + NB) * n + i0) * es, n, Ip, lb, 0.0, Tm, NB));
+            G9_TRY(dgemm_dev(type, 0, 0, b2, TRSM_NB, b2, -1.0, Ip + NB * (lb + 1) * es, lb, Tm, NB, 0.0, Ip + NB * lb * es, lb));
+        }
+    }
+    TrsmSolve rec{type, n, m, es, lb, (const char *)Ld, (const char *)Iv, (char *)Yd, (char *)Zd};
+    G9_TRY(rec.solve(0, nleaf));
     G9_TRY(by_es(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
         hipLaunchKernelGGL((trsm_store_kernel<T>), dim3(grid_for((ll)n * m)), dim3(256), 0, stream, (const T *)Zd,

@@ -103,7 +103,8 @@ def test_trsm(g9, kind, dt, acc, tol):
         for uplo in "LU":
             for ta in (False, True):
                 for dg in (False, True):
-                    for (M, N) in [(40, 30), (300, 200), (70, 600)]:
+                    for (M, N) in [(40, 30), (300, 200), (70, 600), (400, 400)]:   # n = 400: a last 256-row
+                        # leaf whose second half has 16 rows
                         n = M if side == "L" else N
                         A = rng.uniform(-1, 1, (n, n)).astype(np.float32)
                         A[np.diag_indices(n)] = n if not dg else 0.5
