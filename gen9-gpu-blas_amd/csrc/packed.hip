@@ -171,8 +171,11 @@ __global__ void __launch_bounds__(SKS * 64) skinny_pb_lds_kernel(int M, int N, i
     }
     const char *wb = reinterpret_cast<const char *>(W + (long long)n0 * ldw);
     const char *ab = reinterpret_cast<const char *>(A);
-    auto issue = [&](int j, int st) {   // group wv + SKS·j into stage st
-        const int gg = wv + SKS * j;
+    // every workgroup reads the same rows of A: each wave starts its walk over its k groups at an offset given by the
+    // workgroup's place on its XCD (dispatch slot / 8), so an XCD's workgroups read different columns of A at once
+    const int rot = ng > 1 ? (int)((blockIdx.x >> 3) % (unsigned)ng) : 0;
+    auto issue = [&](int j, int st) {   // group wv + SKS·((j + rot) mod ng) into stage st
+        const int gg = wv + SKS * (j + rot < ng ? j + rot : j + rot - ng);
         const unsigned dst = lbase + st * SB;
 #pragma unroll
         for (int c = 0; c < NWC; c++) lds_dma16(wb + (long long)gg * WROW, woff[c], dst + c * 1024);

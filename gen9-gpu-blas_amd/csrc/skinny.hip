@@ -48,9 +48,9 @@ int launch_skinny(const SkinnyCall &c) {
         G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "skinny grid too large (M %d, N %d)", c.M, c.N);
     if (c.type == GEN9BLAS_S) return launch_typed<float>(p, vec);
     // FP16, M > 2: the matrix-core kernel when K is a multiple of its 256-k groups and the rows are 16-byte aligned
-    // (MI355X, W 4096×4096 rotated over 32 copies, µs per call: M = 4 8.2 against 8.7-9.1 for the dot kernel; M = 8
-    // 8.6, M = 16 9.2 against 11.1 and 16.0 for the dot kernel; 2 waves with 4 stages (M = 16: 3) against 9.2 and
-    // 9.6 for 4 waves with 2 stages and 2 waves with 4; M ≤ 2 stays on the dot kernel: 7.2-7.7 against 8.1)
+    // (MI355X, W 4096×4096 rotated over 32 copies, µs per call: M = 4 7.6 against 8.7-9.1 for the dot kernel; M = 8
+    // 7.8-8.0, M = 16 8.3-8.5 against 11.1 and 16.0 for the dot kernel; 2 waves with 4 stages (M = 16: 3) against
+    // 1 or 4 waves and 2-6 stages; M ≤ 2 stays on the dot kernel: 7.1-7.7 against 7.6-7.7)
     if (p.M > 2 && vec && p.K % 256 == 0 && (c.swn + c.sam) * 2 * 16 < (1LL << 32)) {   // 32-bit lane offsets
         if (p.M <= 4) return launch_mfma<4, 2, 4>(p);
         if (p.M <= 8) return launch_mfma<8, 2, 4>(p);

@@ -199,8 +199,13 @@ __global__ void __launch_bounds__(KS * 64) skinny_mfma_kernel(Params p) {
     }
     const char *wb = reinterpret_cast<const char *>(reinterpret_cast<const f16 *>(p.w) + (long long)n0 * p.swn);
     const char *ab = reinterpret_cast<const char *>(reinterpret_cast<const f16 *>(p.a) + (long long)m0 * p.sam);
-    auto issue = [&](int j, int st) {   // group wv + KS·j into stage st
-        const long long kofs = (long long)(wv + KS * j) * ROWB;
+    // Every workgroup reads the same rows of a. Walking the k groups in the same order everywhere would have all of an
+    // XCD's workgroups on the same 512-byte columns of a at once, a few L2 channels serving them all; each wave
+    // therefore starts its walk at an offset given by the workgroup's place on its XCD (dispatch slot / 8).
+    const int rot = ng > 1 ? (int)((blockIdx.x >> 3) % (unsigned)ng) : 0;
+    auto issue = [&](int j, int st) {   // group wv + KS·((j + rot) mod ng) into stage st
+        const int jj = j + rot < ng ? j + rot : j + rot - ng;
+        const long long kofs = (long long)(wv + KS * jj) * ROWB;
         const unsigned dst = lbase + st * SB;
 #pragma unroll
         for (int i = 0; i < 8; i++) lds_dma16(wb + kofs, woff[i], dst + i * 1024);
