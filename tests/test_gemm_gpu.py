@@ -116,6 +116,25 @@ def test_gemm_config_sizes(g9, orc, torch_dev, kind, n):
     assert np.isfinite(W).all()
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_sgemm_two_group_tiles(g9, orc, torch_dev, ta, tb):
+    """FP32 products whose 128×128 tiles fill whole rounds of CUs take 128×128 tiles with two k groups: 2000×2048
+    (256 tiles, edge tiles in m) with K = 1000 (not a multiple of the groups' 64-k step, so the second group's last
+    block tile is partly past K), alpha = 1.5, beta = 0.5, every layout, against float64 on sampled rows."""
+    torch = torch_dev
+    M, N, K = 2000, 2048, 1000
+    a = orc.uniform((K, M) if ta else (M, K), np.float32, orc.SEED_A)
+    b = orc.uniform((N, K) if tb else (K, N), np.float32, orc.SEED_B)
+    c0 = orc.uniform((M, N), np.float32, 3)
+    Ad, Bd, Cd = _to_dev(torch, a), _to_dev(torch, b), _to_dev(torch, c0)
+    W = g9.gemm(Ad.t() if ta else Ad, Bd.t() if tb else Bd, 1.5, 0.5, Cd).cpu().numpy()
+    opA = a.T if ta else a
+    rows = np.unique(np.r_[0, M - 1, np.random.default_rng(6).integers(0, M, 62)])
+    mean, mx = _sampled_rows_error(W, opA, b, rows, 1.5, 0.5, c0, tB=bool(tb))
+    assert mx <= MAX_E["S"], f"tA={ta} tB={tb}: max e {mx:.2e}"
+    assert mean <= MEAN_E["S"], f"tA={ta} tB={tb}: mean e {mean:.2e}"
+
+
 def test_sgemm_odd_shape(g9, orc, torch_dev):
     """BASELINE odd shape: M = 3000, N = 11008, K = 4096, transB (B stored N×K), beta = 0.5, C pre-filled U[-1, 1]."""
     torch = torch_dev
