@@ -121,6 +121,13 @@ static int launch_layout(const GemmParams<typename Mma<T>::Sum> &p, int count) {
         }
         return launch_t<T, CF::small, AK, BKC, VEC>(p, count);
     }
+    // FP32 with B k-contiguous has 64×64 big tiles, so a product of exactly num_cus of them lands here: the same
+    // two-k-group tiles (NT n = 1024)
+    if constexpr (sizeof(T) == 4) {
+        const long long t64 = (long long)((p.M + 63) / 64) * ((p.N + 63) / 64) * count;
+        if (splitk_forced() < 0 && t64 * 2 >= num_cus && t64 <= num_cus)
+            return launch_t<T, TileCfg{64, 64, 2, 2}, AK, BKC, VEC, 2>(p, count);
+    }
     // FP32: 128×128 tiles with two k groups of 2×2 waves (64×64 per wave, 147 KiB of LDS: one workgroup per CU) when
     // their count fills whole rounds of num_cus workgroups (the last round at least 95 % full). Measured (TFLOP/s,
     // against the big tiles above): n = 4096 NN 123 → 125.5, TN 110 → 127.5, NT 123 → 132, n = 2048 NN 118 → 121.5;
