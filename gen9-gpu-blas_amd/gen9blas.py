@@ -1,76 +1,111 @@
-"""gen9blas for MI355X: ctypes + NumPy module over libgen9blas.so (the drop-in for the reference's gen9blas.py).
+"""gen9blas for MI355X: the Python module over libgen9blas.so (ctypes), for NumPy arrays and torch GPU tensors.
 
     import numpy as np, gen9blas
-    C = gen9blas.hgemm(A, B)                  # float16 in, float16 out; accurate=True: GEN9BLAS_HS
-    C = gen9blas.sgemm(A.T, B, alpha=2.0)     # transposed views pass as transpose flags, no copy
-    C = gen9blas.gemm_batched(A3, B3)         # (count, M, K) · (count, K, N)
+    C = gen9blas.hgemm(A, B)                  # float16 in, float16 out; accurate=True selects GEN9BLAS_HS
+    C = gen9blas.sgemm(A.T, B, alpha=2.0)     # a transposed view travels as a transpose flag, not as a copy
+    C = gen9blas.gemm_batched(A3, B3)         # (count, M, K) · (count, K, N) in one launch
     y = gen9blas.gemv(A, x); d = gen9blas.dot(x, y); gen9blas.axpy(0.5, x, y)
 
-Same functions, arguments and errors as the reference module (reference: lib/gen9blas.py:96-410): the element type
-follows the data, views with a row stride or a transpose are passed without copying, a non-zero status raises
-RuntimeError(gen9blas_error()), the library must report version 0.2.x.
+API contract (reference lib/gen9blas.py:96-610): the same public names, positional arguments and defaults.
+- The compute type follows the data: float16, float64, and float32 for every other element type.
+- Row-strided matrices, transposed views and negative vector strides reach the library without a copy. An input in
+  any other layout is copied; an output in such a layout is rejected with TypeError.
+- Shape mismatches raise ValueError. A non-zero library status raises RuntimeError with gen9blas_error()'s text.
+- The library must report version 0.2.x.
 
-MI355X additions: operands may also be torch tensors on the GPU (or any object with __cuda_array_interface__ when
-the output is supplied); the kernels then use them in place and results stay on the device. NumPy arrays are host
-memory: the library copies them to the GPU and back. gen9blas.empty returns pinned host memory from gen9blas_alloc
-(faster DMA than pageable memory).
+Operands on MI355X. A NumPy array is host memory: the library stages it to the GPU and back. A torch tensor on the
+GPU (or an object exposing __cuda_array_interface__) is used in place, and new results for device inputs are
+allocated on the same device. empty() hands out pinned host memory (gen9blas_alloc) from a recycling pool.
 """
+import atexit
+import collections
 import ctypes
 import os
-import weakref
+from typing import NamedTuple
 
 import numpy as np
 
-_HERE = os.path.dirname(os.path.realpath(__file__))
+# ------------------------------------------------------------------------------------------------------------------
+# The shared library and its C signatures
+# ------------------------------------------------------------------------------------------------------------------
 
 
-def _find(name):
-    p = os.path.join(_HERE, name)
-    return p if os.path.exists(p) else name
+def _library_path():
+    """$GEN9BLAS_LIB, else the in-tree build next to this file, else whatever the dynamic loader finds."""
+    explicit = os.environ.get("GEN9BLAS_LIB")
+    if explicit:
+        return explicit
+    local = os.path.join(os.path.dirname(os.path.realpath(__file__)), "libgen9blas.so")
+    return local if os.path.exists(local) else "libgen9blas.so"
 
 
-_lib = ctypes.CDLL(os.environ.get("GEN9BLAS_LIB") or _find("libgen9blas.so"))
-_i, _f, _p, _l, _d = ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.c_long, ctypes.c_double
-_lib.gen9blas_init.argtypes = []
-_lib.gen9blas_gemm.argtypes = [_i, _i, _i, _i, _i, _i, _d, _p, _i, _p, _i, _d, _p, _i]
-_lib.gen9blas_gemm_batched.argtypes = [_i, _i, _i, _i, _i, _i, _d, _p, _i, _l, _p, _i, _l, _d, _p, _i, _l, _i]
-_lib.gen9blas_symm.argtypes = [_i, _i, _i, _i, _i, _d, _p, _i, _p, _i, _d, _p, _i]
-_lib.gen9blas_syrk.argtypes = [_i, _i, _i, _i, _i, _d, _p, _i, _d, _p, _i]
-_lib.gen9blas_syr2k.argtypes = [_i, _i, _i, _i, _i, _d, _p, _i, _p, _i, _d, _p, _i]
-_lib.gen9blas_trmm.argtypes = [_i, _i, _i, _i, _i, _i, _i, _d, _p, _i, _p, _i]
-_lib.gen9blas_trsm.argtypes = [_i, _i, _i, _i, _i, _i, _i, _d, _p, _i, _p, _i]
-_lib.gen9blas_last_time_ms.restype = ctypes.c_double
-_lib.gen9blas_alloc.argtypes = [ctypes.c_size_t]
-_lib.gen9blas_alloc.restype = ctypes.c_void_p
-_lib.gen9blas_free.argtypes = [ctypes.c_void_p]
-_lib.gen9blas_error.restype = ctypes.c_char_p
-_lib.gen9blas_hip_stream.restype = ctypes.c_void_p
-_lib.gen9blas_set_nowait.argtypes = [_i]
-_lib.gen9blas_pack_b.argtypes = [_i, _i, _i, _i, _p, _i]
-_lib.gen9blas_pack_b.restype = _p
-_lib.gen9blas_gemm_pb.argtypes = [_i, _i, _d, _p, _i, _p, _d, _p, _i]
-_lib.gen9blas_packed_b_free.argtypes = [_p]
-_lib.gen9blas_gemm_pb_skinny.argtypes = [_i, _p, _i, _p, _p, _i, ctypes.POINTER(_i)]   # gen9blas_ml.h
+_lib = ctypes.CDLL(_library_path())
+
+# One letter per C type. Upper case letters are pointers to the lower case scalar.
+_CTYPE = {"i": ctypes.c_int, "l": ctypes.c_int64, "d": ctypes.c_double, "f": ctypes.c_float,
+          "p": ctypes.c_void_p, "z": ctypes.c_size_t, "s": ctypes.c_char_p, "v": None,
+          "I": ctypes.POINTER(ctypes.c_int), "L": ctypes.POINTER(ctypes.c_int64),
+          "D": ctypes.POINTER(ctypes.c_double), "F": ctypes.POINTER(ctypes.c_float)}
+
+# gen9blas_<name> = <result>:<arguments>, as declared in include/gen9blas.h, gen9blas_ml.h and gen9blas_hip.h.
+_SIGNATURES = """
+    version=i:  init=i:  device_gen=i:  has=i:i  error=s:  last_status=i:  last_time_ms=d:  last_zero_copy=i:
+    alloc=p:z  free=v:p  is_usm=i:pz
+    gemm=i:iiiiiidpipidpi  gemm_batched=i:iiiiiidpilpildpili  hgemm=i:iiidpipidpi  sgemm=i:iiidpipidpi
+    pack_b=p:iiiipi  gemm_pb=i:iidpipdpi  packed_b_free=v:p  gemm_pb_skinny=i:ipippiI
+    symm=i:iiiiidpipidpi  syrk=i:iiiiidpidpi  syr2k=i:iiiiidpipidpi  trmm=i:iiiiiiidpipi  trsm=i:iiiiiiidpipi
+    axpy=i:iidpipi  scal=i:iidpi  copy=i:iipipi  swap=i:iipipi  rot=i:iipipidd  rotm=i:iipipiD
+    rotg=v:FFFF  rotmg=v:FFFfF  dot=i:iipipiD  asum=i:iipiD  nrm2=i:iipiD  iamax=i:iipiL
+    gemv=i:iiiidpipidpi  ger=i:iiidpipipi  symv=i:iiidpipidpi  trmv=i:iiiiipipi  trsv=i:iiiiipipi
+    syr=i:iiidpipi  syr2=i:iiidpipipi  gbmv=i:iiiiiidpipidpi  sbmv=i:iiiidpipidpi  tbmv=i:iiiiiipipi
+    tbsv=i:iiiiiipipi  spmv=i:iiidppidpi  tpmv=i:iiiiippi  tpsv=i:iiiiippi  spr=i:iiidpip  spr2=i:iiidpipip
+    device_arch=i:  hip_stream=p:  device_alloc=p:z  device_free=v:p  is_device=i:pz  memcpy=i:ppz
+    set_nowait=v:i  flush=i:
+"""
+
+
+def _declare(spec):
+    for item in spec.split():
+        name, sig = item.split("=")
+        result, args = sig.split(":")
+        fn = getattr(_lib, "gen9blas_" + name)
+        fn.restype = _CTYPE[result]
+        fn.argtypes = [_CTYPE[c] for c in args]
+
+
+_declare(_SIGNATURES)
+
+# Type codes of the C API (gen9blas.h) and gen9blas_has features.
 GEN9BLAS_H, GEN9BLAS_S, GEN9BLAS_HS, GEN9BLAS_D = 0, 1, 2, 3
 FEAT_FP16, FEAT_FP32, FEAT_FP64 = 0, 1, 2
-_lib.gen9blas_version.restype = ctypes.c_int
-if _lib.gen9blas_version() // 100 != 2:
-    raise ImportError(f"gen9blas.py expects libgen9blas 0.2.x, loaded {_lib.gen9blas_version()}")
-_SIDE = {"L": 0, "R": 1}
-_TRI = {"L": 0, "U": 1}
-_ready = False
+
+_found = _lib.gen9blas_version()
+if _found // 100 != 2:
+    raise ImportError(f"this gen9blas module is written for libgen9blas 0.2.x; the library reports {_found}")
+
+_F16, _F32, _F64 = np.dtype(np.float16), np.dtype(np.float32), np.dtype(np.float64)
+_TYPE_CODE = {_F16: GEN9BLAS_H, _F32: GEN9BLAS_S, _F64: GEN9BLAS_D}
+_FEATURE = {GEN9BLAS_H: FEAT_FP16, GEN9BLAS_HS: FEAT_FP16, GEN9BLAS_S: FEAT_FP32, GEN9BLAS_D: FEAT_FP64}
+_SIDE_CODE = {"L": 0, "R": 1}
+_UPLO_CODE = {"L": 0, "U": 1}
+_OTHER_UPLO = {"L": "U", "U": "L"}
+_initialized = False
 
 
 def _init():
-    global _ready
-    if not _ready:
-        if _lib.gen9blas_init() != 0:
-            raise RuntimeError(_lib.gen9blas_error().decode())
-        _ready = True
+    """Initializes the library once per process; raises RuntimeError with the library's message if it cannot."""
+    global _initialized
+    if _initialized:
+        return
+    if _lib.gen9blas_init() != 0:
+        raise RuntimeError(_lib.gen9blas_error().decode())
+    _initialized = True
 
 
-def _check(w):
-    if w != 0:
+def _call(name, *args):
+    """gen9blas_<name>(*args) after initialization; a non-zero status becomes RuntimeError(gen9blas_error())."""
+    _init()
+    if getattr(_lib, "gen9blas_" + name)(*args) != 0:
         raise RuntimeError(_lib.gen9blas_error().decode())
 
 
@@ -81,657 +116,738 @@ def hip_stream():
 
 
 def set_nowait(on):
-    """No-wait mode: calls on device operands return without waiting; flush() waits."""
-    _lib.gen9blas_set_nowait(int(bool(on)))
+    """No-wait mode: calls whose operands are all in device memory return once queued; flush() waits for them."""
+    _lib.gen9blas_set_nowait(1 if on else 0)
 
 
 def flush():
-    _check(_lib.gen9blas_flush())
-
-
-# ---------------- pinned host memory pool (gen9blas.empty) ----------------
-_pool = {}
-_pool_bytes = 0
-POOL_MAX = 1 << 30
-
-
-def _block_size(n):
-    return max(4096, (n + 65535) // 65536 * 65536 if n > 65536 else (n + 4095) // 4096 * 4096)
-
-
-def _release(p, n):
-    global _pool_bytes
-    if _pool_bytes + n <= POOL_MAX:
-        _pool.setdefault(n, []).append(p)
-        _pool_bytes += n
-    else:
-        _lib.gen9blas_free(p)
-
-
-def free_pool():
-    """Returns the pooled blocks to the runtime (arrays still in use stay)."""
-    global _pool_bytes
-    for blocks in _pool.values():
-        for p in blocks:
-            _lib.gen9blas_free(p)
-    _pool.clear()
-    _pool_bytes = 0
-
-
-def empty(shape, dtype=np.float16):
-    """C-contiguous array in pinned host memory (gen9blas_alloc). When every view is gone the block returns to a pool
-    (up to POOL_MAX bytes) for later empty() calls of the same rounded size."""
-    global _pool_bytes
-    _init()
-    dtype = np.dtype(dtype)
-    n = int(np.prod(shape)) * dtype.itemsize
-    nb = _block_size(n)
-    if _pool.get(nb):
-        p = _pool[nb].pop()
-        _pool_bytes -= nb
-    else:
-        p = _lib.gen9blas_alloc(nb)
-        if not p:
-            raise MemoryError(_lib.gen9blas_error().decode())
-    raw = (ctypes.c_char * nb).from_address(p)
-    f = weakref.finalize(raw, _release, p, nb)
-    f.atexit = False
-    return np.frombuffer(raw, dtype=np.uint8, count=n).view(dtype).reshape(shape)
-
-
-def available(dt, accurate=False):
-    _init()
-    k = _kind(dt, accurate)
-    return bool(_lib.gen9blas_has(FEAT_FP32 if k == GEN9BLAS_S else FEAT_FP64 if k == GEN9BLAS_D else FEAT_FP16))
-
-
-def _kind(dt, accurate):
-    dt = _np_dtype(dt)
-    if dt == np.float32:
-        return GEN9BLAS_S
-    if dt == np.float64:
-        return GEN9BLAS_D
-    if dt == np.float16:
-        return GEN9BLAS_HS if accurate else GEN9BLAS_H
-    raise TypeError("supported types: float16, float32, float64")
-
-
-# ---------------- device tensors (torch) ----------------
-def _is_dev(X):
-    return getattr(X, "is_cuda", False) and hasattr(X, "data_ptr")
-
-
-def _np_dtype(dt):
-    if isinstance(dt, np.dtype) or isinstance(dt, type):
-        return np.dtype(dt)
-    s = str(dt)   # torch.float16 -> "torch.float16"
-    if s.startswith("torch."):
-        return np.dtype(s[6:])
-    return np.dtype(dt)
-
-
-def _torch_dtype(dt):
-    import torch
-    return {np.dtype(np.float16): torch.float16, np.dtype(np.float32): torch.float32,
-            np.dtype(np.float64): torch.float64}[np.dtype(dt)]
-
-
-def _dtype_of_arr(X):
-    return _np_dtype(X.dtype)
-
-
-def _dev_mat(A, dt, write=False):
-    """(tensor, pointer, rows, cols, ld, trans) of a 2-D device tensor; strided rows and transposes in place."""
-    if A.dim() != 2:
-        raise ValueError("expected a 2-D matrix")
-    if _np_dtype(A.dtype) != np.dtype(dt):
-        if write:
-            raise TypeError(f"the result must be a {np.dtype(dt).name} matrix")
-        A = A.to(_torch_dtype(dt))
-    s0, s1 = A.stride()
-    r, c = A.shape
-    if s1 == 1 and s0 >= c:
-        return A, A.data_ptr(), r, c, s0, 0
-    if not write and s0 == 1 and s1 >= r:
-        return A, A.data_ptr(), c, r, s1, 1
-    if write:
-        raise TypeError(f"the result must be a {np.dtype(dt).name} matrix with contiguous rows")
-    A = A.contiguous()
-    return A, A.data_ptr(), r, c, c, 0
-
-
-def _dev_vec(x, dt, write=False):
-    if x.dim() != 1:
-        raise ValueError("expected a 1-D vector")
-    if _np_dtype(x.dtype) != np.dtype(dt) or x.stride()[0] == 0:
-        if write:
-            raise TypeError(f"the result must be a {np.dtype(dt).name} vector with a non-zero stride")
-        x = x.to(_torch_dtype(dt)).contiguous()
-    n, inc = x.shape[0], x.stride()[0]
-    return x, x.data_ptr(), n, inc
-
-
-# ---------------- level 3 ----------------
-def _m3(X, dt, write=False):
-    X, p, _, _, ld, tr = _mat(X, dt, write)
-    return X, p, ld, tr
-
-
-def _c(X, dt):
-    if _is_dev(X):
-        return X.to(_torch_dtype(dt)).contiguous()
-    return np.ascontiguousarray(X, dtype=dt)
-
-
-def _output(C, shape, dt, like):
-    """(C, given, ldc): a new C (device tensor for device inputs, else pinned host memory) or the supplied C."""
-    if C is None:
-        if _is_dev(like):
-            import torch
-            return torch.empty(tuple(shape), dtype=_torch_dtype(dt), device=like.device), False, shape[-1]
-        return empty(shape, dt), False, shape[-1]
-    if _is_dev(C):
-        if tuple(C.shape) != tuple(shape) or _np_dtype(C.dtype) != np.dtype(dt) or C.stride()[-1] != 1:
-            raise ValueError(f"C must have shape {tuple(shape)}, type {np.dtype(dt).name} and contiguous rows")
-        if C.dim() == 2:
-            return C, True, _dev_mat(C, dt, True)[4]
-        if not C.is_contiguous():
-            raise ValueError("C (batch) must be C-contiguous")
-        return C, True, shape[-1]
-    if C.shape != tuple(shape) or C.dtype != dt or C.strides[-1] != C.itemsize:
-        raise ValueError(f"C must have shape {tuple(shape)}, type {np.dtype(dt).name} and contiguous rows")
-    if C.ndim == 2:
-        return C, True, _mat(C, dt, True)[4]
-    if not C.flags.c_contiguous:
-        raise ValueError("C (batch) must be C-contiguous")
-    return C, True, shape[-1]
-
-
-def _ptr(X):
-    return X.data_ptr() if _is_dev(X) else X.ctypes.data
-
-
-def gemm(A, B, alpha=1.0, beta=0.0, C=None, accurate=False):
-    """C = alpha·A·B + beta·C (float16, float32 or float64 according to A)."""
-    _init()
-    dt = _dtype_of_arr(A)
-    if dt not in (np.float16, np.float32, np.float64):
-        dt = np.dtype(np.float32)
-    (M, K), (K2, N) = tuple(A.shape), tuple(B.shape)
-    if K != K2:
-        raise ValueError(f"incompatible dimensions: {tuple(A.shape)} · {tuple(B.shape)}")
-    a, pa, lda, ta = _m3(A, dt)
-    b, pb, ldb, tb = _m3(B, dt)
-    C, given, ldc = _output(C, (M, N), dt, A)
-    _check(_lib.gen9blas_gemm(_kind(dt, accurate), ta, tb, M, N, K, alpha, pa, lda, pb, ldb, beta if given else 0.0,
-                              _ptr(C), ldc))
-    return C
-
-
-def _astype(X, dt):
-    if _is_dev(X):
-        return X if _np_dtype(X.dtype) == np.dtype(dt) else X.to(_torch_dtype(dt))
-    return X if X.dtype == dt else X.astype(dt)
-
-
-def hgemm(A, B, alpha=1.0, beta=0.0, C=None, accurate=False):
-    return gemm(_astype(A, np.float16), _astype(B, np.float16), alpha, beta, C, accurate)
-
-
-def sgemm(A, B, alpha=1.0, beta=0.0, C=None):
-    return gemm(_astype(A, np.float32), _astype(B, np.float32), alpha, beta, C)
-
-
-def gemm_batched(A, B, alpha=1.0, beta=0.0, C=None, accurate=False):
-    """Batch of products: A (count, M, K), B (count, K, N) -> C (count, M, N), one launch."""
-    _init()
-    dt = _dtype_of_arr(A)
-    if dt not in (np.float16, np.float32, np.float64):
-        dt = np.dtype(np.float32)
-    a, b = _c(A, dt), _c(B, dt)
-    (cnt, M, K), (cnt2, K2, N) = tuple(a.shape), tuple(b.shape)
-    if K != K2 or cnt != cnt2:
-        raise ValueError(f"incompatible dimensions: {tuple(a.shape)} · {tuple(b.shape)}")
-    C, given, _ = _output(C, (cnt, M, N), dt, A)
-    _check(_lib.gen9blas_gemm_batched(_kind(dt, accurate), 0, 0, M, N, K, alpha, _ptr(a), K, M * K, _ptr(b), N, K * N,
-                                      beta if given else 0.0, _ptr(C), N, M * N, cnt))
-    return C
-
-
-def _square(A, dt, uplo):
-    A, p, r, c, ld, tr = _mat(A, dt)
-    if r != c:
-        raise ValueError("expected a square matrix")
-    return A, p, r, ld, tr, ({"L": "U", "U": "L"}[uplo] if tr else uplo)
-
-
-def _copy_of(B, dt):
-    b = empty(tuple(B.shape), dt)
-    b[...] = B
-    return b
-
-
-def symm(A, B, side="L", uplo="L", alpha=1.0, beta=0.0, C=None, accurate=False):
-    _init()
-    dt = _dtype_of_arr(B)
-    a, pa, n, lda, _, uplo = _square(A, dt, uplo)
-    b, pb, ldb, tb = _m3(B, dt)
-    if tb:
-        b, pb, ldb, tb = _m3(_c(B, dt), dt)
-    M, N = B.shape
-    C, given, ldc = _output(C, (M, N), dt, B)
-    _check(_lib.gen9blas_symm(_kind(dt, accurate), _SIDE[side], _TRI[uplo], M, N, alpha, pa, lda, pb, ldb,
-                              beta if given else 0.0, _ptr(C), ldc))
-    return C
-
-
-def syrk(A, uplo="L", trans=False, alpha=1.0, beta=0.0, C=None, accurate=False):
-    _init()
-    dt = _dtype_of_arr(A)
-    N, K = (A.shape[1], A.shape[0]) if trans else A.shape
-    a, pa, lda, ta = _m3(A, dt)
-    C, given, ldc = _output(C, (N, N), dt, A)
-    if not given:
-        C[...] = 0
-    _check(_lib.gen9blas_syrk(_kind(dt, accurate), _TRI[uplo], int(trans) ^ ta, N, K, alpha, pa, lda,
-                              beta if given else 0.0, _ptr(C), ldc))
-    return C
-
-
-def syr2k(A, B, uplo="L", trans=False, alpha=1.0, beta=0.0, C=None, accurate=False):
-    _init()
-    dt = _dtype_of_arr(A)
-    N, K = (A.shape[1], A.shape[0]) if trans else A.shape
-    a, pa, lda, ta = _m3(A, dt)
-    b, pb, ldb, tb = _m3(B, dt)
-    if ta != tb:
-        b, pb, ldb, tb = _m3(np.ascontiguousarray(B.T, dtype=dt).T if ta else _c(B, dt), dt)
-    C, given, ldc = _output(C, (N, N), dt, A)
-    if not given:
-        C[...] = 0
-    _check(_lib.gen9blas_syr2k(_kind(dt, accurate), _TRI[uplo], int(trans) ^ ta, N, K, alpha, pa, lda, pb, ldb,
-                               beta if given else 0.0, _ptr(C), ldc))
-    return C
-
-
-def trmm(A, B, side="L", uplo="L", transA=False, diag=False, alpha=1.0, accurate=False):
-    _init()
-    dt = _dtype_of_arr(B)
-    a, pa, _, lda, ta, uplo = _square(A, dt, uplo)
-    b = _copy_of(B, dt)
-    M, N = b.shape
-    _check(_lib.gen9blas_trmm(_kind(dt, accurate), _SIDE[side], _TRI[uplo], int(transA) ^ ta, int(diag), M, N, alpha, pa,
-                              lda, b.ctypes.data, N))
-    return b
-
-
-def trsm(A, B, side="L", uplo="L", transA=False, diag=False, alpha=1.0, accurate=False):
-    _init()
-    dt = _dtype_of_arr(B)
-    if dt not in (np.float16, np.float32, np.float64):
-        dt = np.dtype(np.float32)
-    a, pa, _, lda, ta, uplo = _square(A, dt, uplo)
-    b = _copy_of(B, dt)
-    M, N = b.shape
-    _check(_lib.gen9blas_trsm(_kind(dt, accurate), _SIDE[side], _TRI[uplo], int(transA) ^ ta, int(diag), M, N, alpha, pa,
-                              lda, b.ctypes.data, N))
-    return b
+    _call("flush")
 
 
 def last_time_ms():
+    """Duration of the last call in ms: the device time of its kernels with GEN9BLAS_PROFILE=1, else the whole call."""
     return _lib.gen9blas_last_time_ms()
 
 
 def last_zero_copy():
+    """Operands of the last level-3 call used in place in device memory, as bits: 1 = A, 2 = B, 4 = C."""
     return _lib.gen9blas_last_zero_copy()
 
 
-# ---------------- levels 1-2 (FP16 computed in FP32, reductions in FP64) ----------------
-_lib.gen9blas_axpy.argtypes = [_i, _i, _d, _p, _i, _p, _i]
-_lib.gen9blas_scal.argtypes = [_i, _i, _d, _p, _i]
-_lib.gen9blas_copy.argtypes = [_i, _i, _p, _i, _p, _i]
-_lib.gen9blas_swap.argtypes = [_i, _i, _p, _i, _p, _i]
-_lib.gen9blas_rot.argtypes = [_i, _i, _p, _i, _p, _i, _d, _d]
-_lib.gen9blas_dot.argtypes = [_i, _i, _p, _i, _p, _i, ctypes.POINTER(_d)]
-_lib.gen9blas_asum.argtypes = [_i, _i, _p, _i, ctypes.POINTER(_d)]
-_lib.gen9blas_nrm2.argtypes = [_i, _i, _p, _i, ctypes.POINTER(_d)]
-_lib.gen9blas_iamax.argtypes = [_i, _i, _p, _i, ctypes.POINTER(_l)]
-_lib.gen9blas_gemv.argtypes = [_i, _i, _i, _i, _d, _p, _i, _p, _i, _d, _p, _i]
-_lib.gen9blas_ger.argtypes = [_i, _i, _i, _d, _p, _i, _p, _i, _p, _i]
+# ------------------------------------------------------------------------------------------------------------------
+# Pinned host memory: empty() and its pool
+# ------------------------------------------------------------------------------------------------------------------
+POOL_MAX = 1 << 30     # bytes of released pinned blocks kept for reuse; blocks beyond that are freed at release
+_exiting = False
 
 
-def _dtype_of(*X):
-    dt = _dtype_of_arr(X[0])
-    return np.dtype(np.float16) if dt == np.float16 else np.dtype(np.float64) if dt == np.float64 else np.dtype(np.float32)
+@atexit.register
+def _mark_exit():
+    # Arrays collected during interpreter shutdown must not call into a library that may already be torn down; the
+    # process exit returns pinned memory to the driver anyway.
+    global _exiting
+    _exiting = True
 
 
-def _vec(x, dt, write=False):
-    """(array, pointer to the lowest address, n, inc) of a 1-D vector; inc < 0 as in BLAS."""
-    if _is_dev(x):
-        x, p, n, inc = _dev_vec(x, dt, write)
-        return x, p + (min(inc, 0) * (n - 1) * x.element_size() if n else 0), n, inc
-    if x.ndim != 1:
-        raise ValueError("expected a 1-D vector")
-    if x.dtype != dt or x.strides[0] % x.itemsize or x.strides[0] == 0:
-        if write:
-            raise TypeError(f"the result must be a {np.dtype(dt).name} vector with a stride that is a multiple of the "
-                            "element size")
-        x = np.ascontiguousarray(x, dtype=dt)
-    n, inc = x.shape[0], x.strides[0] // x.itemsize
-    return x, x.ctypes.data + (min(inc, 0) * (n - 1) * x.itemsize if n else 0), n, inc
+class _PinnedPool:
+    """Pinned (page-locked) host blocks from gen9blas_alloc, which the DMA engines read at full speed but which are
+    slow to allocate. A released block waits, keyed by its size class, for a later request of the same class."""
+
+    def __init__(self):
+        self.spare = collections.defaultdict(list)
+        self.spare_bytes = 0
+
+    @staticmethod
+    def size_class(nbytes):
+        """Powers of two up to 1 MiB (at least one 4 KiB page), whole MiB above: a small block wastes at most half of
+        itself, a large one less than 1 MiB."""
+        if nbytes <= 1 << 20:
+            return max(4096, 1 << max(nbytes - 1, 0).bit_length())
+        return -(-nbytes >> 20) << 20
+
+    def take(self, nbytes):
+        size = self.size_class(nbytes)
+        if self.spare[size]:
+            self.spare_bytes -= size
+            return self.spare[size].pop(), size
+        _init()
+        ptr = _lib.gen9blas_alloc(size)
+        if not ptr:
+            raise MemoryError(_lib.gen9blas_error().decode())
+        return ptr, size
+
+    def give(self, ptr, size):
+        if self.spare_bytes + size > POOL_MAX:
+            _lib.gen9blas_free(ptr)
+            return
+        self.spare[size].append(ptr)
+        self.spare_bytes += size
+
+    def drain(self):
+        for blocks in self.spare.values():
+            while blocks:
+                _lib.gen9blas_free(blocks.pop())
+        self.spare_bytes = 0
 
 
-def _mat(A, dt, write=False):
-    """(array, pointer, rows, columns, ld, trans) for a row-major matrix with ld; a transposed view passes as trans."""
-    if _is_dev(A):
-        return _dev_mat(A, dt, write)
-    if A.ndim != 2:
-        raise ValueError("expected a 2-D matrix")
-    e = A.itemsize
-    if A.dtype == dt and A.strides[1] == e and A.strides[0] >= A.shape[1] * e and A.strides[0] % e == 0:
-        return A, A.ctypes.data, A.shape[0], A.shape[1], A.strides[0] // e, 0
-    if not write and A.dtype == dt and A.strides[0] == e and A.strides[1] >= A.shape[0] * e and A.strides[1] % e == 0:
-        return A, A.ctypes.data, A.shape[1], A.shape[0], A.strides[1] // e, 1
-    if write:
-        raise TypeError(f"the result must be a {np.dtype(dt).name} matrix with contiguous rows")
-    A = np.ascontiguousarray(A, dtype=dt)
-    return A, A.ctypes.data, A.shape[0], A.shape[1], A.shape[1], 0
+_pool = _PinnedPool()
 
 
-def _kind_basic(dt):
-    return GEN9BLAS_S if dt == np.float32 else GEN9BLAS_D if dt == np.float64 else GEN9BLAS_H
+class _PinnedBlock:
+    """Owns one pooled block. NumPy arrays built on it hold it through their .base chain, so it is collected, and the
+    block handed back to the pool, only when no view of it is left."""
+
+    def __init__(self, ptr, size, nbytes):
+        self.ptr, self.size = ptr, size
+        self.__array_interface__ = {"version": 3, "shape": (nbytes,), "typestr": "|u1", "data": (ptr, False)}
+
+    def __del__(self):
+        if not _exiting:
+            _pool.give(self.ptr, self.size)
 
 
-def _new_vec(n, dt, like):
-    if _is_dev(like):
+def empty(shape, dtype=np.float16):
+    """Uninitialized C-contiguous array in pinned host memory (faster transfers than pageable NumPy memory). When
+    every view of it is gone, its block returns to a pool (up to POOL_MAX bytes) for later empty() calls."""
+    dt = np.dtype(dtype)
+    shape = (int(shape),) if np.ndim(shape) == 0 else tuple(int(s) for s in shape)
+    nbytes = int(np.prod(shape, dtype=np.int64)) * dt.itemsize
+    ptr, size = _pool.take(nbytes)
+    return np.asarray(_PinnedBlock(ptr, size, nbytes)).view(dt).reshape(shape)
+
+
+def free_pool():
+    """Frees the released blocks waiting in the pool (arrays still in use keep theirs)."""
+    _pool.drain()
+
+
+# ------------------------------------------------------------------------------------------------------------------
+# Operands: one description for NumPy arrays and torch tensors
+# ------------------------------------------------------------------------------------------------------------------
+_torch = None
+
+
+def _torch_module():
+    global _torch
+    if _torch is None:
         import torch
-        return torch.empty((n,), dtype=_torch_dtype(dt), device=like.device)
-    return empty((n,), dt)
+        _torch = torch
+    return _torch
+
+
+def _is_tensor(X):
+    return type(X).__module__.startswith("torch") and hasattr(X, "data_ptr")
+
+
+def _torch_dtype(t):
+    torch = _torch_module()
+    return {_F16: torch.float16, _F32: torch.float32, _F64: torch.float64}[t]
+
+
+def _numpy_dtype(X):
+    """Element type of X as a NumPy dtype, or None for a torch type NumPy does not know (bfloat16, ...)."""
+    if _is_tensor(X):
+        name = str(X.dtype).rpartition(".")[2]
+        return np.dtype(name) if name in ("float16", "float32", "float64") else None
+    return np.asarray(X).dtype if not hasattr(X, "dtype") else np.dtype(X.dtype)
+
+
+class _Operand(NamedTuple):
+    obj: object        # the array or tensor the address belongs to
+    ptr: int
+    shape: tuple
+    steps: tuple       # strides in elements; None if one of them is not a whole number of elements
+    dtype: object      # NumPy dtype, or None (an element type the library has no kernel for)
+    on_gpu: bool
+
+
+def _operand(X):
+    if _is_tensor(X):
+        if X.is_cuda:
+            return _Operand(X, X.data_ptr(), tuple(X.shape), tuple(X.stride()), _numpy_dtype(X), True)
+        X = X.numpy()                                   # a CPU tensor: its NumPy view shares the memory
+    elif hasattr(X, "__cuda_array_interface__") and not isinstance(X, np.ndarray):
+        return _operand(_torch_module().as_tensor(X, device="cuda"))
+    X = X if isinstance(X, np.ndarray) else np.asarray(X)
+    e = X.itemsize
+    steps = tuple(s // e for s in X.strides) if all(s % e == 0 for s in X.strides) else None
+    return _Operand(X, X.ctypes.data, X.shape, steps, X.dtype, False)
+
+
+def _compute_type(X):
+    """float16 and float64 compute in their own type, everything else in float32."""
+    dt = _numpy_dtype(X)
+    return dt if dt in (_F16, _F64) else _F32
+
+
+def _strict_type(X):
+    dt = _numpy_dtype(X)
+    if dt not in _TYPE_CODE:
+        raise TypeError("supported types: float16, float32, float64")
+    return dt
+
+
+def _kind(t, accurate=False):
+    return GEN9BLAS_HS if (accurate and t == _F16) else _TYPE_CODE[t]
+
+
+def available(dt, accurate=False):
+    """Whether the device runs this element type (float16 with accurate=True: the GEN9BLAS_HS mode)."""
+    _init()
+    dt = np.dtype(str(dt).rpartition(".")[2]) if not isinstance(dt, (np.dtype, type)) else np.dtype(dt)
+    if dt not in _TYPE_CODE:
+        raise TypeError("supported types: float16, float32, float64")
+    return bool(_lib.gen9blas_has(_FEATURE[_kind(dt, accurate)]))
+
+
+def _dense(X, t):
+    """X as a C-contiguous array of type t on the same side (host or device); no copy if it already is one."""
+    if _is_tensor(X) and X.is_cuda:
+        return X.to(dtype=_torch_dtype(t)).contiguous()
+    return np.ascontiguousarray(X, dtype=t)
+
+
+def _as_type(X, t):
+    """X itself if its elements are already of type t (any layout), else a converted copy."""
+    if _numpy_dtype(X) == t:
+        return X
+    if _is_tensor(X) and X.is_cuda:
+        return X.to(dtype=_torch_dtype(t))
+    return np.asarray(X).astype(t)
+
+
+def _transposed(X):
+    return X.t() if _is_tensor(X) else X.T
+
+
+def _writable_check(X, what):
+    if not (isinstance(X, np.ndarray) or _is_tensor(X) or hasattr(X, "__cuda_array_interface__")):
+        raise TypeError(f"the result ({what}) must be a NumPy array or a GPU tensor")
+
+
+class _Mat(NamedTuple):
+    keep: object       # what the address belongs to (the argument, or its copy)
+    ptr: int
+    shape: tuple       # the shape the caller sees
+    ld: int            # row stride of the matrix as it lies in memory
+    trans: int         # 1: the caller's matrix is the transpose of the row-major matrix in memory
+
+    @property
+    def stored(self):
+        return self.shape[::-1] if self.trans else self.shape
+
+
+def _matrix(X, t, out=False):
+    """A 2-D operand of type t as the library takes it: row-major with a row stride, or (inputs only) the transpose
+    of one. Inputs in another layout or type are copied; outputs must already be row-major of type t."""
+    if out:
+        _writable_check(X, "matrix")
+    d = _operand(X)
+    if len(d.shape) != 2:
+        raise ValueError("expected a 2-D matrix")
+    rows, cols = d.shape
+    if d.dtype == t and d.steps is not None:
+        row_step, col_step = d.steps
+        if col_step == 1 and row_step >= max(cols, 1):
+            return _Mat(d.obj, d.ptr, (rows, cols), row_step, 0)
+        if not out and row_step == 1 and col_step >= max(rows, 1):
+            return _Mat(d.obj, d.ptr, (rows, cols), col_step, 1)
+        if rows <= 1 and col_step == 1:                 # one row: any row stride will do
+            return _Mat(d.obj, d.ptr, (rows, cols), max(cols, 1), 0)
+    if out:
+        raise TypeError(f"the result must be a {t.name} matrix with contiguous rows")
+    return _matrix(_dense(d.obj, t), t)
+
+
+class _Vec(NamedTuple):
+    keep: object
+    ptr: int           # lowest address touched (for inc < 0 the last element), as BLAS expects
+    n: int
+    inc: int
+
+
+def _vector(x, t, out=False):
+    """A 1-D operand of type t with a non-zero element stride (negative strides allowed). Inputs of another type or
+    with a stride that is not a whole number of elements are copied; outputs raise TypeError instead."""
+    if out:
+        _writable_check(x, "vector")
+    d = _operand(x)
+    if len(d.shape) != 1:
+        raise ValueError("expected a 1-D vector")
+    n = d.shape[0]
+    if d.dtype == t and d.steps is not None and d.steps[0] != 0:
+        inc = d.steps[0]
+        low = d.ptr + (inc * (n - 1) * t.itemsize if inc < 0 and n > 0 else 0)
+        return _Vec(d.obj, low, n, inc)
+    if out:
+        raise TypeError(f"the result must be a {t.name} vector whose stride is a non-zero multiple of the element size")
+    return _vector(_dense(d.obj, t), t)
+
+
+def _equal_lengths(*vs):
+    if len({v.n for v in vs}) > 1:
+        raise ValueError("vector lengths differ")
+    return vs
+
+
+def _new(shape, t, like):
+    """A new result: on the device of `like` if that is a GPU tensor, else in pinned host memory."""
+    d = _operand(like)
+    if d.on_gpu:
+        return _torch_module().empty(tuple(shape), dtype=_torch_dtype(t), device=d.obj.device)
+    return empty(shape, t)
+
+
+class _Out(NamedTuple):
+    obj: object
+    ptr: int
+    ld: int            # row stride (matrices) or element stride (vectors)
+    given: bool        # the caller supplied it, so beta applies
+
+    def beta(self, beta):
+        return beta if self.given else 0.0
+
+
+def _out_matrix(C, shape, t, like):
+    if C is None:
+        C = _new(shape, t, like)
+        return _Out(C, _operand(C).ptr, shape[-1], False)
+    _writable_check(C, "C")
+    d = _operand(C)
+    if tuple(d.shape) != tuple(shape) or d.dtype != t or d.steps is None or d.steps[-1] != 1:
+        raise ValueError(f"C must have shape {tuple(shape)}, type {t.name} and contiguous rows")
+    if len(shape) == 2:
+        return _Out(C, d.ptr, _matrix(C, t, out=True).ld, True)
+    dense_steps = tuple(int(np.prod(shape[i + 1:], dtype=np.int64)) for i in range(len(shape)))
+    if any(s != w for s, w, n in zip(d.steps, dense_steps, shape) if n > 1):
+        raise ValueError("C (batch) must be C-contiguous")
+    return _Out(C, d.ptr, shape[-1], True)
+
+
+def _out_vector(y, n, t, like):
+    if y is None:
+        y = _new((n,), t, like)
+        v = _vector(y, t, out=True)
+        return _Out(y, v.ptr, v.inc, False)
+    v = _vector(y, t, out=True)
+    if v.n != n:
+        raise ValueError(f"y has length {v.n}, the product has {n}")
+    return _Out(y, v.ptr, v.inc, True)
+
+
+def _square(A, t, uplo):
+    """A square matrix whose `uplo` triangle is meant, and the triangle as it lies in memory (a transposed view holds
+    the caller's lower triangle in the stored matrix's upper one)."""
+    a = _matrix(A, t)
+    if a.shape[0] != a.shape[1]:
+        raise ValueError("expected a square matrix")
+    return a, (_OTHER_UPLO[uplo] if a.trans else uplo)
+
+
+def _private_copy(B, t):
+    """A new C-contiguous copy of B that a routine may overwrite: on B's device, or in pinned host memory."""
+    if _is_tensor(B) and B.is_cuda:
+        return B.to(dtype=_torch_dtype(t), copy=True).contiguous()
+    b = empty(np.shape(B), t)
+    b[...] = B
+    return b
+
+
+# ------------------------------------------------------------------------------------------------------------------
+# Level 3
+# ------------------------------------------------------------------------------------------------------------------
+
+
+def gemm(A, B, alpha=1.0, beta=0.0, C=None, accurate=False):
+    """C = alpha·A·B + beta·C in the type of A (float16, float32, float64; other types compute in float32). beta
+    applies only to a supplied C. float16 with accurate=True is GEN9BLAS_HS."""
+    t = _compute_type(A)
+    a, b = _matrix(A, t), _matrix(B, t)
+    (M, K), (K_b, N) = a.shape, b.shape
+    if K != K_b:
+        raise ValueError(f"incompatible dimensions: {a.shape} · {b.shape}")
+    c = _out_matrix(C, (M, N), t, A)
+    _call("gemm", _kind(t, accurate), a.trans, b.trans, M, N, K, alpha, a.ptr, a.ld, b.ptr, b.ld, c.beta(beta),
+          c.ptr, c.ld)
+    return c.obj
+
+
+def hgemm(A, B, alpha=1.0, beta=0.0, C=None, accurate=False):
+    """gemm in float16 (inputs of another type are converted first)."""
+    return gemm(_as_type(A, _F16), _as_type(B, _F16), alpha, beta, C, accurate)
+
+
+def sgemm(A, B, alpha=1.0, beta=0.0, C=None):
+    """gemm in float32 (inputs of another type are converted first)."""
+    return gemm(_as_type(A, _F32), _as_type(B, _F32), alpha, beta, C)
+
+
+def gemm_batched(A, B, alpha=1.0, beta=0.0, C=None, accurate=False):
+    """C[i] = alpha·A[i]·B[i] + beta·C[i] for stacks A (count, M, K) and B (count, K, N), in one launch."""
+    t = _compute_type(A)
+    a, b = _dense(A, t), _dense(B, t)
+    if len(a.shape) != 3 or len(b.shape) != 3:
+        raise ValueError("expected stacks of matrices (count, rows, columns)")
+    (count, M, K), (count_b, K_b, N) = tuple(a.shape), tuple(b.shape)
+    if (count, K) != (count_b, K_b):
+        raise ValueError(f"incompatible dimensions: {tuple(a.shape)} · {tuple(b.shape)}")
+    c = _out_matrix(C, (count, M, N), t, A)
+    _call("gemm_batched", _kind(t, accurate), 0, 0, M, N, K, alpha, _operand(a).ptr, K, M * K, _operand(b).ptr, N,
+          K * N, c.beta(beta), c.ptr, N, M * N, count)
+    return c.obj
+
+
+def symm(A, B, side="L", uplo="L", alpha=1.0, beta=0.0, C=None, accurate=False):
+    """C = alpha·A·B + beta·C (side "L") or alpha·B·A + beta·C (side "R"), A symmetric from its `uplo` triangle."""
+    t = _strict_type(B)
+    a, stored_uplo = _square(A, t, uplo)
+    b = _matrix(B, t)
+    if b.trans:
+        b = _matrix(_dense(B, t), t)
+    M, N = b.shape
+    c = _out_matrix(C, (M, N), t, B)
+    _call("symm", _kind(t, accurate), _SIDE_CODE[side], _UPLO_CODE[stored_uplo], M, N, alpha, a.ptr, a.ld, b.ptr,
+          b.ld, c.beta(beta), c.ptr, c.ld)
+    return c.obj
+
+
+def syrk(A, uplo="L", trans=False, alpha=1.0, beta=0.0, C=None, accurate=False):
+    """The `uplo` triangle of alpha·A·Aᵀ + beta·C (trans: alpha·Aᵀ·A + beta·C); a new C is zero off the triangle."""
+    t = _strict_type(A)
+    a = _matrix(A, t)
+    N, K = a.shape[::-1] if trans else a.shape
+    c = _out_matrix(C, (N, N), t, A)
+    if not c.given:
+        c.obj[...] = 0
+    _call("syrk", _kind(t, accurate), _UPLO_CODE[uplo], int(bool(trans)) ^ a.trans, N, K, alpha, a.ptr, a.ld,
+          c.beta(beta), c.ptr, c.ld)
+    return c.obj
+
+
+def syr2k(A, B, uplo="L", trans=False, alpha=1.0, beta=0.0, C=None, accurate=False):
+    """The `uplo` triangle of alpha·(A·Bᵀ + B·Aᵀ) + beta·C (trans: alpha·(Aᵀ·B + Bᵀ·A) + beta·C)."""
+    t = _strict_type(A)
+    a, b = _matrix(A, t), _matrix(B, t)
+    if b.trans != a.trans:
+        # One transpose flag covers both operands: lay B out in memory the way A lies.
+        b = _matrix(_transposed(_dense(_transposed(B), t)) if a.trans else _dense(B, t), t)
+    N, K = a.shape[::-1] if trans else a.shape
+    c = _out_matrix(C, (N, N), t, A)
+    if not c.given:
+        c.obj[...] = 0
+    _call("syr2k", _kind(t, accurate), _UPLO_CODE[uplo], int(bool(trans)) ^ a.trans, N, K, alpha, a.ptr, a.ld, b.ptr,
+          b.ld, c.beta(beta), c.ptr, c.ld)
+    return c.obj
+
+
+def _triangular_solve_or_product(name, A, B, side, uplo, transA, diag, alpha, accurate, t):
+    a, stored_uplo = _square(A, t, uplo)
+    X = _private_copy(B, t)
+    M, N = X.shape
+    _call(name, _kind(t, accurate), _SIDE_CODE[side], _UPLO_CODE[stored_uplo], int(bool(transA)) ^ a.trans,
+          int(bool(diag)), M, N, alpha, a.ptr, a.ld, _operand(X).ptr, max(N, 1))
+    return X
+
+
+def trmm(A, B, side="L", uplo="L", transA=False, diag=False, alpha=1.0, accurate=False):
+    """alpha·op(A)·B (side "L") or alpha·B·op(A) (side "R"), A triangular (diag: unit diagonal). B is unchanged."""
+    return _triangular_solve_or_product("trmm", A, B, side, uplo, transA, diag, alpha, accurate, _strict_type(B))
+
+
+def trsm(A, B, side="L", uplo="L", transA=False, diag=False, alpha=1.0, accurate=False):
+    """X with op(A)·X = alpha·B (side "L") or X·op(A) = alpha·B (side "R"), A triangular. B is unchanged."""
+    return _triangular_solve_or_product("trsm", A, B, side, uplo, transA, diag, alpha, accurate, _compute_type(B))
+
+
+# ------------------------------------------------------------------------------------------------------------------
+# Level 1 (float16 computes in float32; dot, asum and nrm2 accumulate in float64)
+# ------------------------------------------------------------------------------------------------------------------
+
+
+def _two_in_place(name, x, y, *extra):
+    t = _compute_type(x)
+    vx, vy = _equal_lengths(_vector(x, t, out=True), _vector(y, t, out=True))
+    _call(name, _TYPE_CODE[t], vx.n, vx.ptr, vx.inc, vy.ptr, vy.inc, *extra)
+    return x, y
+
+
+def _reduction(name, box, *xs):
+    t = _compute_type(xs[0])
+    vs = _equal_lengths(*(_vector(x, t) for x in xs))
+    args = [a for v in vs for a in (v.ptr, v.inc)]
+    result = box()
+    _call(name, _TYPE_CODE[t], vs[0].n, *args, ctypes.byref(result))
+    return result.value
 
 
 def axpy(a, x, y):
-    """y = a·x + y (in place); returns y."""
-    _init(); t = _dtype_of(y); y, py, n, iy = _vec(y, t, True); x, px, nx, ix = _vec(x, t)
-    if nx != n:
-        raise ValueError("lengths differ")
-    _check(_lib.gen9blas_axpy(_kind_basic(t), n, a, px, ix, py, iy)); return y
+    """y = a·x + y in place; returns y."""
+    t = _compute_type(y)
+    vy, vx = _equal_lengths(_vector(y, t, out=True), _vector(x, t))
+    _call("axpy", _TYPE_CODE[t], vy.n, a, vx.ptr, vx.inc, vy.ptr, vy.inc)
+    return y
 
 
 def scal(a, x):
-    """x = a·x (in place); returns x."""
-    _init(); t = _dtype_of(x); x, px, n, ix = _vec(x, t, True)
-    _check(_lib.gen9blas_scal(_kind_basic(t), n, a, px, ix)); return x
+    """x = a·x in place; returns x."""
+    t = _compute_type(x)
+    vx = _vector(x, t, out=True)
+    _call("scal", _TYPE_CODE[t], vx.n, a, vx.ptr, vx.inc)
+    return x
 
 
 def copy(x, y=None):
-    """y = x; without y: a new array of the type of x."""
-    _init(); t = _dtype_of(y if y is not None else x)
+    """y = x; without y, a new vector of x's type (on x's device for a GPU tensor)."""
+    t = _compute_type(x if y is None else y)
     if y is None:
-        y = _new_vec(x.shape[0], t, x)
-    y, py, n, iy = _vec(y, t, True); x, px, nx, ix = _vec(x, t)
-    if nx != n:
-        raise ValueError("lengths differ")
-    _check(_lib.gen9blas_copy(_kind_basic(t), n, px, ix, py, iy)); return y
+        y = _new((len(x),), t, x)
+    vy, vx = _equal_lengths(_vector(y, t, out=True), _vector(x, t))
+    _call("copy", _TYPE_CODE[t], vy.n, vx.ptr, vx.inc, vy.ptr, vy.inc)
+    return y
 
 
 def swap(x, y):
-    _init(); t = _dtype_of(x); x, px, n, ix = _vec(x, t, True); y, py, ny, iy = _vec(y, t, True)
-    if ny != n:
-        raise ValueError("lengths differ")
-    _check(_lib.gen9blas_swap(_kind_basic(t), n, px, ix, py, iy)); return x, y
+    """Exchanges x and y in place; returns (x, y)."""
+    return _two_in_place("swap", x, y)
 
 
 def rot(x, y, c, s):
-    """x, y = c·x + s·y, c·y − s·x (in place)."""
-    _init(); t = _dtype_of(x); x, px, n, ix = _vec(x, t, True); y, py, ny, iy = _vec(y, t, True)
-    if ny != n:
-        raise ValueError("lengths differ")
-    _check(_lib.gen9blas_rot(_kind_basic(t), n, px, ix, py, iy, c, s)); return x, y
-
-
-def dot(x, y):
-    _init(); t = _dtype_of(x); x, px, n, ix = _vec(x, t); y, py, ny, iy = _vec(y, t)
-    if ny != n:
-        raise ValueError("lengths differ")
-    w = _d(); _check(_lib.gen9blas_dot(_kind_basic(t), n, px, ix, py, iy, ctypes.byref(w))); return w.value
-
-
-def asum(x):
-    _init(); t = _dtype_of(x); x, px, n, ix = _vec(x, t)
-    w = _d(); _check(_lib.gen9blas_asum(_kind_basic(t), n, px, ix, ctypes.byref(w))); return w.value
-
-
-def nrm2(x):
-    _init(); t = _dtype_of(x); x, px, n, ix = _vec(x, t)
-    w = _d(); _check(_lib.gen9blas_nrm2(_kind_basic(t), n, px, ix, ctypes.byref(w))); return w.value
-
-
-def iamax(x):
-    """Index (0-based) of the first largest |x|; -1 for an empty vector."""
-    _init(); t = _dtype_of(x); x, px, n, ix = _vec(x, t)
-    w = _l(); _check(_lib.gen9blas_iamax(_kind_basic(t), n, px, ix, ctypes.byref(w))); return w.value
-
-
-def gemv(A, x, alpha=1.0, beta=0.0, y=None, trans=False):
-    """y = alpha·op(A)·x + beta·y; without y: a new array. An A.T view is passed as trans."""
-    _init(); t = _dtype_of(A); A, pa, M, N, lda, tr = _mat(A, t); tr ^= int(trans)
-    x, px, nx, ix = _vec(x, t)
-    ny = N if tr else M
-    if nx != (M if tr else N):
-        raise ValueError("length of x does not match A")
-    if y is None:
-        y, beta = _new_vec(ny, t, A), 0.0
-    y, py, n, iy = _vec(y, t, True)
-    if n != ny:
-        raise ValueError("length of y does not match A")
-    _check(_lib.gen9blas_gemv(_kind_basic(t), tr, M, N, alpha, pa, lda, px, ix, beta, py, iy)); return y
-
-
-def ger(alpha, x, y, A):
-    """A = alpha·x·yᵀ + A (in place); returns A."""
-    _init(); t = _dtype_of(A); A, pa, M, N, lda, _ = _mat(A, t, True)
-    x, px, nx, ix = _vec(x, t); y, py, ny, iy = _vec(y, t)
-    if nx != M or ny != N:
-        raise ValueError("lengths of x, y do not match A")
-    _check(_lib.gen9blas_ger(_kind_basic(t), M, N, alpha, px, ix, py, iy, pa, lda)); return A
-
-
-# ---------------- level 2 on symmetric, triangular, banded and packed matrices ----------------
-# Full storage: a square matrix of which the `uplo` triangle is used (an A.T view passes as the other triangle, no
-# copy). Band: a row-major array (rows, KL+KU+1) with A[i, j] in row i, column KL + j − i (symmetric / triangular:
-# lower KL = K, KU = 0; upper KL = 0, KU = K). Packed: a contiguous vector of n(n+1)/2 elements holding the rows of
-# the triangle (upper: j = i..n−1, lower: j = 0..i). (reference: lib/gen9blas.py:424-610)
-for _name, _types in {
-        "gen9blas_symv": [_i, _i, _i, _d, _p, _i, _p, _i, _d, _p, _i], "gen9blas_trmv": [_i] * 5 + [_p, _i, _p, _i],
-        "gen9blas_trsv": [_i] * 5 + [_p, _i, _p, _i], "gen9blas_syr": [_i, _i, _i, _d, _p, _i, _p, _i],
-        "gen9blas_syr2": [_i, _i, _i, _d, _p, _i, _p, _i, _p, _i],
-        "gen9blas_gbmv": [_i] * 6 + [_d, _p, _i, _p, _i, _d, _p, _i], "gen9blas_sbmv": [_i] * 4 + [_d, _p, _i, _p, _i, _d, _p, _i],
-        "gen9blas_tbmv": [_i] * 6 + [_p, _i, _p, _i], "gen9blas_tbsv": [_i] * 6 + [_p, _i, _p, _i],
-        "gen9blas_spmv": [_i] * 3 + [_d, _p, _p, _i, _d, _p, _i], "gen9blas_tpmv": [_i] * 5 + [_p, _p, _i],
-        "gen9blas_tpsv": [_i] * 5 + [_p, _p, _i], "gen9blas_spr": [_i] * 3 + [_d, _p, _i, _p],
-        "gen9blas_spr2": [_i] * 3 + [_d, _p, _i, _p, _i, _p],
-        "gen9blas_rotm": [_i, _i, _p, _i, _p, _i, ctypes.POINTER(_d)]}.items():
-    getattr(_lib, _name).argtypes = _types
-_fptr = ctypes.POINTER(_f)
-_lib.gen9blas_rotg.argtypes = [_fptr] * 4
-_lib.gen9blas_rotmg.argtypes = [_fptr, _fptr, _fptr, _f, _fptr]
-
-
-def _sq(A, t, uplo):
-    """(array, pointer, n, ld, transposed, triangle in memory) of a square matrix; a transposed view swaps uplo."""
-    A, pa, r, c, lda, tr = _mat(A, t)
-    if r != c:
-        raise ValueError("expected a square matrix")
-    return A, pa, r, lda, tr, ({"L": "U", "U": "L"}[uplo] if tr else uplo)
-
-
-def _y_for(y, n, t, like):
-    """(y, pointer, inc, beta applies) for an output vector of length n: a new one when y is None."""
-    if y is None:
-        y = _new_vec(n, t, like)
-        y, py, _, iy = _vec(y, t, True)
-        return y, py, iy, False
-    y, py, ny, iy = _vec(y, t, True)
-    if ny != n:
-        raise ValueError("length of y does not match A")
-    return y, py, iy, True
-
-
-def symv(A, x, uplo="L", alpha=1.0, beta=0.0, y=None):
-    """y = alpha·A·x + beta·y, A symmetric from its `uplo` triangle; without y: a new vector."""
-    _init(); t = _dtype_of(A); A, pa, n, lda, _, u = _sq(A, t, uplo)
-    x, px, nx, ix = _vec(x, t)
-    if nx != n:
-        raise ValueError("length of x does not match A")
-    y, py, iy, given = _y_for(y, n, t, x)
-    _check(_lib.gen9blas_symv(_kind_basic(t), _TRI[u], n, alpha, pa, lda, px, ix, beta if given else 0.0, py, iy))
-    return y
-
-
-def trmv(A, x, uplo="L", trans=False, diag=False):
-    """x = op(A)·x in place, A triangular (`uplo`; diag=True: unit diagonal). Returns x."""
-    _init(); t = _dtype_of(x); A, pa, n, lda, tr, u = _sq(A, t, uplo)
-    x, px, nx, ix = _vec(x, t, True)
-    if nx != n:
-        raise ValueError("length of x does not match A")
-    _check(_lib.gen9blas_trmv(_kind_basic(t), _TRI[u], int(trans) ^ tr, int(diag), n, pa, lda, px, ix)); return x
-
-
-def trsv(A, x, uplo="L", trans=False, diag=False):
-    """Solves op(A)·z = x and stores z in x, A triangular. Returns x."""
-    _init(); t = _dtype_of(x); A, pa, n, lda, tr, u = _sq(A, t, uplo)
-    x, px, nx, ix = _vec(x, t, True)
-    if nx != n:
-        raise ValueError("length of x does not match A")
-    _check(_lib.gen9blas_trsv(_kind_basic(t), _TRI[u], int(trans) ^ tr, int(diag), n, pa, lda, px, ix)); return x
-
-
-def syr(alpha, x, A, uplo="L"):
-    """A = alpha·x·xᵀ + A on the `uplo` triangle (in place). Returns A."""
-    _init(); t = _dtype_of(A); A, pa, M, N, lda, _ = _mat(A, t, True)
-    x, px, n, ix = _vec(x, t)
-    if not M == N == n:
-        raise ValueError("dimensions do not match")
-    _check(_lib.gen9blas_syr(_kind_basic(t), _TRI[uplo], n, alpha, px, ix, pa, lda)); return A
-
-
-def syr2(alpha, x, y, A, uplo="L"):
-    """A = alpha·(x·yᵀ + y·xᵀ) + A on the `uplo` triangle (in place). Returns A."""
-    _init(); t = _dtype_of(A); A, pa, M, N, lda, _ = _mat(A, t, True)
-    x, px, n, ix = _vec(x, t); y, py, ny, iy = _vec(y, t)
-    if not M == N == n == ny:
-        raise ValueError("dimensions do not match")
-    _check(_lib.gen9blas_syr2(_kind_basic(t), _TRI[uplo], n, alpha, px, ix, py, iy, pa, lda)); return A
-
-
-def _band(A, t, width, write=False):
-    A, pa, rows, w, lda, tr = _mat(A, t, write)
-    if tr or w != width:
-        raise ValueError(f"band: expected a row-major array with {width} columns")
-    return A, pa, rows, lda
-
-
-def _packed(Ap, t, n, write=False):
-    Ap, pp, m, inc = _vec(Ap, t, write)
-    if inc != 1 or m != n * (n + 1) // 2:
-        raise ValueError(f"packed: expected a contiguous vector of length {n * (n + 1) // 2}")
-    return Ap, pp
-
-
-def gbmv(A, x, M, N, KL, KU, alpha=1.0, beta=0.0, y=None, trans=False):
-    """y = alpha·op(A)·x + beta·y, A an M×N band matrix stored as an (M, KL+KU+1) array."""
-    _init(); t = _dtype_of(A); A, pa, m, lda = _band(A, t, KL + KU + 1)
-    if m != M:
-        raise ValueError("number of band rows != M")
-    x, px, nx, ix = _vec(x, t)
-    if nx != (M if trans else N):
-        raise ValueError("length of x")
-    y, py, iy, given = _y_for(y, N if trans else M, t, x)
-    _check(_lib.gen9blas_gbmv(_kind_basic(t), int(trans), M, N, KL, KU, alpha, pa, lda, px, ix, beta if given else 0.0,
-                              py, iy))
-    return y
-
-
-def sbmv(A, x, K, uplo="L", alpha=1.0, beta=0.0, y=None):
-    """y = alpha·A·x + beta·y, A symmetric band (array (n, K+1), triangle `uplo`)."""
-    _init(); t = _dtype_of(A); A, pa, n, lda = _band(A, t, K + 1)
-    x, px, nx, ix = _vec(x, t)
-    if nx != n:
-        raise ValueError("length of x")
-    y, py, iy, given = _y_for(y, n, t, x)
-    _check(_lib.gen9blas_sbmv(_kind_basic(t), _TRI[uplo], n, K, alpha, pa, lda, px, ix, beta if given else 0.0, py, iy))
-    return y
-
-
-def tbmv(A, x, K, uplo="L", trans=False, diag=False):
-    """x = op(A)·x in place, A triangular band (array (n, K+1))."""
-    _init(); t = _dtype_of(x); A, pa, n, lda = _band(A, t, K + 1); x, px, nx, ix = _vec(x, t, True)
-    if nx != n:
-        raise ValueError("length of x")
-    _check(_lib.gen9blas_tbmv(_kind_basic(t), _TRI[uplo], int(trans), int(diag), n, K, pa, lda, px, ix)); return x
-
-
-def tbsv(A, x, K, uplo="L", trans=False, diag=False):
-    """Solves op(A)·z = x in place, A triangular band (array (n, K+1))."""
-    _init(); t = _dtype_of(x); A, pa, n, lda = _band(A, t, K + 1); x, px, nx, ix = _vec(x, t, True)
-    if nx != n:
-        raise ValueError("length of x")
-    _check(_lib.gen9blas_tbsv(_kind_basic(t), _TRI[uplo], int(trans), int(diag), n, K, pa, lda, px, ix)); return x
-
-
-def spmv(Ap, x, uplo="L", alpha=1.0, beta=0.0, y=None):
-    """y = alpha·A·x + beta·y, A symmetric packed (vector of n(n+1)/2)."""
-    _init(); t = _dtype_of(Ap); x, px, n, ix = _vec(x, t); Ap, pp = _packed(Ap, t, n)
-    y, py, iy, given = _y_for(y, n, t, x)
-    _check(_lib.gen9blas_spmv(_kind_basic(t), _TRI[uplo], n, alpha, pp, px, ix, beta if given else 0.0, py, iy)); return y
-
-
-def tpmv(Ap, x, uplo="L", trans=False, diag=False):
-    """x = op(A)·x in place, A triangular packed."""
-    _init(); t = _dtype_of(x); x, px, n, ix = _vec(x, t, True); Ap, pp = _packed(Ap, t, n)
-    _check(_lib.gen9blas_tpmv(_kind_basic(t), _TRI[uplo], int(trans), int(diag), n, pp, px, ix)); return x
-
-
-def tpsv(Ap, x, uplo="L", trans=False, diag=False):
-    """Solves op(A)·z = x in place, A triangular packed."""
-    _init(); t = _dtype_of(x); x, px, n, ix = _vec(x, t, True); Ap, pp = _packed(Ap, t, n)
-    _check(_lib.gen9blas_tpsv(_kind_basic(t), _TRI[uplo], int(trans), int(diag), n, pp, px, ix)); return x
-
-
-def spr(alpha, x, Ap, uplo="L"):
-    """A = alpha·x·xᵀ + A, A packed (in place). Returns Ap."""
-    _init(); t = _dtype_of(Ap); x, px, n, ix = _vec(x, t); Ap, pp = _packed(Ap, t, n, True)
-    _check(_lib.gen9blas_spr(_kind_basic(t), _TRI[uplo], n, alpha, px, ix, pp)); return Ap
-
-
-def spr2(alpha, x, y, Ap, uplo="L"):
-    """A = alpha·(x·yᵀ + y·xᵀ) + A, A packed (in place). Returns Ap."""
-    _init(); t = _dtype_of(Ap); x, px, n, ix = _vec(x, t); y, py, ny, iy = _vec(y, t)
-    if ny != n:
-        raise ValueError("lengths of x, y")
-    Ap, pp = _packed(Ap, t, n, True)
-    _check(_lib.gen9blas_spr2(_kind_basic(t), _TRI[uplo], n, alpha, px, ix, py, iy, pp)); return Ap
+    """x, y = c·x + s·y, c·y − s·x in place; returns (x, y)."""
+    return _two_in_place("rot", x, y, c, s)
 
 
 def rotm(x, y, param):
     """x, y = h11·x + h12·y, h21·x + h22·y in place; param = (flag, h11, h21, h12, h22) as in BLAS."""
-    _init(); t = _dtype_of(x); x, px, n, ix = _vec(x, t, True); y, py, ny, iy = _vec(y, t, True)
-    if ny != n:
-        raise ValueError("lengths differ")
-    pr = (_d * 5)(*[float(v) for v in param])
-    _check(_lib.gen9blas_rotm(_kind_basic(t), n, px, ix, py, iy, pr)); return x, y
+    return _two_in_place("rotm", x, y, (ctypes.c_double * 5)(*map(float, param)))
+
+
+def dot(x, y):
+    """Σ x·y as a Python float (float64 accumulation)."""
+    return _reduction("dot", ctypes.c_double, x, y)
+
+
+def asum(x):
+    """Σ |x|."""
+    return _reduction("asum", ctypes.c_double, x)
+
+
+def nrm2(x):
+    """Euclidean norm of x."""
+    return _reduction("nrm2", ctypes.c_double, x)
+
+
+def iamax(x):
+    """0-based index of the first element of largest |x|; -1 for an empty vector."""
+    return _reduction("iamax", ctypes.c_int64, x)
 
 
 def rotg(a, b):
-    """(r, z, c, s) of the Givens rotation that zeroes b (computed on the host)."""
-    w = [_f(a), _f(b), _f(), _f()]
-    _lib.gen9blas_rotg(*[ctypes.byref(v) for v in w])
-    return tuple(v.value for v in w)
+    """(r, z, c, s) of the Givens rotation that zeroes b (computed on the host, in float32)."""
+    cells = [ctypes.c_float(v) for v in (a, b, 0.0, 0.0)]
+    _lib.gen9blas_rotg(*map(ctypes.byref, cells))
+    return tuple(c.value for c in cells)
 
 
 def rotmg(d1, d2, x1, y1):
-    """(d1, d2, x1, param) of the modified Givens rotation (computed on the host); param has 5 entries."""
-    w = [_f(d1), _f(d2), _f(x1)]
-    pr = (_f * 5)()
-    _lib.gen9blas_rotmg(*[ctypes.byref(v) for v in w], _f(y1), pr)
-    return w[0].value, w[1].value, w[2].value, np.array(pr[:], np.float32)
+    """(d1, d2, x1, param) of the modified Givens rotation (host, float32); param holds 5 numbers as in BLAS."""
+    cells = [ctypes.c_float(v) for v in (d1, d2, x1)]
+    param = (ctypes.c_float * 5)()
+    _lib.gen9blas_rotmg(*map(ctypes.byref, cells), ctypes.c_float(y1), param)
+    return cells[0].value, cells[1].value, cells[2].value, np.frombuffer(param, np.float32).copy()
+
+
+# ------------------------------------------------------------------------------------------------------------------
+# Level 2 on general and full-storage matrices
+# ------------------------------------------------------------------------------------------------------------------
+
+
+def _vector_of_length(x, n, t, out=False, what="x"):
+    v = _vector(x, t, out)
+    if v.n != n:
+        raise ValueError(f"{what} has length {v.n}, the matrix needs {n}")
+    return v
+
+
+def gemv(A, x, alpha=1.0, beta=0.0, y=None, trans=False):
+    """y = alpha·op(A)·x + beta·y (op = transpose when trans); without y, a new vector. A.T passes as a flag."""
+    t = _compute_type(A)
+    a = _matrix(A, t)
+    M, N = a.stored
+    tr = a.trans ^ int(bool(trans))
+    vx = _vector_of_length(x, M if tr else N, t)
+    o = _out_vector(y, N if tr else M, t, A)
+    _call("gemv", _TYPE_CODE[t], tr, M, N, alpha, a.ptr, a.ld, vx.ptr, vx.inc, o.beta(beta), o.ptr, o.ld)
+    return o.obj
+
+
+def ger(alpha, x, y, A):
+    """A = alpha·x·yᵀ + A in place; returns A."""
+    t = _compute_type(A)
+    a = _matrix(A, t, out=True)
+    M, N = a.shape
+    vx, vy = _vector_of_length(x, M, t), _vector_of_length(y, N, t, what="y")
+    _call("ger", _TYPE_CODE[t], M, N, alpha, vx.ptr, vx.inc, vy.ptr, vy.inc, a.ptr, a.ld)
+    return A
+
+
+def symv(A, x, uplo="L", alpha=1.0, beta=0.0, y=None):
+    """y = alpha·A·x + beta·y with A symmetric from its `uplo` triangle; without y, a new vector."""
+    t = _compute_type(A)
+    a, u = _square(A, t, uplo)
+    n = a.shape[0]
+    vx = _vector_of_length(x, n, t)
+    o = _out_vector(y, n, t, x)
+    _call("symv", _TYPE_CODE[t], _UPLO_CODE[u], n, alpha, a.ptr, a.ld, vx.ptr, vx.inc, o.beta(beta), o.ptr, o.ld)
+    return o.obj
+
+
+def _triangular_vector(name, A, x, uplo, trans, diag):
+    t = _compute_type(x)
+    a, u = _square(A, t, uplo)
+    vx = _vector_of_length(x, a.shape[0], t, out=True)
+    _call(name, _TYPE_CODE[t], _UPLO_CODE[u], int(bool(trans)) ^ a.trans, int(bool(diag)), vx.n, a.ptr, a.ld, vx.ptr,
+          vx.inc)
+    return x
+
+
+def trmv(A, x, uplo="L", trans=False, diag=False):
+    """x = op(A)·x in place, A triangular (`uplo`; diag: unit diagonal); returns x."""
+    return _triangular_vector("trmv", A, x, uplo, trans, diag)
+
+
+def trsv(A, x, uplo="L", trans=False, diag=False):
+    """Overwrites x with the solution z of op(A)·z = x, A triangular; returns x."""
+    return _triangular_vector("trsv", A, x, uplo, trans, diag)
+
+
+def syr(alpha, x, A, uplo="L"):
+    """A = alpha·x·xᵀ + A on the `uplo` triangle, in place; returns A."""
+    t = _compute_type(A)
+    a = _matrix(A, t, out=True)
+    if a.shape[0] != a.shape[1]:
+        raise ValueError("expected a square matrix")
+    vx = _vector_of_length(x, a.shape[0], t)
+    _call("syr", _TYPE_CODE[t], _UPLO_CODE[uplo], vx.n, alpha, vx.ptr, vx.inc, a.ptr, a.ld)
+    return A
+
+
+def syr2(alpha, x, y, A, uplo="L"):
+    """A = alpha·(x·yᵀ + y·xᵀ) + A on the `uplo` triangle, in place; returns A."""
+    t = _compute_type(A)
+    a = _matrix(A, t, out=True)
+    if a.shape[0] != a.shape[1]:
+        raise ValueError("expected a square matrix")
+    vx, vy = _vector_of_length(x, a.shape[0], t), _vector_of_length(y, a.shape[0], t, what="y")
+    _call("syr2", _TYPE_CODE[t], _UPLO_CODE[uplo], vx.n, alpha, vx.ptr, vx.inc, vy.ptr, vy.inc, a.ptr, a.ld)
+    return A
+
+
+# ------------------------------------------------------------------------------------------------------------------
+# Level 2 on band and packed storage (row layout of CBLAS RowMajor).
+# Band: an array (rows, KL+KU+1) with A[i, j] at row i, column KL + j − i; symmetric and triangular band matrices use
+# KL = K, KU = 0 (lower) or KL = 0, KU = K (upper). Packed: a contiguous vector of n(n+1)/2 elements holding the rows
+# of the triangle one after another (upper: j = i..n−1, lower: j = 0..i). (reference lib/gen9blas.py:517-610)
+# ------------------------------------------------------------------------------------------------------------------
+
+
+def _band(A, t, width):
+    a = _matrix(A, t)
+    if a.trans or a.shape[1] != width:
+        raise ValueError(f"band storage: expected a row-major array with {width} columns")
+    return a
+
+
+def _packed(Ap, t, n, out=False):
+    v = _vector(Ap, t, out)
+    if v.inc != 1 or v.n != n * (n + 1) // 2:
+        raise ValueError(f"packed storage: expected a contiguous vector of {n * (n + 1) // 2} elements")
+    return v
+
+
+def gbmv(A, x, M, N, KL, KU, alpha=1.0, beta=0.0, y=None, trans=False):
+    """y = alpha·op(A)·x + beta·y, A an M×N band matrix with KL sub- and KU super-diagonals."""
+    t = _compute_type(A)
+    a = _band(A, t, KL + KU + 1)
+    if a.shape[0] != M:
+        raise ValueError(f"band storage has {a.shape[0]} rows, M is {M}")
+    vx = _vector_of_length(x, M if trans else N, t)
+    o = _out_vector(y, N if trans else M, t, x)
+    _call("gbmv", _TYPE_CODE[t], int(bool(trans)), M, N, KL, KU, alpha, a.ptr, a.ld, vx.ptr, vx.inc, o.beta(beta),
+          o.ptr, o.ld)
+    return o.obj
+
+
+def sbmv(A, x, K, uplo="L", alpha=1.0, beta=0.0, y=None):
+    """y = alpha·A·x + beta·y, A symmetric band (array (n, K+1) of its `uplo` triangle)."""
+    t = _compute_type(A)
+    a = _band(A, t, K + 1)
+    n = a.shape[0]
+    vx = _vector_of_length(x, n, t)
+    o = _out_vector(y, n, t, x)
+    _call("sbmv", _TYPE_CODE[t], _UPLO_CODE[uplo], n, K, alpha, a.ptr, a.ld, vx.ptr, vx.inc, o.beta(beta), o.ptr, o.ld)
+    return o.obj
+
+
+def _band_triangular(name, A, x, K, uplo, trans, diag):
+    t = _compute_type(x)
+    a = _band(A, t, K + 1)
+    vx = _vector_of_length(x, a.shape[0], t, out=True)
+    _call(name, _TYPE_CODE[t], _UPLO_CODE[uplo], int(bool(trans)), int(bool(diag)), vx.n, K, a.ptr, a.ld, vx.ptr,
+          vx.inc)
+    return x
+
+
+def tbmv(A, x, K, uplo="L", trans=False, diag=False):
+    """x = op(A)·x in place, A triangular band (array (n, K+1))."""
+    return _band_triangular("tbmv", A, x, K, uplo, trans, diag)
+
+
+def tbsv(A, x, K, uplo="L", trans=False, diag=False):
+    """Overwrites x with the solution of op(A)·z = x, A triangular band (array (n, K+1))."""
+    return _band_triangular("tbsv", A, x, K, uplo, trans, diag)
+
+
+def spmv(Ap, x, uplo="L", alpha=1.0, beta=0.0, y=None):
+    """y = alpha·A·x + beta·y, A symmetric in packed storage."""
+    t = _compute_type(Ap)
+    vx = _vector(x, t)
+    ap = _packed(Ap, t, vx.n)
+    o = _out_vector(y, vx.n, t, x)
+    _call("spmv", _TYPE_CODE[t], _UPLO_CODE[uplo], vx.n, alpha, ap.ptr, vx.ptr, vx.inc, o.beta(beta), o.ptr, o.ld)
+    return o.obj
+
+
+def _packed_triangular(name, Ap, x, uplo, trans, diag):
+    t = _compute_type(x)
+    vx = _vector(x, t, out=True)
+    ap = _packed(Ap, t, vx.n)
+    _call(name, _TYPE_CODE[t], _UPLO_CODE[uplo], int(bool(trans)), int(bool(diag)), vx.n, ap.ptr, vx.ptr, vx.inc)
+    return x
+
+
+def tpmv(Ap, x, uplo="L", trans=False, diag=False):
+    """x = op(A)·x in place, A triangular in packed storage."""
+    return _packed_triangular("tpmv", Ap, x, uplo, trans, diag)
+
+
+def tpsv(Ap, x, uplo="L", trans=False, diag=False):
+    """Overwrites x with the solution of op(A)·z = x, A triangular in packed storage."""
+    return _packed_triangular("tpsv", Ap, x, uplo, trans, diag)
+
+
+def spr(alpha, x, Ap, uplo="L"):
+    """A = alpha·x·xᵀ + A in packed storage, in place; returns Ap."""
+    t = _compute_type(Ap)
+    vx = _vector(x, t)
+    ap = _packed(Ap, t, vx.n, out=True)
+    _call("spr", _TYPE_CODE[t], _UPLO_CODE[uplo], vx.n, alpha, vx.ptr, vx.inc, ap.ptr)
+    return Ap
+
+
+def spr2(alpha, x, y, Ap, uplo="L"):
+    """A = alpha·(x·yᵀ + y·xᵀ) + A in packed storage, in place; returns Ap."""
+    t = _compute_type(Ap)
+    vx, vy = _equal_lengths(_vector(x, t), _vector(y, t))
+    ap = _packed(Ap, t, vx.n, out=True)
+    _call("spr2", _TYPE_CODE[t], _UPLO_CODE[uplo], vx.n, alpha, vx.ptr, vx.inc, vy.ptr, vy.inc, ap.ptr)
+    return Ap
