@@ -61,6 +61,10 @@ struct Operand {
 // (copy_in: with the data; otherwise the buffer contents are undefined, as for outputs not read, except the gaps of
 // a written operand, which are copied in so the copy back preserves them).
 G9_HIDDEN int resolve(Operand &op, int slot, bool copy_in, bool written, bool repitch);
+// Where p .. p+bytes lies: host memory (pageable or pinned, or NULL), inside one device (or managed) allocation, or in
+// device memory but running past the end of its allocation (an ld or increment too large for the buffer).
+enum { MEM_HOST = 0, MEM_DEVICE = 1, MEM_DEVICE_OVERRUN = 2 };
+G9_HIDDEN int mem_kind(const void *p, size_t bytes);
 // 1 if p .. p+bytes lies in one device allocation.
 G9_HIDDEN int is_device(const void *p, size_t bytes);
 // End of a call: in no-wait mode with every operand in place, returns at once; otherwise waits for the stream and

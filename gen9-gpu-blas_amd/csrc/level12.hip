@@ -61,11 +61,13 @@ static int reduction(int type, int mode, int n, const void *x, int incx, const v
     int es;
     const int ok = l12_es(type, &es);
     // a host result is 0 until the sum is known, as in the reference (reference: lib/src/level12.c:172)
-    if (result && (ok == GEN9BLAS_ERR_NO_DEVICE || !is_device(result, sizeof(double)))) *result = 0;
+    const int rkind = ok == GEN9BLAS_ERR_NO_DEVICE ? MEM_HOST : mem_kind(result, sizeof(double));
+    if (result && rkind == MEM_HOST) *result = 0;
     G9_TRY(ok);
     if (n <= 0) return 0;
     if (!incx || (mode == 0 && !incy)) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "vector increment 0");
     if (!result) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "NULL result pointer");
+    if (rkind == MEM_DEVICE_OVERRUN) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "result pointer runs past its device allocation");
     Operand o[2];
     vec(o[0], x, n, incx, es);
     G9_TRY(resolve(o[0], SLOT_A, true, false, false));
@@ -77,7 +79,7 @@ static int reduction(int type, int mode, int n, const void *x, int incx, const v
     }
     // A result pointer in device memory receives the sum in place (no wait in no-wait mode); a host pointer is
     // filled after the wait.
-    const bool dev_result = is_device(result, sizeof(double));
+    const bool dev_result = rkind == MEM_DEVICE;
     void *res = result;
     if (!dev_result) G9_TRY(scratch(SLOT_Q, 64, &res));
     prof_begin();

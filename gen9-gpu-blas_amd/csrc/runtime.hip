@@ -138,22 +138,25 @@ int scratch(int slot, size_t bytes, void **p) {
 }
 
 // ---------------- operand resolution ----------------
-int is_device(const void *p, size_t bytes) {
-    if (!p) return 0;
+int mem_kind(const void *p, size_t bytes) {
+    if (!p) return MEM_HOST;
     hipPointerAttribute_t a;
     if (hipPointerGetAttributes(&a, p) != hipSuccess) {
         (void)hipGetLastError();   // plain host memory: the query fails, clear the error
-        return 0;
+        return MEM_HOST;
     }
-    if (a.type != hipMemoryTypeDevice && a.type != hipMemoryTypeManaged && a.type != hipMemoryTypeUnified) return 0;
+    if (a.type != hipMemoryTypeDevice && a.type != hipMemoryTypeManaged && a.type != hipMemoryTypeUnified)
+        return MEM_HOST;
     hipDeviceptr_t base = nullptr;
     size_t size = 0;
     if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) != hipSuccess) {
         (void)hipGetLastError();
-        return 1;   // device memory whose extent the runtime does not report: trust the caller
+        return MEM_DEVICE;   // device memory whose extent the runtime does not report: trust the caller
     }
-    return (uintptr_t)p + bytes <= (uintptr_t)base + size;
+    return (uintptr_t)p + bytes <= (uintptr_t)base + size ? MEM_DEVICE : MEM_DEVICE_OVERRUN;
 }
+
+int is_device(const void *p, size_t bytes) { return mem_kind(p, bytes) == MEM_DEVICE; }
 
 // ---------------- staged copies between pageable host memory and the device ----------------
 // From pageable memory hipMemcpy reaches about 30 GB/s to the device and 18 GB/s back on an MI355X host, against
@@ -321,7 +324,11 @@ int resolve(Operand &op, int slot, bool copy_in, bool written, bool repitch) {
     const size_t es = op.es;
     const size_t span = ((size_t)(op.rows - 1) * (size_t)op.caller_ld + (size_t)op.cols) * es;
     op.written = written;
-    if (is_device(op.host, span)) {
+    const int kind = mem_kind(op.host, span);
+    if (kind == MEM_DEVICE_OVERRUN)
+        G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "an operand of %zu bytes (with its leading dimension or increment) runs past "
+                "the end of its device allocation", span);
+    if (kind == MEM_DEVICE) {
         op.dev = const_cast<void *>(op.host);
         op.ld = op.caller_ld;
         op.zc = true;

@@ -20,7 +20,9 @@ allocated on the same device. empty() hands out pinned host memory (gen9blas_all
 import atexit
 import collections
 import ctypes
+import importlib.util
 import os
+import sys
 from typing import NamedTuple
 
 import numpy as np
@@ -39,6 +41,23 @@ def _library_path():
     return local if os.path.exists(local) else "libgen9blas.so"
 
 
+def _share_torch_hip_runtime():
+    """torch ships its own HIP runtime (torch/lib/libamdhip64.so, soname libamdhip64.so.7, RPATH $ORIGIN) and its
+    libraries ask for it by the unversioned name. libgen9blas.so asks for libamdhip64.so.7, so when it is loaded
+    before torch the process ends up with two HIP (and HSA) runtimes, and the second to initialize finds no device.
+    Loading torch's runtime first makes libgen9blas.so bind to it by soname, and torch later reuses the same file:
+    one runtime in either import order. Without torch installed, the system runtime is used."""
+    if "torch" in sys.modules:
+        return                                   # torch's runtime is loaded already; the soname binds to it
+    spec = importlib.util.find_spec("torch")
+    if spec is None or not spec.submodule_search_locations:
+        return
+    runtime = os.path.join(list(spec.submodule_search_locations)[0], "lib", "libamdhip64.so")
+    if os.path.exists(runtime):
+        ctypes.CDLL(runtime, mode=ctypes.RTLD_GLOBAL)
+
+
+_share_torch_hip_runtime()
 _lib = ctypes.CDLL(_library_path())
 
 # One letter per C type. Upper case letters are pointers to the lower case scalar.

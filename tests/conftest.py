@@ -9,6 +9,13 @@ import sys
 import numpy as np
 import pytest
 
+try:
+    # torch's HIP runtime first: libgen9blas.so, loaded later by any test, then binds to the same runtime (two HIP
+    # runtimes in one process leave the second without a device)
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 ROOT = os.path.dirname(os.path.dirname(os.path.realpath(__file__)))
 PKG = os.path.join(ROOT, "gen9-gpu-blas_amd")
 for p in (PKG, os.path.join(ROOT, "oracle"), ROOT):

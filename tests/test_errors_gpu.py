@@ -81,3 +81,30 @@ def test_level23_type_check_and_host_operands(L):
     assert b"type 9" in L.gen9blas_error()
     assert L.gen9blas_symm(9, 0, 0, 8, 8, d(1.0), a.ctypes.data, 8, a.ctypes.data, 8, d(0.0), a.ctypes.data, 8) == UNSUPPORTED
     assert b"type 9" in L.gen9blas_error()
+
+
+def test_device_operand_past_its_allocation(L):
+    """A device operand whose span (rows × ld) runs past the end of its allocation gives INVALID_ARG: it is neither
+    used in place (a kernel would read past the buffer) nor taken for host memory (host threads would copy from a
+    device address). The gemm call is made only after gen9blas_is_device has classified the span: device memory
+    (in range for the buffer's own size) whose requested span lies outside the allocation."""
+    n = 64
+    nbytes = n * n * 4
+    bufs = [L.gen9blas_device_alloc(nbytes) for _ in range(3)]
+    try:
+        assert all(bufs)
+        zeros = np.zeros(n * n, np.float32)
+        for p in bufs:
+            assert L.gen9blas_memcpy(p, zeros.ctypes.data, nbytes) == OK
+        A, B, C = bufs
+        big_ld = 1 << 20
+        span = ((n - 1) * big_ld + n) * 4
+        assert L.gen9blas_is_device(A, nbytes) == 1
+        assert L.gen9blas_is_device(A, span) == 0
+        assert L.gen9blas_gemm(1, 0, 0, n, n, n, 1.0, A, big_ld, B, n, 0.0, C, n) == INVALID
+        assert L.gen9blas_last_status() == INVALID and b"allocation" in L.gen9blas_error()
+        assert L.gen9blas_gemm(1, 0, 0, n, n, n, 1.0, A, n, B, n, 0.0, C, n) == OK
+    finally:
+        for p in bufs:
+            if p:
+                L.gen9blas_device_free(p)

@@ -116,13 +116,15 @@ def test_gemm_config_sizes(g9, orc, torch_dev, kind, n):
     assert np.isfinite(W).all()
 
 
+@pytest.mark.parametrize("K", [1000, 1024])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
-def test_sgemm_two_group_tiles(g9, orc, torch_dev, ta, tb):
+def test_sgemm_two_group_tiles(g9, orc, torch_dev, ta, tb, K):
     """FP32 products whose 128×128 tiles fill whole rounds of CUs take 128×128 tiles with two k groups: 2000×2048
-    (256 tiles, edge tiles in m) with K = 1000 (not a multiple of the groups' 64-k step, so the second group's last
-    block tile is partly past K), alpha = 1.5, beta = 0.5, every layout, against float64 on sampled rows."""
+    (256 tiles, edge tiles in m), alpha = 1.5, beta = 0.5, every layout, against float64 on sampled rows. K = 1000 is
+    not a multiple of the groups' 64-k step, so the second group's last block tile is partly past K and every tile
+    takes the checked loop; with K = 1024 the interior tiles take the unchecked fast loop in every layout."""
     torch = torch_dev
-    M, N, K = 2000, 2048, 1000
+    M, N = 2000, 2048
     a = orc.uniform((K, M) if ta else (M, K), np.float32, orc.SEED_A)
     b = orc.uniform((N, K) if tb else (K, N), np.float32, orc.SEED_B)
     c0 = orc.uniform((M, N), np.float32, 3)
@@ -131,8 +133,8 @@ def test_sgemm_two_group_tiles(g9, orc, torch_dev, ta, tb):
     opA = a.T if ta else a
     rows = np.unique(np.r_[0, M - 1, np.random.default_rng(6).integers(0, M, 62)])
     mean, mx = _sampled_rows_error(W, opA, b, rows, 1.5, 0.5, c0, tB=bool(tb))
-    assert mx <= MAX_E["S"], f"tA={ta} tB={tb}: max e {mx:.2e}"
-    assert mean <= MEAN_E["S"], f"tA={ta} tB={tb}: mean e {mean:.2e}"
+    assert mx <= MAX_E["S"], f"tA={ta} tB={tb} K={K}: max e {mx:.2e}"
+    assert mean <= MEAN_E["S"], f"tA={ta} tB={tb} K={K}: mean e {mean:.2e}"
 
 
 def test_sgemm_odd_shape(g9, orc, torch_dev):
@@ -285,40 +287,57 @@ def test_hgemm_whole_tile_kernel(g9, torch_dev, M, N, K, count):
                     assert e.max() <= 2e-3, f"{tag}: max e {e.max():.2e}"
 
 
-def test_banded_launch(tmp_path):
-    """GEN9BLAS_MAX_LAUNCH_MS splits a long product into row bands, each its own launch (reference:
-    lib/src/gemm.c:119-164): results equal the unbanded call's (with GEN9BLAS_SPLITK=0: split-K slices and the
-    two-k-group tiles are picked from the shape, so a band may sum in another order). The variable is read once per process, so the banded call runs in a child
-    process (one extra GPU process, sequential)."""
+def _child(args, extra_env, timeout):
+    """Runs tests/long_launch_child.py in a child process with the given variables (read once per process)."""
     import os
     import subprocess
     import sys
-    script = tmp_path / "banded.py"
-    script.write_text(
-        "import sys, numpy as np\n"
-        f"sys.path.insert(0, {os.path.join(os.path.dirname(os.path.dirname(os.path.realpath(__file__))), 'gen9-gpu-blas_amd')!r})\n"
-        "import gen9blas as g\n"
-        "rng = np.random.default_rng(4)\n"
-        "for dt in (np.float32, np.float64, np.float16):\n"
-        "    a = rng.uniform(-1, 1, (1100, 700)).astype(dt); b = rng.uniform(-1, 1, (700, 900)).astype(dt)\n"
-        "    c0 = rng.uniform(-1, 1, (1100, 900)).astype(dt)\n"
-        "    c = g.gemm(a, b, 1.5, 0.5, c0.copy())\n"
-        "    np.save(sys.argv[1] + '_' + np.dtype(dt).name + '.npy', c)\n")
-    outs = {}
-    for band in ("", "0.0001"):
-        env = dict(os.environ)
-        env.pop("GEN9BLAS_MAX_LAUNCH_MS", None)
-        env["GEN9BLAS_SPLITK"] = "0"   # a band's split-K choice differs from the whole product's (other rounding)
-        if band:
-            env["GEN9BLAS_MAX_LAUNCH_MS"] = band
-        prefix = str(tmp_path / ("banded" if band else "plain"))
-        r = subprocess.run([sys.executable, str(script), prefix], env=env, capture_output=True, text=True, timeout=100)
-        assert r.returncode == 0, r.stderr[-2000:]
-        outs[band] = prefix
-    for dt in ("float32", "float64", "float16"):
-        plain = np.load(outs[""] + "_" + dt + ".npy")
-        banded = np.load(outs["0.0001"] + "_" + dt + ".npy")
-        assert np.array_equal(plain, banded), dt   # bands compute the same per-element sums in the same order
+    env = dict(os.environ)
+    for v in ("GEN9BLAS_MAX_LAUNCH_MS", "GEN9BLAS_SPLITK"):
+        env.pop(v, None)
+    env.update(extra_env)
+    child = os.path.join(os.path.dirname(os.path.realpath(__file__)), "long_launch_child.py")
+    r = subprocess.run([sys.executable, "-u", child, *args], env=env, capture_output=True, text=True, timeout=timeout)
+    print(r.stdout[-2000:])
+    assert r.returncode == 0, (r.stdout[-2000:], r.stderr[-2000:])
+
+
+def test_banded_launch(g9, tmp_path):
+    """GEN9BLAS_MAX_LAUNCH_MS splits a long product into row bands, each its own launch (reference:
+    lib/src/gemm.c:119-164). Every type, A plain and transposed (a band of op(A) is a column range of the stored
+    matrix), and a strided batch of 3 with both operands transposed (bands inside every matrix of the batch):
+    - the banded result meets the reference bounds against float64 (full matrices, the reference metric);
+    - it equals the unbanded call's result bit for bit (GEN9BLAS_SPLITK=0 in both runs: otherwise split-K slices and
+      two-k-group tiles are picked from each band's shape and may sum in another order)."""
+    import numpy as np
+    plain, banded = tmp_path / "plain.npz", tmp_path / "banded.npz"
+    _child(["layouts", str(plain)], {"GEN9BLAS_SPLITK": "0"}, 100)
+    _child(["layouts", str(banded)], {"GEN9BLAS_SPLITK": "0", "GEN9BLAS_MAX_LAUNCH_MS": "0.0001"}, 100)
+    P, B = np.load(plain), np.load(banded)
+    for kind in ("S", "D", "H", "HS"):
+        for case in ("tA0", "tA1", "batch"):
+            key = f"{kind}_{case}"
+            bound = case_bounds(kind, 700)[1]
+            assert float(B[key + "_err"]) <= bound, f"banded {key}: max e {float(B[key + '_err']):.2e}"
+            assert float(P[key + "_err"]) <= bound, f"plain {key}: max e {float(P[key + '_err']):.2e}"
+            assert np.array_equal(P[key], B[key]), f"{key}: banded result differs from the unbanded one"
+
+
+@pytest.mark.parametrize("banded", [False, True])
+def test_long_launch_cases(g9, tmp_path, banded):
+    """The reference's long-launch sizes (reference: lib/test_long_launch.py:39-51): DGEMM n = 4096, SGEMM n = 8192,
+    accurate HGEMM n = 8192 and batched DGEMM 2 × 3072, U(0, 1) inputs in pinned host memory, checked against
+    float64 on sampled rows (first, middle, last, and both sides of every 256-row band boundary) with the reference's
+    bounds 1e-12 / 1e-4 / 5e-3 / 1e-12 (relative to |ref|; all products are positive, so this is also the reference
+    GEMM metric). Unbanded, and with GEN9BLAS_MAX_LAUNCH_MS = 1 (6-16 bands per product)."""
+    import json
+    out = tmp_path / "long.json"
+    _child(["cases", str(out)], {"GEN9BLAS_MAX_LAUNCH_MS": "1"} if banded else {}, 110)
+    res = json.loads(out.read_text())
+    bounds = {"dgemm n=4096": 1e-12, "sgemm n=8192": 1e-4, "hgemm accurate n=8192": 5e-3,
+              "batched dgemm 2 x 3072": 1e-12}
+    for name, bound in bounds.items():
+        assert res[name] <= bound, f"{name} banded={banded}: max rel err {res[name]:.2e}"
 
 
 def test_gemm_split_k(tmp_path):

@@ -121,3 +121,20 @@ def test_skinny_matrix_core_kernel(g9, torch_dev, M, N, K):
     mask = np.ones(big.shape, bool)
     mask[2:M + 2, 1:N + 1] = False
     assert np.array_equal(big[mask], D0[mask]), "write outside the C slice"
+
+
+def test_skinny_forced_threshold(g9):
+    """GEN9BLAS_SKINNY=64, as the reference's skinny test forces it (reference: lib/test_skinny.py:14, 43-44): every
+    product with min(M, N) ≤ 64 takes a skinny kernel, so M = 17, 33, 64 (and the role-swapped small N) run in M
+    tiles of 16 rows (grid.y > 1), on both the dot-product kernel and, for K a multiple of 256, the FP16 matrix-core
+    kernel. All of the reference test's cases against float64 (tests/skinny_forced_child.py). The variable is read
+    once per process, so the cases run in a child process (one more GPU process, sequential)."""
+    import os
+    import subprocess
+    import sys
+    env = dict(os.environ, GEN9BLAS_SKINNY="64")
+    child = os.path.join(os.path.dirname(os.path.realpath(__file__)), "skinny_forced_child.py")
+    r = subprocess.run([sys.executable, "-u", child], env=env, capture_output=True, text=True, timeout=110)
+    print(r.stdout[-3000:])
+    assert r.returncode == 0, (r.stdout[-3000:], r.stderr[-2000:])
+    assert "failed 0" in r.stdout
