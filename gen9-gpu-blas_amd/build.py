@@ -26,7 +26,7 @@ HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC", "-fvisibilit
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wall", "-Wno-unused-function"]
 HIP_SOURCES = ["runtime.hip", "gemm.hip", "gemm_kernels.hip", "skinny.hip", "level12.hip", "level12_kernels.hip",
-               "packed.hip", "level3.hip", "level2.hip"]
+               "packed.hip", "level3.hip", "level2.hip", "noalloc.hip"]
 HEADERS = ["internal.h", "skinny_kernel.h", "gemm_kernel.h", "hgemm_kernel.h", "lds_dma.h", "wave.h"]
 
 

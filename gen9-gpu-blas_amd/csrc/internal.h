@@ -42,6 +42,13 @@ enum Slot { SLOT_A = 0, SLOT_B, SLOT_C, SLOT_P, SLOT_Q, SLOT_T, SLOT_X, SLOT_Y, 
 // Device scratch owned by the library, grown on demand and kept between calls (the reference's work buffers,
 // reference: lib/src/core.c:272-277). Growing waits for queued work first.
 G9_HIDDEN int scratch(int slot, size_t bytes, void **p);
+// While a fixed work space is set (base != nullptr), scratch() allocates nothing: the split-K slices (SLOT_P) are
+// placed at `base` if they fit in `bytes`, and every other request (staging of host operands, other work buffers)
+// fails with INVALID_ARG. set_fixed_workspace(nullptr, 0) returns to the growing buffers.
+G9_HIDDEN void set_fixed_workspace(void *base, size_t bytes, const char *who);
+// Set-up of the no-allocation entry point on `dev` (called by init with `dev` current): finds the device address of
+// its static work space. A failure is kept and reported by that entry point only.
+G9_HIDDEN void noalloc_setup(int dev);
 
 // A vector or matrix operand. Matrices are described as rows × cols elements with row stride ld; vectors as
 // rows = 1, cols = span (elements from the lowest address), ld = cols.

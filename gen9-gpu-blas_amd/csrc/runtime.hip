@@ -82,6 +82,7 @@ static int init_impl() {
         G9_FAIL(GEN9BLAS_ERR_NO_DEVICE, "device %d is %s; this build has gfx950 kernels only", d, p.gcnArchName);
     if (hipSetDevice(d) != hipSuccess) G9_FAIL(GEN9BLAS_ERR_NO_DEVICE, "hipSetDevice(%d) failed", d);
     device = d;
+    noalloc_setup(d);
     arch = 950;
     num_cus = p.multiProcessorCount;
     // Default flags and default priority: the stream orders itself with the legacy null stream.
@@ -115,7 +116,27 @@ int begin() {
 static void *sbuf[NSLOTS];
 static size_t ssize[NSLOTS];
 
+static void *fixed_base;
+static size_t fixed_bytes;
+static const char *fixed_who;
+
+void set_fixed_workspace(void *base, size_t bytes, const char *who) {
+    fixed_base = base;
+    fixed_bytes = base ? bytes : 0;
+    fixed_who = who;
+}
+
 int scratch(int slot, size_t bytes, void **p) {
+    if (fixed_base) {
+        if (slot != SLOT_P)
+            G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "%s takes device operands only: an operand in host memory would need a "
+                    "staging buffer", fixed_who);
+        if (bytes > fixed_bytes)
+            G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "%s: this product needs %zu bytes of split-K work space, more than its "
+                    "fixed maximum of %zu", fixed_who, bytes, fixed_bytes);
+        *p = fixed_base;
+        return 0;
+    }
     if (bytes == 0) bytes = 256;
     if (ssize[slot] < bytes) {
         if (sbuf[slot]) {

@@ -60,7 +60,8 @@ def test_header_declares_the_reference_surface():
               "gen9blas_last_zero_copy", "gen9blas_alloc", "gen9blas_free", "gen9blas_is_usm"):
         assert f in names, f
     assert "gen9blas_gemm_pb_skinny" in names   # the packed-weight decode entry of the reference's ML header
-    assert len(names) == 60
+    assert "gen9blas_gemm_noalloc" in names     # MI355X addition: gen9blas_gemm without allocations
+    assert len(names) == 61
 
 
 def test_exports_exactly_the_header(lib):
