@@ -1,13 +1,16 @@
 """Benchmark of the gen9blas hot path on one MI355X: SGEMM/HGEMM/DGEMM TFLOPS at n = 4096, skinny 4096² FP16 µs/call
 and HBM GB/s, level 1/2 GB/s, each as a fraction of its roofline, with the reference's CPU path timed beside it.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu] [--case NAME ...]
+    python bench.py [--steps K] [--warmup W] [--settle S] [--gpus 1] [--quick] [--no-cpu] [--case NAME ...]
 
 Prints ONE JSON line. `value` is HGEMM (GEN9BLAS_H) TFLOP/s at n = 4096 (NN, alpha = 1, beta = 0, inputs resident in
 HBM); every other configuration of BASELINE.json is in `results`. A step is one library call on one configuration,
 timed with HIP events recorded on the library's own stream (the stream its kernels run on) around K back-to-back calls
-after W warm-up calls, in no-wait mode (device operands, no host synchronization per call). `--case` runs only the
-named cases (for profiling runs; the JSON line then carries only what was measured).
+after W warm-up calls, in no-wait mode (device operands, no host synchronization per call). Before the W warm-ups each
+case runs the same call for S seconds (default 1.5): the MI355X clock climbs for about a second after the GPU has been
+idle (measured 1.7 → 2.4 GHz over 1.2 s) and then settles under the board's power limit, so shorter runs measure the
+ramp, not the sustained rate. The hipBLASLt calibration is timed the same way. `--case` runs only the named cases (for
+profiling runs; the JSON line then carries only what was measured).
 Inputs: np.random.default_rng seeds A = 1, B = 2, C = 3, W copies 100..131, x = 20, y = 21 (synthetic data).
 """
 import argparse
@@ -37,8 +40,9 @@ GEMM_CASES = {
     "sgemm_odd_3000x11008x4096_tB_beta05": ("S", None),
 }
 QUICK = ("hgemm_n4096", "hgemm_accurate_n4096", "hbm_read_1GiB", "skinny")
-OTHER_CASES = ("hgemm_n4096_host", "hbm_read_1GiB", "skinny", "packed_decode", "level3_n4096", "saxpy_2^26",
-               "sdot_2^26", "sgemv_16384", "level2_16384", "copy_256MiB", "calibration")
+OTHER_CASES = ("hgemm_n4096_host", "hbm_read_1GiB", "skinny", "skinny_read_floor", "packed_decode", "level3_n4096",
+               "saxpy_2^26", "sdot_2^26", "sgemv_16384", "level2_16384", "copy_256MiB", "calibration", "mfma_ceiling")
+CALIB_LIB = os.path.join(ROOT, "gen9-gpu-blas_amd", "libgen9blas_calib.so")   # calibration kernels (calib/calibrate.hip)
 
 
 def log(*a):
@@ -58,8 +62,9 @@ def traffic_from_summary():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--settle", type=float, default=1.5, help="seconds of the same call before each case's warm-ups")
     ap.add_argument("--quick", action="store_true", help="HGEMM n=4096, HBM read and skinny only, no CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--case", action="append", default=[], choices=list(GEMM_CASES) + list(OTHER_CASES))
@@ -77,6 +82,12 @@ def main():
     stream = torch.cuda.ExternalStream(g9.hip_stream())
     steps, warm = args.steps, args.warmup
     dev = torch.device("cuda:0")
+    cal = ctypes.CDLL(CALIB_LIB)
+    cal.g9cal_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    cal.g9cal_mfma.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                               ctypes.c_int, ctypes.c_void_p]
+    lib_stream = ctypes.c_void_p(g9.hip_stream())
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
     p, d = ctypes.c_void_p, ctypes.c_double
 
     def to_dev(x):
@@ -86,8 +97,19 @@ def main():
         if rc:
             raise RuntimeError(L.gen9blas_error().decode())
 
+    def settle(fn, seconds):
+        """Runs fn back to back for `seconds` (waiting every 64 calls, so the queue stays short)."""
+        t_end = time.perf_counter() + seconds
+        while time.perf_counter() < t_end:
+            for _ in range(64):
+                fn()
+            g9.flush()
+            torch.cuda.synchronize()
+
     def timed(fn, k=steps, w=warm):
-        """ms per call: HIP events on the library stream around k back-to-back calls after w warm-ups."""
+        """ms per call: HIP events on the library stream around k back-to-back calls after the settle period and w
+        warm-ups."""
+        settle(fn, args.settle)
         for _ in range(w):
             fn()
         g9.flush()
@@ -161,25 +183,53 @@ def main():
     # ---------------- measured HBM bandwidth: streaming read of 1 GiB (> 256 MB MALL) ----------------
     out_d = torch.zeros(1, dtype=torch.float64, device=dev)   # device result: no host wait per call
     out_p = ctypes.cast(ctypes.c_void_p(out_d.data_ptr()), ctypes.POINTER(ctypes.c_double))
-    hbm = None
     if "hbm_read_1GiB" in cases:
         nh = 1 << 28
         big = torch.empty(nh, dtype=torch.float32, device=dev).uniform_(-1, 1)
-        ms = timed(lambda: check(L.gen9blas_asum(1, nh, p(big.data_ptr()), 1, out_p)), k=10, w=2)
+        ms = timed(lambda: check(L.gen9blas_asum(1, nh, p(big.data_ptr()), 1, out_p)), k=20, w=2)
         hbm = 4.0 * nh / (ms * 1e-3) / 1e9
         res["hbm_read_1GiB"] = {"kernel": "gen9blas_asum FP32 2^28 (pure streaming read)", "ms": round(ms, 4),
                                 "GBs": round(hbm, 1), "frac_of_datasheet": round(hbm / PEAK_HBM_GBS, 4)}
         log("hbm_read_1GiB", res["hbm_read_1GiB"])
-        del big
+        sink = torch.empty(4 * ncu, dtype=torch.float32, device=dev)
+        ms = timed(lambda: check(cal.g9cal_stream_read(big.data_ptr(), 4 * nh, sink.data_ptr(), 4 * ncu, lib_stream)),
+                   k=20, w=2)
+        gbs = 4.0 * nh / (ms * 1e-3) / 1e9
+        res["calib_stream_read_1GiB"] = {"kernel": "calibration streaming read (8 loads of 16 B in flight per lane)",
+                                         "ms": round(ms, 4), "GBs": round(gbs, 1),
+                                         "frac_of_datasheet": round(gbs / PEAK_HBM_GBS, 4)}
+        log("calib_stream_read_1GiB", res["calib_stream_read_1GiB"])
+        del big, sink
+
+    hbm_rated = []   # streaming results whose fraction of the measured HBM bandwidth is filled in at the end
 
     def hbm_fracs(r):
-        if hbm:
-            r["frac_of_measured_hbm"] = round(r["GBs"] / hbm, 4)
         r["frac_of_datasheet_hbm"] = round(r["GBs"] / PEAK_HBM_GBS, 4)
+        hbm_rated.append(r)
         return r
 
+    # ---------------- level 1/2 ----------------
+    n = 1 << 26
+    if cases & {"saxpy_2^26", "sdot_2^26", "copy_256MiB"}:
+        xd = to_dev(np.random.default_rng(20).uniform(-1, 1, n).astype(np.float32))
+        yd = to_dev(np.random.default_rng(21).uniform(-1, 1, n).astype(np.float32))
+        if "saxpy_2^26" in cases:
+            ms = timed(lambda: check(L.gen9blas_axpy(1, n, d(0.5), p(xd.data_ptr()), 1, p(yd.data_ptr()), 1)))
+            res["saxpy_2^26"] = hbm_fracs({"ms": round(ms, 4), "GBs": round(12.0 * n / (ms * 1e-3) / 1e9, 1)})
+            log("saxpy_2^26", res["saxpy_2^26"])
+        if "sdot_2^26" in cases:
+            ms = timed(lambda: check(L.gen9blas_dot(1, n, p(xd.data_ptr()), 1, p(yd.data_ptr()), 1, out_p)))
+            res["sdot_2^26"] = hbm_fracs({"ms": round(ms, 4), "GBs": round(8.0 * n / (ms * 1e-3) / 1e9, 1),
+                                          "note": "FP64 result written to device memory"})
+            log("sdot_2^26", res["sdot_2^26"])
+        if "copy_256MiB" in cases:
+            # known-size copy (reads 256 MiB, writes 256 MiB): the reference point for the HBM byte counters
+            ms = timed(lambda: check(L.gen9blas_copy(1, n, p(xd.data_ptr()), 1, p(yd.data_ptr()), 1)))
+            res["copy_256MiB"] = hbm_fracs({"ms": round(ms, 4), "GBs": round(8.0 * n / (ms * 1e-3) / 1e9, 1)})
+            log("copy_256MiB", res["copy_256MiB"])
+        del xd, yd
     # ---------------- skinny C = A·Wᵀ, W 4096² fp16, 32 rotated copies (1 GiB) ----------------
-    if "skinny" in cases:
+    if cases & {"skinny", "skinny_read_floor"}:
         K = N = 4096
         ncopy = 32
         Wd = torch.empty((ncopy, N, K), dtype=torch.float16, device=dev)
@@ -188,7 +238,7 @@ def main():
             Wd[c].copy_(torch.from_numpy(w.astype(np.float16)))
         sk = {}
         wp = [Wd[c].data_ptr() for c in range(ncopy)]
-        for M in (1, 2, 4, 8, 16):
+        for M in ((1, 2, 4, 8, 16) if "skinny" in cases else ()):
             Ad = to_dev(np.random.default_rng(1).standard_normal((M, K), dtype=np.float32).astype(np.float16))
             Cd = torch.empty((M, N), dtype=torch.float16, device=dev)
             state = {"j": 0}
@@ -203,6 +253,36 @@ def main():
             sk[f"M{M}"] = hbm_fracs({"us_per_call": round(ms * 1e3, 2), "GBs": round(byts / (ms * 1e-3) / 1e9, 1)})
             log("skinny", M, sk[f"M{M}"])
         res["skinny_fp16_4096x4096"] = sk
+        if "skinny_read_floor" in cases:
+            # the floor of one skinny call: a pure read of the same 32 MiB weight copy per call, over the same 32
+            # rotated copies, by the calibration streaming-read kernel (one kernel per call, as the skinny product) with
+            # 512 and 1024 blocks, and by the library's own asum (two kernels per call: partial sums, then their sum)
+            sink = torch.empty(1024, dtype=torch.float32, device=dev)
+            byts = 2.0 * N * K
+            floor = {}
+            for blocks in (512, 1024):
+                state = {"j": 0}
+
+                def fn():
+                    j = state["j"]
+                    state["j"] = (j + 1) % ncopy
+                    check(cal.g9cal_stream_read(wp[j], N * K * 2, sink.data_ptr(), blocks, lib_stream))
+                ms = timed(fn, k=max(steps, 32) * 2, w=max(warm, 32))
+                floor[f"calib_read_{blocks}_blocks"] = hbm_fracs({"us_per_call": round(ms * 1e3, 2),
+                                                                  "GBs": round(byts / (ms * 1e-3) / 1e9, 1)})
+            state = {"j": 0}
+
+            def fn():
+                j = state["j"]
+                state["j"] = (j + 1) % ncopy
+                check(L.gen9blas_asum(0, N * K, p(wp[j]), 1, out_p))
+            ms = timed(fn, k=max(steps, 32) * 2, w=max(warm, 32))
+            floor["gen9blas_asum_fp16"] = hbm_fracs({"us_per_call": round(ms * 1e3, 2),
+                                                     "GBs": round(byts / (ms * 1e-3) / 1e9, 1)})
+            floor["note"] = "a pure read of one 4096x4096 fp16 copy per call, 32 copies rotated (1 GiB)"
+            res["skinny_read_floor_32MiB"] = floor
+            log("skinny_read_floor", floor)
+            del sink
         del Wd
 
     # ---------------- packed weights: gemm_pb (M = 1..16) on 32 resident packed copies of a 4096² fp16 W ----------
@@ -291,26 +371,6 @@ def main():
             del Ad, Bd, Cd, Xd
         res["level3_n4096"] = l3
 
-    # ---------------- level 1/2 ----------------
-    n = 1 << 26
-    if cases & {"saxpy_2^26", "sdot_2^26", "copy_256MiB"}:
-        xd = to_dev(np.random.default_rng(20).uniform(-1, 1, n).astype(np.float32))
-        yd = to_dev(np.random.default_rng(21).uniform(-1, 1, n).astype(np.float32))
-        if "saxpy_2^26" in cases:
-            ms = timed(lambda: check(L.gen9blas_axpy(1, n, d(0.5), p(xd.data_ptr()), 1, p(yd.data_ptr()), 1)))
-            res["saxpy_2^26"] = hbm_fracs({"ms": round(ms, 4), "GBs": round(12.0 * n / (ms * 1e-3) / 1e9, 1)})
-            log("saxpy_2^26", res["saxpy_2^26"])
-        if "sdot_2^26" in cases:
-            ms = timed(lambda: check(L.gen9blas_dot(1, n, p(xd.data_ptr()), 1, p(yd.data_ptr()), 1, out_p)))
-            res["sdot_2^26"] = hbm_fracs({"ms": round(ms, 4), "GBs": round(8.0 * n / (ms * 1e-3) / 1e9, 1),
-                                          "note": "FP64 result written to device memory"})
-            log("sdot_2^26", res["sdot_2^26"])
-        if "copy_256MiB" in cases:
-            # known-size copy (reads 256 MiB, writes 256 MiB): the reference point for the HBM byte counters
-            ms = timed(lambda: check(L.gen9blas_copy(1, n, p(xd.data_ptr()), 1, p(yd.data_ptr()), 1)))
-            res["copy_256MiB"] = hbm_fracs({"ms": round(ms, 4), "GBs": round(8.0 * n / (ms * 1e-3) / 1e9, 1)})
-            log("copy_256MiB", res["copy_256MiB"])
-        del xd, yd
     if "sgemv_16384" in cases:
         m = 16384
         Ad = to_dev(np.random.default_rng(1).uniform(-1, 1, (m, m)).astype(np.float32))
@@ -365,31 +425,71 @@ def main():
 
     g9.set_nowait(False)
 
+    # ---------------- the matrix cores' sustained FP16 rate on random operands, with no data movement ----------------
+    if "mfma_ceiling" in cases:
+        src = torch.from_numpy(np.random.default_rng(1).standard_normal(8 << 20, dtype=np.float32).astype(np.float16)).to(dev)
+        blocks, iters = 2 * ncu, 2000                 # 8 waves per CU; about 2 ms per call
+        outb = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+        flop = blocks * 4 * iters * float(1 << 20)
+        mc = {}
+        for shape in (32, 16):
+            ms = timed(lambda: check(cal.g9cal_mfma(shape, src.data_ptr(), src.numel() * 2, outb.data_ptr(), blocks,
+                                                    iters, lib_stream)), k=20, w=2)
+            mc[f"mfma_f32_{shape}x{shape}x{512 // shape}_f16"] = round(flop / (ms * 1e-3) / 1e12, 1)
+        mc["note"] = ("calibration loop of MFMAs on random FP16 register operands (8 waves per CU, no memory traffic): "
+                      "the rate the matrix cores sustain under the board's power limit")
+        res["mfma_ceiling_fp16_tflops"] = mc
+        log("mfma_ceiling", mc)
+        del src, outb
+
     # ---------------- calibration: AMD's libraries through torch.matmul (hipBLASLt / rocBLAS), not this library ----
     if "calibration" in cases:
         cal = {}
         for name, tdt in (("fp16", torch.float16), ("fp32", torch.float32), ("fp64", torch.float64)):
-            a = torch.randn(4096, 4096, dtype=tdt, device=dev)
-            b = torch.randn(4096, 4096, dtype=tdt, device=dev)
-            for _ in range(3):
-                torch.matmul(a, b)
-            torch.cuda.synchronize()
+            if tdt == torch.float16:
+                a = torch.from_numpy(np.random.default_rng(1).standard_normal((4096, 4096), dtype=np.float32)).to(dev, tdt)
+                b = torch.from_numpy(np.random.default_rng(2).standard_normal((4096, 4096), dtype=np.float32)).to(dev, tdt)
+            else:
+                a = torch.empty(4096, 4096, dtype=tdt, device=dev).uniform_(-1, 1)
+                b = torch.empty(4096, 4096, dtype=tdt, device=dev).uniform_(-1, 1)
+            c = torch.empty(4096, 4096, dtype=tdt, device=dev)
+            t_end = time.perf_counter() + args.settle
+            while time.perf_counter() < t_end:
+                for _ in range(16):
+                    torch.matmul(a, b, out=c)
+                torch.cuda.synchronize()
+            for _ in range(warm):
+                torch.matmul(a, b, out=c)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-            for _ in range(10):
-                torch.matmul(a, b)
+            for _ in range(steps):
+                torch.matmul(a, b, out=c)
             e1.record()
             e1.synchronize()
-            ms = e0.elapsed_time(e1) / 10
+            ms = e0.elapsed_time(e1) / steps
             cal[name] = round(2.0 * 4096 ** 3 / (ms * 1e-3) / 1e12, 1)
-            del a, b
+            del a, b, c
         res["calibration_torch_matmul_n4096_tflops"] = cal
         log("calibration", cal)
+
+    # ---------------- fractions of the measured HBM bandwidth ----------------
+    # The reference point is the fastest streaming kernel over working sets beyond the MALL: the library's 1 GiB read
+    # (asum), the calibration read of the same 1 GiB, SDOT (2 × 256 MiB read) and the copy (256 MiB read + written).
+    ref_keys = ("hbm_read_1GiB", "calib_stream_read_1GiB", "sdot_2^26", "copy_256MiB")
+    streams = [res[k]["GBs"] for k in ref_keys if k in res]
+    if streams:
+        hbm_ref = max(streams)
+        res["measured_hbm_GBs"] = {"GBs": round(hbm_ref, 1), "of": "max of " + ", ".join(k for k in ref_keys if k in res)}
+        for r in hbm_rated:
+            r["frac_of_measured_hbm"] = round(r["GBs"] / hbm_ref, 4)
 
     # ---------------- CPU baseline: the reference's CPU path on the host cores ----------------
     cpu = None
     if not args.quick and not args.no_cpu and not args.case:
-        cpu = cpu_baseline()
+        cpu, per_config = cpu_baselines()
+        for k, v in per_config.items():
+            res.setdefault("cpu_path", {})[k] = v
+            log("cpu", k, v)
 
     h = res.get("hgemm_n4096")
     line = {
@@ -398,7 +498,7 @@ def main():
         "ms_per_step": h["ms"] if h else None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp16", "data": "synthetic",
         "config": {"workload": "HGEMM FP16 (GEN9BLAS_H) n=4096 NN alpha=1 beta=0, A,B ~ N(0,1) fp16, HBM-resident",
-                   "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU"},
+                   "M": 4096, "N": 4096, "K": 4096, "parallelism": "single GPU", "settle_s": args.settle},
         "roofline": {"bound": "mfma", "achieved": h["tflops"] if h else None, "peak": PEAK_TFLOPS["H"],
                      "unit": "TFLOP/s", "frac": h["frac_of_peak"] if h else None, "traffic": traffic_from_summary(),
                      "traffic_unit": "bytes per launch (HBM, FETCH_SIZE + WRITE_SIZE scaled by a known-size copy)",
@@ -409,35 +509,106 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def cpu_baseline():
-    """HGEMM n=4096 on the reference's CPU path (NumPy FP32 math on the FP16 inputs = OpenBLAS sgemm), bounded sample."""
+def cpu_baselines(budget_s=40.0):
+    """The reference's CPU path (its BLAS layer forwards to OpenBLAS; HGEMM and skinny are NumPy FP32 math on the
+    FP16 inputs, reference: lib/src/cblas.c:43-56, bench/gemm_cpu.py:33-37, bench/l12_cpu.py:13-16) on the host
+    cores, for every BASELINE configuration: best of up to 5 timed runs after one warm-up, on the same inputs as the
+    GPU cases. Returns (the HGEMM n = 4096 entry, which is `cpu_baseline`, {config: entry}). Bounded: each config stops
+    after ~3 s of runs and the whole set after `budget_s`."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
+    from scipy.linalg import blas
     threads = min(16, os.cpu_count() or 1)
     try:
         from threadpoolctl import threadpool_limits
         lim = threadpool_limits(threads)
     except Exception:
         lim = None
-    n = 4096
-    A = oracle.normal((n, n), np.float16, oracle.SEED_A)
-    B = oracle.normal((n, n), np.float16, oracle.SEED_B)
-    oracle.cpu_path.hgemm(A[:256], B)
-    ts = []
-    t_end = time.perf_counter() + 20
-    for _ in range(5):
-        t = time.perf_counter()
-        oracle.cpu_path.hgemm(A, B)
-        ts.append(time.perf_counter() - t)
-        if time.perf_counter() > t_end:
-            break
-    best = min(ts)
     ver, nth = oracle.openblas_info()
-    if lim is not None:
-        lim.unregister() if hasattr(lim, "unregister") else None
-    return {"value": round(2.0 * n ** 3 / best / 1e12, 3), "unit": "TFLOPS", "cores": nth or threads, "kind": "port",
-            "sample": f"HGEMM n=4096 on the reference CPU path: NumPy FP32 matmul (OpenBLAS {ver}) of the same FP16 "
-                      f"inputs, best of {len(ts)} after 1 warm-up, {nth or threads} threads on {os.cpu_count()} cpus"}
+    cores = nth or threads
+    t_all = time.perf_counter() + budget_s
+    out = {}
+
+    def best_of(fn, per_s=3.0):
+        fn()
+        ts, t_end = [], time.perf_counter() + per_s
+        for _ in range(5):
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+            if time.perf_counter() > t_end:
+                break
+        return min(ts), len(ts)
+
+    def entry(name, value, unit, sample):
+        out[name] = {"value": value, "unit": unit, "cores": cores, "kind": "port",
+                     "sample": f"{sample}; OpenBLAS {ver}, {cores} threads on {os.cpu_count()} cpus"}
+
+    rng = np.random.default_rng
+    for n in (4096, 1024, 2048):
+        if time.perf_counter() > t_all:
+            break
+        A = oracle.normal((n, n), np.float16, oracle.SEED_A)
+        B = oracle.normal((n, n), np.float16, oracle.SEED_B)
+        t, k = best_of(lambda: oracle.cpu_path.hgemm(A, B))
+        entry(f"hgemm_n{n}", round(2.0 * n ** 3 / t / 1e12, 4), "TFLOPS",
+              f"NumPy FP32 matmul of the FP16 inputs (H and HS alike), n={n}, best of {k}")
+    for kind, dt in (("sgemm", np.float32), ("dgemm", np.float64)):
+        for n in (1024, 4096):
+            if time.perf_counter() > t_all:
+                break
+            A = rng(1).uniform(-1, 1, (n, n)).astype(dt)
+            B = rng(2).uniform(-1, 1, (n, n)).astype(dt)
+            t, k = best_of(lambda: A @ B)
+            entry(f"{kind}_n{n}", round(2.0 * n ** 3 / t / 1e12, 4), "TFLOPS", f"NumPy {kind} n={n}, best of {k}")
+    if time.perf_counter() < t_all:
+        M, N, K = 3000, 11008, 4096
+        A = rng(1).uniform(-1, 1, (M, K)).astype(np.float32)
+        Bt = rng(2).uniform(-1, 1, (N, K)).astype(np.float32)
+        C0 = rng(3).uniform(-1, 1, (M, N)).astype(np.float32)
+        # one OpenBLAS sgemm with beta, in place: C (column-major view Cᵀ, N×M) = Bt·Aᵀ + 0.5·Cᵀ
+        Cw = np.array(C0.T, order="F")
+        t, k = best_of(lambda: blas.sgemm(1.0, Bt.T, A.T, beta=0.5, c=Cw, trans_a=1, overwrite_c=1))
+        entry("sgemm_odd_3000x11008x4096_tB_beta05", round(2.0 * M * N * K / t / 1e12, 4), "TFLOPS",
+              f"scipy.linalg.blas.sgemm (beta = 0.5), best of {k}")
+    if time.perf_counter() < t_all:
+        K = N = 4096
+        Ws = [oracle.normal((N, K), np.float16, 100 + c, 0.02) for c in range(4)]
+        for M in (1, 2, 4, 8, 16):
+            A = oracle.normal((M, K), np.float16, oracle.SEED_A)
+            state = {"j": 0}
+
+            def call():
+                state["j"] = (state["j"] + 1) % len(Ws)
+                oracle.cpu_path.skinny(A, Ws[state["j"]])
+            t, k = best_of(call, per_s=1.0)
+            entry(f"skinny_M{M}", round(t * 1e6, 1), "us_per_call",
+                  f"NumPy FP32 A·Wᵀ of the FP16 inputs (FP16→FP32 conversion of W included), 4 rotated W copies, "
+                  f"best of {k}")
+    if time.perf_counter() < t_all:
+        n = 1 << 26
+        x = rng(20).uniform(-1, 1, n).astype(np.float32)
+        y = rng(21).uniform(-1, 1, n).astype(np.float32)
+        t, k = best_of(lambda: blas.saxpy(x, y, a=0.5))
+        entry("saxpy_2^26", round(12.0 * n / t / 1e9, 1), "GB/s", f"scipy.linalg.blas.saxpy, best of {k}")
+        t, k = best_of(lambda: blas.sdot(x, y))
+        entry("sdot_2^26", round(8.0 * n / t / 1e9, 1), "GB/s", f"scipy.linalg.blas.sdot, best of {k}")
+        del x, y
+    if time.perf_counter() < t_all:
+        m = 16384
+        A = rng(1).uniform(-1, 1, (m, m)).astype(np.float32)
+        xv = rng(20).uniform(-1, 1, m).astype(np.float32)
+        for tr in (0, 1):
+            t, k = best_of(lambda: A.T @ xv if tr else A @ xv)
+            entry(f"sgemv_{'T' if tr else 'N'}_16384", round((4.0 * m * m + 8.0 * m) / t / 1e9, 1), "GB/s",
+                  f"NumPy float32 matrix-vector (OpenBLAS sgemv), best of {k}")
+        del A
+    if lim is not None and hasattr(lim, "unregister"):
+        lim.unregister()
+    head = out.get("hgemm_n4096")
+    if head:
+        head = dict(head, sample="HGEMM n=4096 on the reference CPU path: " + head["sample"])
+    return head, out
 
 
 if __name__ == "__main__":

@@ -3,7 +3,8 @@
     python gen9-gpu-blas_amd/build.py            # rebuild what changed
     python gen9-gpu-blas_amd/build.py --force    # rebuild everything
 
-The libraries are written next to this file (git-ignored), object files under _build/. hipcc cross-compiles for gfx950
+The libraries are written next to this file (git-ignored), object files under _build/; libgen9blas_calib.so holds
+the calibration kernels bench.py measures ceilings with and is not part of the library. hipcc cross-compiles for gfx950
 without a GPU. Replaces the reference's CMake + ocloc kernel-table build (reference: lib/CMakeLists.txt): the HIP
 kernels are compiled into the library, there is no separate kernel table.
 """
@@ -20,6 +21,7 @@ INCLUDE = os.path.join(ROOT, "include")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 LIB = os.path.join(HERE, "libgen9blas.so")
 BLAS_LIB = os.path.join(HERE, "libgen9blas_blas.so")
+CALIB_LIB = os.path.join(HERE, "libgen9blas_calib.so")   # bench.py's calibration kernels, not part of the library
 
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC", "-fvisibility=hidden", "-I" + INCLUDE, "-I" + CSRC,
              # packed FP32 VALU forms are kept out of the generated code
@@ -64,7 +66,16 @@ def build(force=False, jobs=None, verbose=True):
               "-Wl,--version-script=" + os.path.join(CSRC, "exports.map"), "-o", LIB + ".tmp"] + objs)
         os.replace(LIB + ".tmp", LIB)
     _build_blas(force)
+    _build_calib(force)
     return LIB
+
+
+def _build_calib(force):
+    """libgen9blas_calib.so: the calibration kernels bench.py measures ceilings with (calib/calibrate.hip)."""
+    src = os.path.join(HERE, "calib", "calibrate.hip")
+    if force or _stale(CALIB_LIB, [src]):
+        _run([HIPCC] + HIP_FLAGS + ["-shared", "-o", CALIB_LIB + ".tmp", src])
+        os.replace(CALIB_LIB + ".tmp", CALIB_LIB)
 
 
 def _build_blas(force):

@@ -142,12 +142,16 @@ static int launch_layout(const GemmParams<typename Mma<T>::Sum> &p, int count) {
 }
 
 // ---------------- FP16 whole-tile kernel ----------------
-// Configurations from sweeps on MI355X with N(0,1) FP16 inputs: n = 4096, 256×256 tiles, 8 waves (4×2), KB = 64,
-// two stages: 1130-1180 TFLOP/s (NN; hipBLASLt on the same inputs: 1180-1210); n = 2048, 128×128 tiles, 4 waves,
-// KB = 32, four stages: 780 (32×128 or 64×128 tiles: 430-690). Products with fewer 256×256 tiles than CUs take the
-// 128×128 tile, and with fewer 128×128 tiles than CUs (n = 1024: 64) a 32×128 tile, 4 waves of 32×32, KB = 64, three
-// stages: 322 TFLOP/s at n = 1024 against 208 for 128×128 (two or four stages: 290, 312; 64×128: 268). The 32-row
-// tile needs A k-contiguous (the transposed-A loader reads 128-row tiles).
+// Configurations from sweeps on MI355X with N(0,1) FP16 inputs, timed after 1.5 s of the same load (the clock
+// settles under the board's power limit; shorter runs see its ramp), every variant bit-exact on small integers:
+// - products with at least one 256×256 tile per CU: 256×256 tiles, 8 waves of 128×64 (2×4), two stages of KB = 64.
+//   n = 4096 NN 1314-1324 TFLOP/s (8 waves of 64×128: 1276-1286; 4 waves of 128×128: 1243-1246, at 2.03 GHz against
+//   1.79-1.81; the same 8 waves on 32x32x16 MFMAs: 1166-1176); TN 1249, NT 1339, TT 1267 (32x32x16: 1180-1188);
+// - at least one 128×128 tile per CU: 128×128, 8 waves of 64×32 (2×4), three stages. n = 2048 NN 835 (4 waves of
+//   64×64 with 3 or 4 stages: 798-807; 32x32x16 tiles: 795), NT 845 (767), TN and TT 800-804 (800-802);
+// - fewer 128×128 tiles than CUs, with A k-contiguous: 32×128 tiles, 4 waves of 32×32, three stages: n = 1024 NN 370.6
+//   (four stages 359, two 312; 32x32x16: 346), NT 363 (343). The 32-row tile needs A k-contiguous (the
+//   transposed-A loader reads 128-row tiles).
 template <int BM, int BN, int WM, int WN, int KB, int NS, bool AK, bool BKC>
 static int launch_hg(const hg::Params &p0, int count) {
     hg::Params p = p0;
@@ -161,13 +165,13 @@ static int launch_hg(const hg::Params &p0, int count) {
 template <bool AK, bool BKC>
 static int launch_hg_layout(const hg::Params &p, int count) {
     if ((long long)(p.M / 256) * (p.N / 256) * count >= num_cus && p.M % 256 == 0 && p.N % 256 == 0)
-        return launch_hg<256, 256, 4, 2, 64, 2, AK, BKC>(p, count);
+        return launch_hg<256, 256, 2, 4, 64, 2, AK, BKC>(p, count);
     if constexpr (AK)
         if ((long long)(p.M / 128) * (p.N / 128) * count < num_cus) return launch_hg<32, 128, 1, 4, 64, 3, AK, BKC>(p, count);
-    return launch_hg<128, 128, 2, 2, 32, 4, AK, BKC>(p, count);
+    return launch_hg<128, 128, 2, 4, 64, 3, AK, BKC>(p, count);
 }
 // The whole-tile FP16 kernel applies when every operand is 16-byte aligned with 16-byte row strides, M and N are
-// multiples of 128, K of 64 (both tile configurations' k-steps divide it), and the grid fits. GEN9BLAS_HGEMM=generic forces the general kernel.
+// multiples of 128, K of 64 (the k-step of every tile configuration), and the grid fits. GEN9BLAS_HGEMM=generic forces the general kernel.
 static bool hgemm_tiles_apply(const GemmCall &c) {
     static int generic = -1;
     if (generic < 0) {

@@ -1,5 +1,5 @@
 // FP16 GEMM kernel for gfx950 with direct global→LDS loads: C = alpha·op(A)·op(B) + beta·C, FP32 accumulation on
-// v_mfma_f32_32x32x16_f16, result rounded once to FP16.
+// v_mfma_f32_16x16x32_f16, result rounded once to FP16.
 //
 // Semantics are those of the reference's FP16 GEMM (reference: lib/kernels/hgemm.cl:838-898 hgemm_v / hgemm_kc_v,
 // lib/kernels/hgemm.cl:558-564 gen9blas_epilog_b): every C element is the sum over k of the A·B products, then
@@ -8,24 +8,31 @@
 //
 // This kernel serves products whose tiles are all full (M % BM = N % BN = K % KB = 0) with 16-byte aligned
 // operands; the general FP16 kernel in gemm_kernel.h takes every other shape. Design:
+// - the matrix-core instruction is v_mfma_f32_16x16x32_f16. It moves a quarter of the accumulator bytes per flop of
+//   v_mfma_f32_32x32x16_f16 (4 instead of 16 FP32 per lane per instruction), and large FP16 products on random data
+//   run at the board's power limit, so the energy per flop sets the rate: a loop of it sustains 1627 TFLOP/s on
+//   MI355X against 1580 for the 32x32x16 form, and this kernel went from 1166-1176 to 1314-1324 TFLOP/s at n = 4096
+//   (NN, sustained) when it moved from 32x32x16 to 16x16x32 tiles;
 // - operand tiles go from global memory straight into LDS with global_load_lds_dwordx4 (no register staging, no
 //   LDS write instructions): lane L of one instruction writes the 16 bytes at LDS offset base + 16·L, so each lane
 //   is given the global address whose data belongs at that LDS position;
-// - NS LDS stages of KB k each form a ring: the loads for k-step t+NS are issued as soon as stage t is free, so a
-//   load has about NS-1 k-steps to arrive;
-// - one barrier per k-step, placed before the last k16 substep: after it the wave issues the next stage's loads and
+// - NS LDS stages of KB = 64 k each form a ring: the loads for k-step t+NS are issued as soon as stage t is free, so
+//   a load has about NS-1 k-steps to arrive;
+// - one barrier per k-step, placed before the last k32 substep: after it the wave issues the next stage's loads and
 //   its first fragment reads, then runs the last substep's MFMAs, so neither the barrier nor the first LDS reads of
 //   a k-step leave the matrix cores idle for long;
 // - a k-contiguous operand (A not transposed, B transposed) is held as rows of KB k and read with ds_read_b128,
-//   one 16-byte fragment per lane. Chunk c (k = 8c .. 8c+7) of row r sits at physical chunk c ^ ((r / R) % CPR)
-//   (CPR chunks per row, R rows per 256 bytes): the 16 lanes that one LDS cycle serves read 16 consecutive rows at
-//   one logical chunk, and the swizzle spreads them over all 64 banks;
+//   one 16-byte fragment per lane. Chunk c (k = 8c .. 8c+7) of row r sits at physical chunk c ^ kswz(r): the 16
+//   lanes that one LDS cycle serves read 16 rows at one logical chunk, and the swizzle spreads them over all 64
+//   banks;
 // - an mn-contiguous operand (A transposed, B not transposed) is held as KB rows of k, each BM (or BN) elements
 //   long, and read with ds_read_b64_tr_b16, which transposes 16-lane groups: lane j of a group reads 4 consecutive
-//   mn of row kb + j/4, and lane i receives mn i of rows kb .. kb+3. Chunk c of row k sits at c ^ (4·(k & 3)), so
-//   the four rows of a group fall on distinct banks;
+//   mn of one k-row, and lane i receives the i-th mn of the group's reads for 4 k-rows. Chunk c of row k sits at
+//   c ^ (4·(k & 3)), so the four rows of a group fall on distinct banks;
 // - operands are swapped in the MFMA (the B fragment is the first input), so each lane ends with runs of 4
-//   consecutive n of one row of C; v_permlane32_swap joins two runs, giving 16-byte stores;
+//   consecutive n of one row of C. n tiles come in pairs whose 16 fragment rows interleave in groups of 4 (rows
+//   4q..4q+3 of the even tile are n 8q..8q+3 of the pair, of the odd tile n 8q+4..8q+7), so a lane's outputs of the
+//   two tiles are 8 consecutive n: one 16-byte store, no lane exchange;
 // - the workgroup → tile mapping gives each XCD a contiguous range of tiles, ordered in groups of 4 tile rows, so
 //   one XCD's L2 serves the A and B panels its tiles share.
 #pragma once
@@ -37,10 +44,18 @@ namespace hg {
 
 typedef _Float16 f16;
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Physical chunk of logical chunk 0 in k-contiguous LDS row r (rows of KB k, CPRK chunks of 8 k): chunk c lives at
+// c ^ kswz(r). 16 rows read together (16 consecutive rows, or the rows {0-3, 8-11, 16-19, 24-27} (+4) of a paired
+// 16x16x32 fragment) land on distinct 16-byte bank groups; kswz(r + 32) = kswz(r).
+template <int KB> __device__ __forceinline__ int kswz(int r) {
+    constexpr int CPRK = KB / 8, RK = 128 / KB;
+    return ((r / RK) ^ (((r >> 4) & 1) * (CPRK / 4))) % CPRK;
+}
 
 struct Params {
     const f16 *A, *B;
@@ -62,7 +77,7 @@ struct Loader {
     static constexpr int CPR = RT / 8, RPI = 512 / RT;                    // mn-contiguous: chunks per row, rows per
                                                                           // instruction
     static_assert(NINST % NW == 0, "tile instructions must divide over the waves");
-    static_assert(!KC || (4 * NW) % CPRK == 0, "k-contiguous swizzle must repeat over a wave's instructions");
+    static_assert(!KC || (RPIK * NW) % 32 == 0, "k-contiguous swizzle must repeat over a wave's instructions");
     static_assert(KC || (RT >= 128 && (RPI * NW) % 4 == 0), "mn-contiguous swizzle must repeat over a wave's instructions");
     const char *org;      // wave-uniform: tile origin at the next k-step to load
     unsigned voff;        // this lane's byte offset for instruction 0
@@ -73,7 +88,7 @@ struct Loader {
         if constexpr (KC) {
             // instruction j = wave + NW·i covers rows RPIK·j ..; lane L: row RPIK·j + L / CPRK, physical chunk L % CPRK
             const int r = RPIK * wave + lane / CPRK;
-            const int c = (lane % CPRK) ^ ((r / RK) % CPRK);
+            const int c = (lane % CPRK) ^ kswz<KB>(r);
             org = reinterpret_cast<const char *>(X + (long long)mn0 * ld);
             voff = (unsigned)(((long long)r * ld + 8 * c) * 2);
             step_i = (long long)RPIK * NW * ld * 2;
@@ -101,51 +116,64 @@ struct Loader {
     __device__ __forceinline__ void advance(bool more) { if (more) org += step_k; }
 };
 
-// Fragment reads of one operand for a wave's TT MFMA tiles (32 rows of m or n each, starting at wave row w0).
-template <int RT, int KB, int TT, bool KC>
+// Fragment reads of one operand for a wave's TT MFMA tiles (16 rows of m or n each, starting at wave row w0): per
+// tile and k32 substep one 16-byte fragment per lane, row lane % 16 and k 8·(lane / 16) .. +7. PAIRED (the first MFMA
+// input, n): tiles 2p and 2p+1 cover n 32p .. 32p+31 of the wave, fragment row r of tile t being n
+// 32·(t/2) + 4·(t%2) + 8·(r/4) + r%4; otherwise row r of tile t is 16t + r.
+template <int RT, int KB, int TT, bool KC, bool PAIRED>
 struct Frags {
-    static constexpr int NSUB = KB / 16, CPRK = KB / 8, RK = 128 / KB;
-    unsigned off[KC ? NSUB : TT];   // per-lane byte offsets: per k16 substep (KC) or per tile (transposed reads)
+    static constexpr int NSUB = KB / 32;
+    static constexpr int NOFF = KC ? 2 * NSUB : TT;
+    unsigned off[NOFF];   // per-lane byte offsets: k-contiguous per tile parity and substep, else per tile
     __device__ __forceinline__ void init(int w0, int lane) {
+        const int g = lane >> 4, i = lane & 15;
         if constexpr (KC) {
-            const int r = lane & 31, hi = lane >> 5, sw = (r / RK) % CPRK;   // w0 + 32·t adds nothing to sw
 #pragma unroll
-            for (int s = 0; s < NSUB; s++) off[s] = (w0 + r) * (KB * 2) + (((2 * s + hi) ^ sw) << 4);
+            for (int par = 0; par < 2; par++) {
+                const int r = w0 + (PAIRED ? 4 * par + 8 * (i >> 2) + (i & 3) : 16 * par + i);   // + 32·(t/2)
+                const int sw = kswz<KB>(r);
+#pragma unroll
+                for (int s = 0; s < NSUB; s++) off[par * NSUB + s] = r * (KB * 2) + (((4 * s + g) ^ sw) << 4);
+            }
         } else {
-            const int G = lane >> 4, j = lane & 15, q = j >> 2;
-            const int krow = 8 * (G >> 1) + q;                      // + 16·s + 4·h (immediates)
-            const int low = 2 * (G & 1) + ((j & 3) >> 1);           // chunk bits 0-1
+            // ds_read_b64_tr_b16: in each 16-lane group (k group g), lane j reads 4 consecutive mn at k-row 8g + j/4
+            // (+ 4 for the second read) from block P(j % 4); lane i then holds mn P(i/4) + i%4 of those 4 k-rows
+            const int q = i >> 2, c = i & 3;
 #pragma unroll
             for (int t = 0; t < TT; t++) {
-                const int tc = (w0 >> 5) + t;                       // 32-wide tile index = chunk bits 2 and up
-                off[t] = krow * (RT * 2) + ((tc ^ q) << 6) + (low << 4) + 8 * (j & 1);   // q < 4 flips bits 2-3 only
+                const int P = w0 + (PAIRED ? 32 * (t >> 1) + 4 * (t & 1) + 8 * c : 16 * t + 4 * c);
+                off[t] = (8 * g + q) * (RT * 2) + (((P >> 3) ^ (4 * q)) << 4) + 2 * (P & 7);
             }
         }
     }
     // 16-byte fragment of tile t, substep s from the stage at `base`.
     __device__ __forceinline__ u32x4 read(const G9_LDS unsigned char *base, int t, int s) const {
         if constexpr (KC) {
-            return *reinterpret_cast<const G9_LDS u32x4 *>(base + off[s] + t * 32 * (KB * 2));
+            return *reinterpret_cast<const G9_LDS u32x4 *>(base + off[(t & 1) * NSUB + s] + (t >> 1) * 32 * (KB * 2));
         } else {
-            const G9_LDS unsigned char *b = base + off[t] + 16 * s * (RT * 2);
-            const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((G9_LDS i16x4 *)(b));
-            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((G9_LDS i16x4 *)(b + 4 * (RT * 2)));
+            const G9_LDS unsigned char *b = base + off[t] + 32 * s * (RT * 2);
+            const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((G9_LDS i16x4 *)(b));                // k-rows +0..3
+            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((G9_LDS i16x4 *)(b + 4 * (RT * 2)));  // +4..7
             const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
             return u32x4{l2[0], l2[1], h2[0], h2[1]};
         }
     }
 };
 
+__device__ __forceinline__ f32x4 mma(u32x4 b, u32x4 a, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, b), __builtin_bit_cast(f16x8, a), c, 0, 0, 0);
+}
+
 template <int BM, int BN, int WM, int WN, int KB, int NS, bool AK, bool BKC>
 __global__ void __launch_bounds__(WM *WN * 64) hgemm_kernel(Params p) {
     constexpr int NW = WM * WN;
-    constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+    constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 16, TN = WTN / 16;
     constexpr int ABYTES = BM * KB * 2, BBYTES = BN * KB * 2, SBYTES = ABYTES + BBYTES;
-    constexpr int NSUB = KB / 16;
+    constexpr int NSUB = KB / 32;
     using LA = Loader<BM, KB, NW, AK>;
     using LB = Loader<BN, KB, NW, BKC>;
     constexpr int LPS = LA::NI + LB::NI;   // loads per stage per wave
-    static_assert(TM * 32 == WTM && TN * 32 == WTN, "wave tile must be a multiple of 32");
+    static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32 (n tiles come in pairs)");
     static_assert(NSUB % 2 == 0, "fragment double buffer alternates over an even number of substeps");
     static_assert(NS >= 2 && (NS - 1) * LPS < 64, "loads in flight must fit vmcnt");
     // stage s: [A tile | B tile] at s·SBYTES
@@ -175,18 +203,16 @@ __global__ void __launch_bounds__(WM *WN * 64) hgemm_kernel(Params p) {
     LB lb;
     la.init(A, p.lda, m0, wave, lane);
     lb.init(B, p.ldb, n0, wave, lane);
-    Frags<BM, KB, TM, AK> fa;
-    Frags<BN, KB, TN, BKC> fb;
+    Frags<BM, KB, TM, AK, false> fa;
+    Frags<BN, KB, TN, BKC, true> fb;
     fa.init(wm * WTM, lane);
     fb.init(wn * WTN, lane);
 
-    f32x16 acc[TN][TM];
+    f32x4 acc[TN][TM];
 #pragma unroll
     for (int i = 0; i < TN; i++)
 #pragma unroll
-        for (int j = 0; j < TM; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+        for (int j = 0; j < TM; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     u32x4 ra[2][TM], rb[2][TN];
     auto read_frags = [&](const G9_LDS unsigned char *stg, int s, int buf) {
@@ -226,8 +252,7 @@ __global__ void __launch_bounds__(WM *WN * 64) hgemm_kernel(Params p) {
 #pragma unroll
             for (int t = 0; t < NMF; t++) {
                 const int i = t / TM, j = t % TM;
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, rb[s & 1][i]),
-                                                                   __builtin_bit_cast(f16x8, ra[s & 1][j]), acc[i][j], 0, 0, 0);
+                acc[i][j] = mma(rb[s & 1][i], ra[s & 1][j], acc[i][j]);
                 constexpr int PER = (NRF + NMF - 1) / NMF;
 #pragma unroll
                 for (int q = t * PER; q < (t + 1) * PER && q < NRF; q++) {   // in order of first use
@@ -251,8 +276,7 @@ __global__ void __launch_bounds__(WM *WN * 64) hgemm_kernel(Params p) {
 #pragma unroll
             for (int t = 0; t < NMF; t++) {
                 const int i = t / TM, j = t % TM;
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, rb[s & 1][i]),
-                                                                   __builtin_bit_cast(f16x8, ra[s & 1][j]), acc[i][j], 0, 0, 0);
+                acc[i][j] = mma(rb[s & 1][i], ra[s & 1][j], acc[i][j]);
 #pragma unroll
                 for (int q = t * PER; q < (t + 1) * PER && q < NIT; q++) {
                     if (q == 0) rb[0][0] = fb.read(nxt + ABYTES, 0, 0);
@@ -271,40 +295,25 @@ __global__ void __launch_bounds__(WM *WN * 64) hgemm_kernel(Params p) {
     }
     wait_vm<0>();   // the loads into stages nobody reads have landed before the wave ends
 
-    // Epilogue. Lane l holds D[n][m] for m = lane % 32 of MFMA tile j and n in runs of 4: rows 8q + 4·(l / 32) .. +3
-    // of tile i, q = 0..3. Each run becomes 4 FP16 values (alpha·acc + beta·C in FP32, rounded once); then lanes l and
-    // l+32 trade runs with v_permlane32_swap, so that each lane holds 8 consecutive n (16 bytes): lane l < 32 those of
-    // q = 2p, lane l + 32 those of q = 2p + 1, for p = 0, 1. Two 16-byte stores per MFMA tile and lane.
+    // Epilogue. Lane l holds D[n][m] for m = lane % 16 of MFMA tile j and, in the n-tile pair p, n = 32p + 8·(l / 16)
+    // + e from tile 2p (e = 0..3) and + 4 + e from tile 2p + 1: 8 consecutive n, one 16-byte store (alpha·acc +
+    // beta·C in FP32, rounded once).
     const float alpha = p.alpha, beta = p.beta;
-    const int hi = lane >> 5;
+    const int g = lane >> 4;
 #pragma unroll
-    for (int i = 0; i < TN; i++)
+    for (int pp = 0; pp < TN / 2; pp++)
 #pragma unroll
         for (int j = 0; j < TM; j++) {
-            const int m = m0 + wm * WTM + j * 32 + (lane & 31);
-            f16 *crow = C + (long long)m * p.ldc + n0 + wn * WTN + i * 32;
+            const int m = m0 + wm * WTM + j * 16 + (lane & 15);
+            f16 *cp = C + (long long)m * p.ldc + n0 + wn * WTN + 32 * pp + 8 * g;
+            union { u32x4 w; f16 e[8]; } o, v;
+            if (beta != 0.f) o.w = *reinterpret_cast<const u32x4 *>(cp);
 #pragma unroll
-            for (int pr = 0; pr < 2; pr++) {
-                unsigned w[2][2];   // [q - 2·pr][dword]: the lane's own run of q, 4 FP16 values
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const int q = 2 * pr + h;
-                    union { u32x2 w; f16 e[4]; } o, v;
-                    if (beta != 0.f) o.w = *reinterpret_cast<const u32x2 *>(crow + 8 * q + 4 * hi);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const float x = alpha * acc[i][j][4 * q + e];
-                        v.e[e] = (f16)(beta != 0.f ? __builtin_fmaf(beta, (float)o.e[e], x) : x);
-                    }
-                    w[h][0] = v.w[0];
-                    w[h][1] = v.w[1];
-                }
-                // swap lanes 32..63 of the q = 2pr run with lanes 0..31 of the q = 2pr+1 run
-                const auto s0 = __builtin_amdgcn_permlane32_swap(w[0][0], w[1][0], false, false);
-                const auto s1 = __builtin_amdgcn_permlane32_swap(w[0][1], w[1][1], false, false);
-                const u32x4 out = {s0[0], s1[0], s0[1], s1[1]};
-                *reinterpret_cast<u32x4 *>(crow + 8 * (2 * pr + hi)) = out;
+            for (int e = 0; e < 8; e++) {
+                const float x = alpha * acc[2 * pp + (e >> 2)][j][e & 3];
+                v.e[e] = (f16)(beta != 0.f ? __builtin_fmaf(beta, (float)o.e[e], x) : x);
             }
+            *reinterpret_cast<u32x4 *>(cp) = v.w;
         }
 }
 

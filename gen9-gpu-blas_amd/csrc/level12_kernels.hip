@@ -131,8 +131,27 @@ __global__ void __launch_bounds__(NT) reduce_kernel(int n, const T *x, ll ix, co
     };
     ll tail = 0;
     if (vec) {
-        const ll nv = n / V;
-        for (ll c = (ll)blockIdx.x * NT + threadIdx.x; c < nv; c += stride) {
+        // Each step a block reads U·NT consecutive chunks (16 KiB for FP32 asum) with every load issued before the
+        // first add: 4 loads of 16 bytes in flight per lane (dot: 2 of x and 2 of y), and the blocks in flight cover
+        // one contiguous span of memory.
+        constexpr int U = MODE == 0 ? 2 : 4;
+        const ll nv = n / V, big = (ll)U * NT, nsc = nv / big;
+        for (ll sc = blockIdx.x; sc < nsc; sc += gridDim.x) {
+            const ll c0 = sc * big + threadIdx.x;
+            Vec<T> xv[U], yv[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                xv[u] = vload_nt(x + (c0 + u * NT) * V);
+                if constexpr (MODE == 0) yv[u] = vload_nt(y + (c0 + u * NT) * V);
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int e = 0; e < V; e++)
+                    acc(e & 1 ? s1 : s0, (double)xv[u].e[e], MODE == 0 ? (double)yv[u].e[e] : 0.0);
+        }
+        ll c = nsc * big + (ll)blockIdx.x * NT + threadIdx.x;   // the chunks past the last whole super-chunk
+        for (; c < nv; c += stride) {
             const Vec<T> xv = vload_nt(x + c * V);
             Vec<T> yv;
             if constexpr (MODE == 0) yv = vload_nt(y + c * V);
