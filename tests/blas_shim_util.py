@@ -352,3 +352,97 @@ def l2_run(L, P, op, o, order, n, K, rng, dt, torch=None, alpha=0.75, beta=-0.5)
         mask = (np.tril if o[0] == "L" else np.triu)(np.ones((n, n), bool))
         got, ref, scale = got[mask], ref[mask], scale[mask]
     return float((np.abs(got - ref) / np.maximum(scale, 1e-300)).max())
+
+
+# ---------------- LD_PRELOAD interposition: an unmodified program linked against another BLAS ----------------
+# stub "system BLAS" the program is linked against: its GEMMs write -1 everywhere, so results tell which library ran
+STUB_BLAS_C = r"""
+void cblas_sgemm(int o, int ta, int tb, int M, int N, int K, float al, const float *A, int lda, const float *B, int ldb,
+                 float be, float *C, int ldc) {
+    for (int i = 0; i < (o == 101 ? M : N); i++) for (int j = 0; j < (o == 101 ? N : M); j++) C[(long)i * ldc + j] = -1.f;
+}
+void sgemm_(const char *ta, const char *tb, const int *M, const int *N, const int *K, const float *al, const float *A,
+            const int *lda, const float *B, const int *ldb, const float *be, float *C, const int *ldc) {
+    for (int j = 0; j < *N; j++) for (int i = 0; i < *M; i++) C[(long)j * *ldc + i] = -1.f;
+}
+"""
+# the program: a row-major CBLAS call and a column-major Fortran call, each checked against a float64 reference on
+# every 32nd row; prints "<name> maxrel=<error>" per call
+PROG_C = r"""
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+void cblas_sgemm(int, int, int, int, int, int, float, const float *, int, const float *, int, float, float *, int);
+void sgemm_(const char *, const char *, const int *, const int *, const int *, const float *, const float *, const int *,
+            const float *, const int *, const float *, float *, const int *);
+static float rnd(unsigned *s) { *s = *s * 1664525u + 1013904223u; return (float)((*s >> 8) & 0xffff) / 32768.f - 1.f; }
+int main(void) {
+    unsigned s = 7;
+    int M = 1024, N = 768, K = 640;   /* 2MNK just above the shim's 1e9-flop level-3 threshold */
+    float *A = malloc(sizeof(float) * M * K), *B = malloc(sizeof(float) * K * N), *C = malloc(sizeof(float) * M * N);
+    for (long i = 0; i < (long)M * K; i++) A[i] = rnd(&s);
+    for (long i = 0; i < (long)K * N; i++) B[i] = rnd(&s);
+    cblas_sgemm(101, 111, 111, M, N, K, 1.f, A, K, B, N, 0.f, C, N);
+    double worst = 0;
+    for (int i = 0; i < M; i += 32)
+        for (int j = 0; j < N; j++) {
+            double r = 0, a = 0;
+            for (int k = 0; k < K; k++) { r += (double)A[(long)i * K + k] * B[(long)k * N + j]; a += fabs((double)A[(long)i * K + k] * B[(long)k * N + j]); }
+            const double e = fabs(C[(long)i * N + j] - r) / a;
+            if (e > worst) worst = e;
+        }
+    printf("cblas_sgemm maxrel=%.3e\n", worst);
+    /* Fortran: column-major C (m x n) = A (m x k) * B (k x n) */
+    int m = 800, n = 900, k = 700;
+    float one = 1.f, zero = 0.f;
+    float *a = malloc(sizeof(float) * m * k), *b = malloc(sizeof(float) * k * n), *c = malloc(sizeof(float) * m * n);
+    for (long i = 0; i < (long)m * k; i++) a[i] = rnd(&s);
+    for (long i = 0; i < (long)k * n; i++) b[i] = rnd(&s);
+    sgemm_("N", "N", &m, &n, &k, &one, a, &m, b, &k, &zero, c, &m);
+    worst = 0;
+    for (int i = 0; i < m; i += 32)
+        for (int j = 0; j < n; j++) {
+            double r = 0, t = 0;
+            for (int q = 0; q < k; q++) { r += (double)a[(long)q * m + i] * b[(long)j * k + q]; t += fabs((double)a[(long)q * m + i] * b[(long)j * k + q]); }
+            const double e = fabs(c[(long)j * m + i] - r) / t;
+            if (e > worst) worst = e;
+        }
+    printf("sgemm_ maxrel=%.3e\n", worst);
+    return 0;
+}
+"""
+
+
+def build_preload_program(tmp):
+    """Compiles the stub BLAS (libstubblas.so) and the program linked against it (rpath to tmp) with gcc; returns the
+    program's path."""
+    import subprocess
+    tmp = str(tmp)
+    with open(os.path.join(tmp, "stub.c"), "w") as f:
+        f.write(STUB_BLAS_C)
+    with open(os.path.join(tmp, "prog.c"), "w") as f:
+        f.write(PROG_C)
+    subprocess.run(["gcc", "-O2", "-shared", "-fPIC", "-o", os.path.join(tmp, "libstubblas.so"),
+                    os.path.join(tmp, "stub.c")], check=True)
+    prog = os.path.join(tmp, "prog")
+    subprocess.run(["gcc", "-O2", "-o", prog, os.path.join(tmp, "prog.c"), "-L" + tmp, "-lstubblas",
+                    "-Wl,-rpath," + tmp, "-lm"], check=True)
+    return prog
+
+
+def run_preload_program(prog, preload, extra_env=None):
+    """Runs the program (with the shim in LD_PRELOAD when `preload`); returns ({call: maxrel}, stderr)."""
+    import subprocess
+    env = dict(os.environ)
+    env.pop("LD_PRELOAD", None)
+    if preload:
+        env["LD_PRELOAD"] = SHIM
+        env["GEN9BLAS_BLAS_INFO"] = "1"
+    env.update(extra_env or {})
+    r = subprocess.run([prog], env=env, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    errs = {}
+    for line in r.stdout.splitlines():
+        name, val = line.split(" maxrel=")
+        errs[name] = float(val)
+    return errs, r.stderr

@@ -34,9 +34,9 @@ def test_exports(L):
     out = subprocess.run(["nm", "-D", "--defined-only", U.SHIM], capture_output=True, text=True, check=True).stdout
     syms = {l.split()[-1] for l in out.splitlines() if l.strip()}
     assert U.OWN <= syms
-    blas = {s for s in syms if s.startswith("cblas_") or s.endswith("_")}
+    blas = {s for s in syms if s.startswith("cblas_") or s.endswith("_") or s == "__xerbla"}
     assert len(blas) == len(syms), f"non-BLAS exports: {sorted(syms - blas)[:10]}"
-    for s in ("cblas_zgemm", "cblas_csyrk", "dtrsm_", "cblas_sgbmv", "xerbla_", "cblas_dtrsv", "zdotc_"):
+    for s in ("cblas_zgemm", "cblas_csyrk", "dtrsm_", "cblas_sgbmv", "xerbla_", "__xerbla", "cblas_dtrsv", "zdotc_"):
         assert s in syms, s
     assert len(syms) > 300
 
@@ -160,3 +160,15 @@ def test_level2_every_option_cpu(L, P, op):
         for order in (U.ROW, U.COL, "F"):
             err = U.l2_run(L, P, op, o, order, 30, 4, rng, DT[P])
             assert err <= tol, (o, order, err)
+
+
+def test_ld_preload_interposition(L, tmp_path):
+    """An unmodified program linked against another BLAS (a stub whose GEMMs write -1) gets the shim's cblas_sgemm and
+    sgemm_ once libgen9blas_blas.so is in LD_PRELOAD (reference: README.md:9-10). Without a GPU the shim routes them
+    to the CPU BLAS, and the routing log (GEN9BLAS_BLAS_INFO) says so; the results match float64 to 1e-5."""
+    prog = U.build_preload_program(tmp_path)
+    plain, _ = U.run_preload_program(prog, preload=False)
+    assert plain["cblas_sgemm"] > 1e-2 and plain["sgemm_"] > 1e-2        # the stub ran (it writes -1)
+    errs, log = U.run_preload_program(prog, preload=True)
+    assert errs["cblas_sgemm"] <= 1e-5 and errs["sgemm_"] <= 1e-5, errs
+    assert "cblas_sgemm -> CPU" in log and "sgemm_ -> CPU" in log, log[-1000:]

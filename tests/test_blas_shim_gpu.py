@@ -179,3 +179,19 @@ def test_level2_device_operands_every_option(L, capfd, torch_dev, P, op):
     capfd.readouterr()
     err = U.l2_run(L, P, op, U.l2_opts(op)[0], U.ROW, n, K, rng, DT[P])
     assert routes(capfd) == ["CPU"] and err <= tol
+
+
+def test_ld_preload_interposition_gpu(g9, tmp_path):
+    """An unmodified program linked against another BLAS (a stub whose GEMMs write -1) gets the shim's cblas_sgemm and
+    sgemm_ once libgen9blas_blas.so is in LD_PRELOAD (reference: README.md:9-10); both products are above the shim's
+    level-3 threshold, so they run on the GPU (routing log, GEN9BLAS_BLAS_INFO) and match float64 to the SGEMM bound;
+    with GEN9BLAS_BLAS=cpu the same program runs them on the CPU BLAS."""
+    prog = U.build_preload_program(tmp_path)
+    plain, _ = U.run_preload_program(prog, preload=False)
+    assert plain["cblas_sgemm"] > 1e-2 and plain["sgemm_"] > 1e-2        # the stub ran (it writes -1)
+    errs, log = U.run_preload_program(prog, preload=True)
+    assert errs["cblas_sgemm"] <= 1e-6 and errs["sgemm_"] <= 1e-6, errs
+    assert "cblas_sgemm -> GPU" in log and "sgemm_ -> GPU" in log, log[-1000:]
+    errs, log = U.run_preload_program(prog, preload=True, extra_env={"GEN9BLAS_BLAS": "cpu"})
+    assert errs["cblas_sgemm"] <= 1e-5 and errs["sgemm_"] <= 1e-5, errs
+    assert "-> GPU" not in log
