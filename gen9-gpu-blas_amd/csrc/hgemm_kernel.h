@@ -38,6 +38,7 @@
 #pragma once
 #include "internal.h"
 #include "lds_dma.h"
+#include <type_traits>
 
 namespace g9 {
 namespace hg {
@@ -164,7 +165,9 @@ __device__ __forceinline__ f32x4 mma(u32x4 b, u32x4 a, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, b), __builtin_bit_cast(f16x8, a), c, 0, 0, 0);
 }
 
-template <int BM, int BN, int WM, int WN, int KB, int NS, bool AK, bool BKC>
+// RA (read-ahead): the main loop reads each k-step's fragments one k-step early (for small wave tiles, whose few
+// MFMAs per k-step cannot cover the LDS read latency inside the k-step).
+template <int BM, int BN, int WM, int WN, int KB, int NS, bool AK, bool BKC, bool RA = false>
 __global__ void __launch_bounds__(WM *WN * 64) hgemm_kernel(Params p) {
     constexpr int NW = WM * WN;
     constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 16, TN = WTN / 16;
@@ -214,13 +217,6 @@ __global__ void __launch_bounds__(WM *WN * 64) hgemm_kernel(Params p) {
 #pragma unroll
         for (int j = 0; j < TM; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    u32x4 ra[2][TM], rb[2][TN];
-    auto read_frags = [&](const G9_LDS unsigned char *stg, int s, int buf) {
-#pragma unroll
-        for (int j = 0; j < TM; j++) ra[buf][j] = fa.read(stg, j, s);
-#pragma unroll
-        for (int i = 0; i < TN; i++) rb[buf][i] = fb.read(stg + ABYTES, i, s);
-    };
     const int nk = p.K / KB;
     // prologue: k-steps 0 .. NS-1 into stages 0 .. NS-1 (past the last k-step, the last one is loaded again into a
     // stage nobody reads, so every k-step issues the same number of loads), then wait for k-step 0
@@ -232,66 +228,130 @@ __global__ void __launch_bounds__(WM *WN * 64) hgemm_kernel(Params p) {
     }
     wait_vm<(NS - 1) * LPS>();
     __syncthreads();
-    read_frags(lds, 0, 0);
 
-    // One k-step: NSUB substeps of TM·TN MFMAs. The instruction order is pinned (sched_barrier between slots):
-    // slot t of a substep holds MFMA t followed by its share of the next substep's fragment reads (in the order the
-    // MFMAs use them); before the last
-    // substep, the wait for k-step kt+1 and the barrier; in the last substep, the reads of k-step kt+1's first
-    // substep and the loads of k-step kt+NS into the stage just released, spread over the MFMA slots.
-    constexpr int NMF = TM * TN;
-    constexpr int NRF = TM + TN;                 // fragments per substep
-    constexpr int NLD = LPS;                     // global→LDS copies per k-step
-    int st = 0;   // stage holding k-step kt
-    for (int kt = 0; kt < nk; kt++) {
-        const G9_LDS unsigned char *cur = lds + st * SBYTES;
-        const int nst = st + 1 == NS ? 0 : st + 1;
+    if constexpr (RA) {
+        // Read-ahead: the fragments of a whole k-step are read one k-step before its MFMAs use them (two register
+        // sets, alternating), so each k-step's LDS reads have all of the previous k-step's MFMAs to arrive. One
+        // barrier per k-step, at its start: after it, k-step kt+1 is in LDS (every wave waited for its own loads
+        // first) and every wave has finished reading k-step kt's stage (its reads were waited for), which then takes
+        // the loads of k-step kt+NS. The k-step loop is unrolled by two so that the register sets are indexed by
+        // constants.
+        u32x4 fa2[2][NSUB][TM], fb2[2][NSUB][TN];
 #pragma unroll
-        for (int s = 0; s < NSUB - 1; s++) {
-            const int nb = (s + 1) & 1;
+        for (int s = 0; s < NSUB; s++) {
 #pragma unroll
-            for (int t = 0; t < NMF; t++) {
-                const int i = t / TM, j = t % TM;
-                acc[i][j] = mma(rb[s & 1][i], ra[s & 1][j], acc[i][j]);
-                constexpr int PER = (NRF + NMF - 1) / NMF;
+            for (int j = 0; j < TM; j++) fa2[0][s][j] = fa.read(lds, j, s);
 #pragma unroll
-                for (int q = t * PER; q < (t + 1) * PER && q < NRF; q++) {   // in order of first use
-                    if (q == 0) rb[nb][0] = fb.read(cur + ABYTES, 0, s + 1);
-                    else if (q <= TM) ra[nb][q - 1] = fa.read(cur, q - 1, s + 1);
-                    else rb[nb][q - TM] = fb.read(cur + ABYTES, q - TM, s + 1);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
+            for (int i = 0; i < TN; i++) fb2[0][s][i] = fb.read(lds + ABYTES, i, s);
         }
-        // k-step kt+1 in LDS: this wave's loads (NS-2 later k-steps may stay in flight) and, after the barrier, every
-        // other wave's; all waves are done reading stage st (lgkmcnt(0) before the barrier) before it is reloaded.
-        wait_vm<(NS - 2) * LPS>();
-        wait_lgkm0();
-        __syncthreads();
-        {
-            constexpr int s = NSUB - 1;
-            const G9_LDS unsigned char *nxt = lds + nst * SBYTES;
+        constexpr int NMF = NSUB * TM * TN, NRD = NSUB * (TM + TN), NIT = NRD + LPS, PER = (NIT + NMF - 1) / NMF;
+        int st = 0;   // stage holding k-step kt
+        auto step = [&](auto cur_c, int kt) {
+            constexpr int cur = decltype(cur_c)::value, nxt = cur ^ 1;
+            const int nst = st + 1 == NS ? 0 : st + 1;
+            wait_vm<(NS - 2) * LPS>();
+            wait_lgkm0();
+            __syncthreads();
+            // the last k-step reads its successor's stage too (unused values, no branch in the schedule)
+            const G9_LDS unsigned char *nx = lds + nst * SBYTES;
             const unsigned dsta = lds_addr + st * SBYTES, dstb = dsta + ABYTES;
-            constexpr int NIT = NRF + NLD, PER = (NIT + NMF - 1) / NMF;
 #pragma unroll
             for (int t = 0; t < NMF; t++) {
-                const int i = t / TM, j = t % TM;
-                acc[i][j] = mma(rb[s & 1][i], ra[s & 1][j], acc[i][j]);
+                const int sub = t / (TM * TN), i = (t % (TM * TN)) / TM, j = t % TM;
+                acc[i][j] = mma(fb2[cur][sub][i], fa2[cur][sub][j], acc[i][j]);
 #pragma unroll
-                for (int q = t * PER; q < (t + 1) * PER && q < NIT; q++) {
-                    if (q == 0) rb[0][0] = fb.read(nxt + ABYTES, 0, 0);
-                    else if (q <= TM) ra[0][q - 1] = fa.read(nxt, q - 1, 0);
-                    else if (q < NRF) rb[0][q - TM] = fb.read(nxt + ABYTES, q - TM, 0);
-                    else if (q - NRF < LA::NI) la.one(q - NRF, dsta, wave);
-                    else lb.one(q - NRF - LA::NI, dstb, wave);
+                for (int q = t * PER; q < (t + 1) * PER && q < NIT; q++) {   // reads in order of first use, then loads
+                    if (q < NRD) {
+                        const int rs = q / (TM + TN), w = q % (TM + TN);
+                        if (w == 0) fb2[nxt][rs][0] = fb.read(nx + ABYTES, 0, rs);
+                        else if (w <= TM) fa2[nxt][rs][w - 1] = fa.read(nx, w - 1, rs);
+                        else fb2[nxt][rs][w - TM] = fb.read(nx + ABYTES, w - TM, rs);
+                    } else if (q - NRD < LA::NI) {
+                        la.one(q - NRD, dsta, wave);
+                    } else {
+                        lb.one(q - NRD - LA::NI, dstb, wave);
+                    }
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
             const bool more = kt + NS + 1 < nk;   // the next issue loads k-step kt+NS+1, if it exists
             la.advance(more);
             lb.advance(more);
+            st = nst;
+        };
+        for (int kt = 0; kt < nk; kt += 2) {
+            step(std::integral_constant<int, 0>{}, kt);
+            if (kt + 1 < nk) step(std::integral_constant<int, 1>{}, kt + 1);
         }
-        st = nst;
+    } else {
+        u32x4 ra[2][TM], rb[2][TN];
+        auto read_frags = [&](const G9_LDS unsigned char *stg, int s, int buf) {
+#pragma unroll
+            for (int j = 0; j < TM; j++) ra[buf][j] = fa.read(stg, j, s);
+#pragma unroll
+            for (int i = 0; i < TN; i++) rb[buf][i] = fb.read(stg + ABYTES, i, s);
+        };
+        read_frags(lds, 0, 0);
+
+        // One k-step: NSUB substeps of TM·TN MFMAs. The instruction order is pinned (sched_barrier between slots):
+        // slot t of a substep holds MFMA t followed by its share of the next substep's fragment reads (in the order the
+        // MFMAs use them); before the last
+        // substep, the wait for k-step kt+1 and the barrier; in the last substep, the reads of k-step kt+1's first
+        // substep and the loads of k-step kt+NS into the stage just released, spread over the MFMA slots.
+        constexpr int NMF = TM * TN;
+        constexpr int NRF = TM + TN;                 // fragments per substep
+        constexpr int NLD = LPS;                     // global→LDS copies per k-step
+        int st = 0;   // stage holding k-step kt
+        for (int kt = 0; kt < nk; kt++) {
+            const G9_LDS unsigned char *cur = lds + st * SBYTES;
+            const int nst = st + 1 == NS ? 0 : st + 1;
+#pragma unroll
+            for (int s = 0; s < NSUB - 1; s++) {
+                const int nb = (s + 1) & 1;
+#pragma unroll
+                for (int t = 0; t < NMF; t++) {
+                    const int i = t / TM, j = t % TM;
+                    acc[i][j] = mma(rb[s & 1][i], ra[s & 1][j], acc[i][j]);
+                    constexpr int PER = (NRF + NMF - 1) / NMF;
+#pragma unroll
+                    for (int q = t * PER; q < (t + 1) * PER && q < NRF; q++) {   // in order of first use
+                        if (q == 0) rb[nb][0] = fb.read(cur + ABYTES, 0, s + 1);
+                        else if (q <= TM) ra[nb][q - 1] = fa.read(cur, q - 1, s + 1);
+                        else rb[nb][q - TM] = fb.read(cur + ABYTES, q - TM, s + 1);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            // k-step kt+1 in LDS: this wave's loads (NS-2 later k-steps may stay in flight) and, after the barrier, every
+            // other wave's; all waves are done reading stage st (lgkmcnt(0) before the barrier) before it is reloaded.
+            wait_vm<(NS - 2) * LPS>();
+            wait_lgkm0();
+            __syncthreads();
+            {
+                constexpr int s = NSUB - 1;
+                const G9_LDS unsigned char *nxt = lds + nst * SBYTES;
+                const unsigned dsta = lds_addr + st * SBYTES, dstb = dsta + ABYTES;
+                constexpr int NIT = NRF + NLD, PER = (NIT + NMF - 1) / NMF;
+#pragma unroll
+                for (int t = 0; t < NMF; t++) {
+                    const int i = t / TM, j = t % TM;
+                    acc[i][j] = mma(rb[s & 1][i], ra[s & 1][j], acc[i][j]);
+#pragma unroll
+                    for (int q = t * PER; q < (t + 1) * PER && q < NIT; q++) {
+                        if (q == 0) rb[0][0] = fb.read(nxt + ABYTES, 0, 0);
+                        else if (q <= TM) ra[0][q - 1] = fa.read(nxt, q - 1, 0);
+                        else if (q < NRF) rb[0][q - TM] = fb.read(nxt + ABYTES, q - TM, 0);
+                        else if (q - NRF < LA::NI) la.one(q - NRF, dsta, wave);
+                        else lb.one(q - NRF - LA::NI, dstb, wave);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                const bool more = kt + NS + 1 < nk;   // the next issue loads k-step kt+NS+1, if it exists
+                la.advance(more);
+                lb.advance(more);
+            }
+            st = nst;
+        }
     }
     wait_vm<0>();   // the loads into stages nobody reads have landed before the wave ends
 
