@@ -86,6 +86,8 @@ def main():
     cal.g9cal_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     cal.g9cal_mfma.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
                                ctypes.c_int, ctypes.c_void_p]
+    cal.g9cal_round_trip_us.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    cal.g9cal_round_trip_us.restype = ctypes.c_double
     lib_stream = ctypes.c_void_p(g9.hip_stream())
     ncu = torch.cuda.get_device_properties(0).multi_processor_count
     p, d = ctypes.c_void_p, ctypes.c_double
@@ -314,8 +316,16 @@ def main():
             pk[f"M{M}"] = hbm_fracs({"us_per_call": round(ms * 1e3, 2), "GBs": round(byts / (ms * 1e-3) / 1e9, 1)})
             log("packed_decode", M, pk[f"M{M}"])
         # gen9blas_gemm_pb_skinny: FP32 activations on the same packed FP16 weights, FP32 result. The call waits for its
-        # kernel (it reports non-finite results), so this time includes the wait and the flag read; the kernel's own
-        # duration is in the rocprofv3 trace (skinny_pb_kernel).
+        # kernel (it reports non-finite results), so this time includes the launch, the wait and the flag read; the
+        # kernel's own duration is in the rocprofv3 trace (skinny_pb_lds_kernel). For scale: the launch-and-wait round
+        # trip of a one-word kernel on the same stream, measured here.
+        touch = torch.zeros(1, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        rt = cal.g9cal_round_trip_us(touch.data_ptr(), 2000, lib_stream)
+        if rt < 0:
+            raise RuntimeError("round-trip probe failed")
+        pk["sync_round_trip_one_word_kernel_us"] = round(rt, 2)
+        log("packed_decode round trip", rt)
         L.gen9blas_gemm_pb_skinny.argtypes = [ctypes.c_int, p, ctypes.c_int, p, p, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
         nfv = ctypes.c_int(0)
         for M in (1, 4, 16):

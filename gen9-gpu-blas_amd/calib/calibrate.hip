@@ -8,6 +8,9 @@
 //   their bits toggle as in a GEMM; FP16 GEMMs on random data run at the board's power limit, and this loop is the
 //   rate the matrix cores sustain there with no data movement at all.
 #include <hip/hip_runtime.h>
+#include <algorithm>
+#include <chrono>
+#include <vector>
 #include <stddef.h>
 
 namespace {
@@ -80,6 +83,11 @@ __global__ void __launch_bounds__(256) mfma16(const f16x8 *src, float *out, int 
     out[t] = s;
 }
 
+// One word written by one lane: the smallest kernel, for the launch-and-wait round trip.
+__global__ void touch(float *out) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) out[0] = 1.f;
+}
+
 }  // namespace
 
 extern "C" {
@@ -102,6 +110,20 @@ __attribute__((visibility("default"))) int g9cal_mfma(int shape, const void *src
     if (shape == 32) hipLaunchKernelGGL(mfma32, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const f16x8 *)src, out, iters);
     else hipLaunchKernelGGL(mfma16, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const f16x8 *)src, out, iters);
     return (int)hipGetLastError();
+}
+
+// Median over `reps` of: launch the one-word kernel on `stream`, then hipStreamSynchronize (µs); < 0 on a HIP error.
+__attribute__((visibility("default"))) double g9cal_round_trip_us(float *out, int reps, void *stream) {
+    if (!out || reps <= 0 || reps > 100000) return -1.0;
+    std::vector<double> t((size_t)reps);
+    for (int i = 0; i < reps; i++) {
+        const auto t0 = std::chrono::steady_clock::now();
+        hipLaunchKernelGGL(touch, dim3(1), dim3(64), 0, (hipStream_t)stream, out);
+        if (hipStreamSynchronize((hipStream_t)stream) != hipSuccess) return -1.0;
+        t[(size_t)i] = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+    }
+    std::sort(t.begin(), t.end());
+    return t[(size_t)reps / 2];
 }
 
 }  // extern "C"

@@ -351,10 +351,13 @@ int gen9blas_gemm_pb_skinny(int M, const float *A, int lda, const gen9blas_packe
     float *cd = (float *)o[1].dev;
     // the LDS-streaming kernel: whole 128-k groups, 16-byte activation rows, 32-bit per-lane offsets
     if (K % 128 == 0 && avec && 16LL * (Bp->ld * 2 + o[0].ld * 4) < (1LL << 32)) {
-        // three stages: deeper rings (6 at M <= 4) measured slower on MI355X
-        if (M <= 4) hipLaunchKernelGGL((skinny_pb_lds_kernel<4, 4, 3>), grid, dim3(4 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
-        else if (M <= 8) hipLaunchKernelGGL((skinny_pb_lds_kernel<8, 4, 3>), grid, dim3(4 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
-        else hipLaunchKernelGGL((skinny_pb_lds_kernel<16, 4, 3>), grid, dim3(4 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
+        // MI355X, 32 packed 4096² copies rotated, µs per synchronous call (a trivial kernel's launch-and-wait round trip
+        // is 11.3 µs of it): M = 1 and 4, 8 waves with two stages 21.7-21.9 (8 waves, three: 22.4-22.9; 4 waves with
+        // three, five: 23.1-24.3; 2 waves with four, eight: 29-31); M = 16, 4 waves with two stages 23.7 (three:
+        // 24.4; 2 waves with four, six: 30.7-31.5). Two waves per SIMD hide each other's ring and LDS waits.
+        if (M <= 4) hipLaunchKernelGGL((skinny_pb_lds_kernel<4, 8, 2>), grid, dim3(8 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
+        else if (M <= 8) hipLaunchKernelGGL((skinny_pb_lds_kernel<8, 8, 2>), grid, dim3(8 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
+        else hipLaunchKernelGGL((skinny_pb_lds_kernel<16, 4, 2>), grid, dim3(4 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
     } else {
         hipLaunchKernelGGL(skinny_pb_kernel, grid, dim3(SPW * 64), 0, stream, M, N, K, ad, o[0].ld, (int)avec, wd, Bp->ld,
                            spw, cd, o[1].ld, (int *)flag);
