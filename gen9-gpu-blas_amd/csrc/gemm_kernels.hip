@@ -1,8 +1,9 @@
 // Host side of the MFMA GEMM: tile configuration per type and dispatch over the transpose layouts.
-// The kernel templates and their design notes are in gemm_kernel.h (every shape and type) and hgemm_kernel.h
-// (FP16, whole tiles, direct global→LDS loads).
+// The kernel templates and their design notes are in gemm_kernel.h (every shape and type), hgemm_kernel.h (FP16,
+// whole tiles, direct global→LDS loads) and sgemm_kernel.h (FP32, whole tiles, direct global→LDS loads).
 #include "gemm_kernel.h"
 #include "hgemm_kernel.h"
+#include "sgemm_kernel.h"
 #include <stdlib.h>
 #include <string.h>
 #include <algorithm>
@@ -209,6 +210,97 @@ static int launch_hgemm_tiles(const GemmCall &c) {
     return launch_hg_layout<false, false>(p, c.count);
 }
 
+// ---------------- FP32 whole-tile kernel ----------------
+// Classes, largest tile first; a product takes the first class whose whole tiles fill the CUs and cover at least
+// 90 % of C. Measured on MI355X (TFLOP/s, sustained, against the general kernel of gemm_kernel.h in the same runs):
+// - 128×256 tiles, 8 waves of 64×64, two stages, sums blocked per 128 k: n = 4096 NN 144.9 (124.6), NT 144.3
+//   (130.8); 8192×8192×2048 144.1 (123.4); 2944×11008×4096 NT β = 0.5 140.0 (127.9). Three stages 142.6, blocks of
+//   32 k 134.3, of 64 k 140.3, of 256 k 142.6; 256×128 tiles 142.7;
+// - 128×128 tiles, 8 waves of 64×32, three stages, 128-k blocks: n = 2048 134.4 (121.4; 4 waves of 64×64: 129.7;
+//   64×64 tiles: 132.4);
+// - 64×64 tiles, 4 waves of 32×32, four stages, 256-k blocks: n = 1024 102.6 (87.7; 128-k blocks 101.9, 32-k blocks
+//   90.9; three stages 94.0, six 93.0, eight 92.2).
+// The rows and columns beyond the whole tiles (an M or N that is not a multiple of the tile) go to the general
+// kernel, each C element still computed by exactly one of the launches.
+template <class T> static int launch_typed(const GemmCall &c);
+struct SgClass { int BM, BN; };
+static constexpr SgClass SG_CLASSES[] = {{128, 256}, {128, 128}, {64, 64}};
+template <int BM, int BN, int WM, int WN, int NS, int BLK, bool AK, bool BKC>
+static int launch_sg(const sg::Params &p0, int count) {
+    sg::Params p = p0;
+    p.tiles_m = p.M / BM;
+    p.tiles_n = p.N / BN;
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)count), block(WM * WN * 64);
+    hipLaunchKernelGGL((sg::sgemm_kernel<BM, BN, WM, WN, NS, AK, BKC, BLK>), grid, block, 0, stream, p);
+    G9_HIP(hipGetLastError());
+    return 0;
+}
+template <bool AK, bool BKC>
+static int launch_sg_layout(const sg::Params &p, int count, int cls) {
+    if (cls == 0) return launch_sg<128, 256, 2, 4, 2, 4, AK, BKC>(p, count);
+    if (cls == 1) return launch_sg<128, 128, 2, 4, 3, 4, AK, BKC>(p, count);
+    return launch_sg<64, 64, 2, 2, 4, 8, AK, BKC>(p, count);
+}
+// The FP32 whole-tile kernel applies to 16-byte aligned operands with 16-byte row strides and K a multiple of 32,
+// unless GEN9BLAS_SGEMM=generic or a forced split-K (GEN9BLAS_SPLITK) asks for the general kernel.
+static bool sgemm_tiles_ok(const GemmCall &c) {
+    static int generic = -1;
+    if (generic < 0) {
+        const char *e = getenv("GEN9BLAS_SGEMM");
+        generic = e && !strcmp(e, "generic");
+    }
+    if (generic || splitk_forced() >= 0 || c.K % 32 || c.count > 65535) return false;
+    const long long es = 4;
+    // each lane's byte offset inside a tile is 32-bit
+    if (c.lda * es * 256 >= (1LL << 32) || c.ldb * es * 256 >= (1LL << 32)) return false;
+    return (uintptr_t)c.A % 16 == 0 && (uintptr_t)c.B % 16 == 0 && (uintptr_t)c.C % 16 == 0 && (c.lda * es) % 16 == 0 &&
+           (c.ldb * es) % 16 == 0 && (c.ldc * es) % 16 == 0 &&
+           (c.count == 1 || ((c.sA * es) % 16 == 0 && (c.sB * es) % 16 == 0 && (c.sC * es) % 16 == 0));
+}
+// The part of an FP32 product in rows [m0, m0 + M) and columns [n0, n0 + N) of C, as a product of its own.
+static GemmCall sub_call(const GemmCall &c, int m0, int M, int n0, int N) {
+    GemmCall s = c;
+    const float *A = reinterpret_cast<const float *>(c.A), *B = reinterpret_cast<const float *>(c.B);
+    s.A = A + (c.tA ? (long long)m0 : (long long)m0 * c.lda);
+    s.B = B + (c.tB ? (long long)n0 * c.ldb : (long long)n0);
+    s.C = reinterpret_cast<float *>(c.C) + (long long)m0 * c.ldc + n0;
+    s.M = M;
+    s.N = N;
+    return s;
+}
+static int launch_sgemm(const GemmCall &c) {
+    if (!sgemm_tiles_ok(c)) return launch_typed<float>(c);
+    int cls = -1, Mi = 0, Ni = 0;
+    for (int k = 0; k < 3 && cls < 0; k++) {
+        const int mi = c.M / SG_CLASSES[k].BM * SG_CLASSES[k].BM, ni = c.N / SG_CLASSES[k].BN * SG_CLASSES[k].BN;
+        const long long tiles = (long long)(mi / SG_CLASSES[k].BM) * (ni / SG_CLASSES[k].BN) * c.count;
+        if (tiles >= num_cus && tiles <= 0x7fffffffLL && (double)mi * ni >= 0.9 * (double)c.M * c.N) {
+            cls = k;
+            Mi = mi;
+            Ni = ni;
+        }
+    }
+    if (cls < 0) return launch_typed<float>(c);
+    sg::Params p;
+    p.A = reinterpret_cast<const float *>(c.A);
+    p.B = reinterpret_cast<const float *>(c.B);
+    p.C = reinterpret_cast<float *>(c.C);
+    p.lda = c.lda; p.ldb = c.ldb; p.ldc = c.ldc;
+    p.sA = c.sA; p.sB = c.sB; p.sC = c.sC;
+    p.M = Mi; p.N = Ni; p.K = c.K;
+    p.tiles_m = p.tiles_n = 0;
+    p.alpha = (float)c.alpha;
+    p.beta = (float)c.beta;
+    const bool ak = !c.tA, bk = c.tB;
+    if (ak && bk) G9_TRY((launch_sg_layout<true, true>(p, c.count, cls)));
+    else if (ak) G9_TRY((launch_sg_layout<true, false>(p, c.count, cls)));
+    else if (bk) G9_TRY((launch_sg_layout<false, true>(p, c.count, cls)));
+    else G9_TRY((launch_sg_layout<false, false>(p, c.count, cls)));
+    if (Ni < c.N) G9_TRY(launch_typed<float>(sub_call(c, 0, Mi, Ni, c.N - Ni)));   // right strip
+    if (Mi < c.M) G9_TRY(launch_typed<float>(sub_call(c, Mi, c.M - Mi, 0, c.N)));  // bottom strip, full width
+    return 0;
+}
+
 template <class T>
 static int launch_typed(const GemmCall &c) {
     using S = typename Mma<T>::Sum;
@@ -353,7 +445,7 @@ int launch_gemm(const GemmCall &c) {
     switch (c.type) {
     case GEN9BLAS_H:
     case GEN9BLAS_HS: return hgemm_tiles_apply(c) ? launch_hgemm_tiles(c) : launch_typed<f16>(c);
-    case GEN9BLAS_S: return launch_typed<float>(c);
+    case GEN9BLAS_S: return launch_sgemm(c);
     case GEN9BLAS_D: return launch_typed<double>(c);
     }
     G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "type %d unavailable", c.type);

@@ -66,10 +66,13 @@ struct Params {
     float alpha, beta;
 };
 
-// Global → LDS loads of one operand tile: RT rows (m or n) × KB k, RT·KB·2 bytes, issued by NW waves.
+// Global → LDS loads of one operand tile: RT rows (m or n) × KB k, RT·KB·2 bytes, issued by NW waves (counted in FP16
+// elements; the FP32 kernel views its operands as FP16 pairs).
 // KC: stored k-contiguous (element (mn, k) at X[mn·ld + k]); otherwise mn-contiguous (element (mn, k) at X[k·ld + mn]).
+// MS: the mn-contiguous swizzle, chunk c of k-row k at c ^ (4·(k & 3)) for the FP16 transposing reads (MS = 0), or at
+// c ^ (8·((k >> 2) & 1)) for the FP32 reads of k-rows k and k + 4 by the two halves of a wave (MS = 1).
 // Each lane's byte offset from the tile origin is fixed for the whole kernel; the wave-uniform origin advances.
-template <int RT, int KB, int NW, bool KC>
+template <int RT, int KB, int NW, bool KC, int MS = 0>
 struct Loader {
     static constexpr int NINST = RT * KB * 2 / 1024;       // 1 KiB instructions per tile
     static constexpr int NI = NINST / NW;                  // per wave
@@ -79,7 +82,8 @@ struct Loader {
                                                                           // instruction
     static_assert(NINST % NW == 0, "tile instructions must divide over the waves");
     static_assert(!KC || (RPIK * NW) % 32 == 0, "k-contiguous swizzle must repeat over a wave's instructions");
-    static_assert(KC || (RT >= 128 && (RPI * NW) % 4 == 0), "mn-contiguous swizzle must repeat over a wave's instructions");
+    static_assert(KC || (RT >= 128 && (RPI * NW) % (MS ? 8 : 4) == 0),
+                  "mn-contiguous swizzle must repeat over a wave's instructions");
     const char *org;      // wave-uniform: tile origin at the next k-step to load
     unsigned voff;        // this lane's byte offset for instruction 0
     long long step_i;     // bytes between consecutive instructions of this wave
@@ -97,7 +101,7 @@ struct Loader {
         } else {
             // instruction j covers k rows RPI·j ..; lane L: row RPI·j + L / CPR, physical chunk L % CPR
             const int k = RPI * wave + lane / CPR;
-            const int c = (lane % CPR) ^ (4 * (k & 3));
+            const int c = (lane % CPR) ^ (MS ? 8 * ((k >> 2) & 1) : 4 * (k & 3));
             org = reinterpret_cast<const char *>(X + mn0);
             voff = (unsigned)(((long long)k * ld + 8 * c) * 2);
             step_i = (long long)RPI * NW * ld * 2;

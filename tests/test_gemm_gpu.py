@@ -288,6 +288,49 @@ def test_hgemm_whole_tile_kernel(g9, torch_dev, M, N, K, count):
                     assert e.max() <= 2e-3, f"{tag}: max e {e.max():.2e}"
 
 
+@pytest.mark.parametrize("M,N,K,count", [(1024, 1024, 96, 1), (2048, 2048, 64, 1), (4096, 4096, 160, 1),
+                                         (1032, 1092, 64, 1), (512, 512, 64, 4)])
+def test_sgemm_whole_tile_kernel(g9, torch_dev, M, N, K, count):
+    """Shapes served by the FP32 whole-tile kernel (16-byte aligned operands, K a multiple of 32, whole tiles filling
+    the CUs): 64×64 tiles with a k-step count below one 256-k block (n = 1024, K = 96), 128×128 tiles (n = 2048),
+    128×256 tiles with one whole 128-k block and a shorter one (K = 160), 64×64 tiles over the interior of
+    1032×1092 with the 8-row and 4-column strips on the general kernel, and a batch of 4; every transpose layout,
+    through the C ABI on device memory. Small-integer inputs make every result exact (bit-equal to the integer
+    product, so a misplaced element, k row, tile or strip shows up); alpha/beta are then checked against float64 with
+    the SGEMM bound."""
+    import ctypes
+    torch = torch_dev
+    rng = np.random.default_rng(22)
+    for ta in (0, 1):
+        for tb in (0, 1):
+            a = rng.integers(-2, 3, (count, M, K)).astype(np.float32)
+            b = rng.integers(-2, 3, (count, K, N)).astype(np.float32)
+            c0 = rng.uniform(-1, 1, (count, M, N)).astype(np.float32)
+            A = np.ascontiguousarray(a.transpose(0, 2, 1)) if ta else a      # stored K×M when transposed
+            B = np.ascontiguousarray(b.transpose(0, 2, 1)) if tb else b      # stored N×K when transposed
+            Ad, Bd = _to_dev(torch, A), _to_dev(torch, B)
+            ref = np.matmul(a.astype(np.float64), b.astype(np.float64))     # exact: |sums| < 2^24
+            assert np.abs(ref).max() < 2 ** 24
+            for al, be in ((1.0, 0.0), (0.5, -1.5)):
+                Cd = _to_dev(torch, c0 if be else np.full_like(c0, np.nan))  # beta = 0: C must not be read
+                lda, ldb = (M if ta else K), (K if tb else N)
+                rc = g9._lib.gen9blas_gemm_batched(g9.GEN9BLAS_S, ta, tb, M, N, K, al, ctypes.c_void_p(Ad.data_ptr()),
+                                                   lda, M * K, ctypes.c_void_p(Bd.data_ptr()), ldb, K * N, be,
+                                                   ctypes.c_void_p(Cd.data_ptr()), N, M * N, count)
+                assert rc == 0, g9._lib.gen9blas_error()
+                torch.cuda.synchronize()
+                W = Cd.cpu().numpy()
+                tag = f"{M}x{N}x{K}x{count} tA={ta} tB={tb} alpha={al} beta={be}"
+                if be == 0.0:
+                    assert np.array_equal(W.astype(np.float64), ref), tag
+                else:
+                    r64 = al * ref + be * c0.astype(np.float64)
+                    scale = abs(al) * np.matmul(np.abs(a.astype(np.float64)), np.abs(b.astype(np.float64))) + \
+                        abs(be) * np.abs(c0.astype(np.float64))
+                    e = np.abs(W.astype(np.float64) - r64) / scale
+                    assert e.max() <= 1e-6, f"{tag}: max e {e.max():.2e}"
+
+
 def _child(args, extra_env, timeout):
     """Runs tests/long_launch_child.py in a child process with the given variables (read once per process)."""
     import os
