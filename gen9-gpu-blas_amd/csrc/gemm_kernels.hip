@@ -257,6 +257,76 @@ static bool sgemm_tiles_ok(const GemmCall &c) {
            (c.ldb * es) % 16 == 0 && (c.ldc * es) % 16 == 0 &&
            (c.count == 1 || ((c.sA * es) % 16 == 0 && (c.sB * es) % 16 == 0 && (c.sC * es) % 16 == 0));
 }
+// Triangle (TRI) and k-limited (KLIM) modes of the FP32 whole-tile kernel for SYRK / SYR2K / TRMM: one product,
+// whole tiles (the callers check), `tiles` workgroups.
+template <int BM, int BN, int WM, int WN, int NS, int BLK, bool AK, bool BKC, int TRI, int KLIM>
+static int launch_sg_mode(const sg::Params &p0, long long tiles) {
+    sg::Params p = p0;
+    p.tiles_m = p.M / BM;
+    p.tiles_n = p.N / BN;
+    hipLaunchKernelGGL((sg::sgemm_kernel<BM, BN, WM, WN, NS, AK, BKC, BLK, TRI, KLIM>), dim3((unsigned)tiles),
+                       dim3(WM * WN * 64), 0, stream, p);
+    G9_HIP(hipGetLastError());
+    return 0;
+}
+static sg::Params sg_params(const GemmCall &c) {
+    sg::Params p;
+    p.A = reinterpret_cast<const float *>(c.A);
+    p.B = reinterpret_cast<const float *>(c.B);
+    p.C = reinterpret_cast<float *>(c.C);
+    p.lda = c.lda; p.ldb = c.ldb; p.ldc = c.ldc;
+    p.sA = c.sA; p.sB = c.sB; p.sC = c.sC;
+    p.M = c.M; p.N = c.N; p.K = c.K;
+    p.tiles_m = p.tiles_n = 0;
+    p.alpha = (float)c.alpha;
+    p.beta = (float)c.beta;
+    return p;
+}
+// Triangle of an FP32 square product on the whole-tile kernel (NT or TN): 128×128 or 64×64 tiles, whichever fills
+// its last round of one workgroup per CU better (n = 4096: 528 tiles of 128×128 are 2.06 rounds, SYRK 90 TFLOP/s;
+// 2080 of 64×64 fill 90 % of 9 rounds), when the triangle has at least one such tile per CU. Returns false (nothing
+// launched) when neither applies; *rc is the launch's status otherwise.
+template <int TRI, bool AK, bool BKC>
+static bool sg_tri_layout(const GemmCall &c, int *rc) {
+    const sg::Params p = sg_params(c);
+    const long long t128 = (long long)(c.M / 128) * (c.M / 128 + 1) / 2, t64 = (long long)(c.M / 64) * (c.M / 64 + 1) / 2;
+    const auto fill = [](long long t) { return (double)t / (double)(((t + num_cus - 1) / num_cus) * num_cus); };
+    const bool ok128 = c.M % 128 == 0 && t128 >= num_cus, ok64 = c.M % 64 == 0 && t64 >= num_cus;
+    if (ok128 && (!ok64 || fill(t128) >= fill(t64))) *rc = launch_sg_mode<128, 128, 2, 4, 3, 4, AK, BKC, TRI, 0>(p, t128);
+    else if (ok64) *rc = launch_sg_mode<64, 64, 2, 2, 4, 8, AK, BKC, TRI, 0>(p, t64);
+    else return false;
+    return true;
+}
+static bool sg_tri(const GemmCall &c, bool lower, int *rc) {
+    if (c.M != c.N || c.count != 1 || !sgemm_tiles_ok(c)) return false;
+    if (!c.tA && c.tB) return lower ? sg_tri_layout<1, true, true>(c, rc) : sg_tri_layout<2, true, true>(c, rc);
+    if (c.tA && !c.tB) return lower ? sg_tri_layout<1, false, false>(c, rc) : sg_tri_layout<2, false, false>(c, rc);
+    return false;
+}
+// k-limited FP32 NN product on the whole-tile kernel (TRMM): the plain products' classes, whole tiles only.
+template <int KLIM>
+static bool sg_klim_mode(const GemmCall &c, int *rc) {
+    const sg::Params p = sg_params(c);
+    const long long t0 = (long long)(c.M / 128) * (c.N / 256), t1 = (long long)(c.M / 128) * (c.N / 128),
+                    t2 = (long long)(c.M / 64) * (c.N / 64);
+    if (c.M % 128 == 0 && c.N % 256 == 0 && t0 >= num_cus) *rc = launch_sg_mode<128, 256, 2, 4, 2, 4, true, false, 0, KLIM>(p, t0);
+    else if (c.M % 128 == 0 && c.N % 128 == 0 && t1 >= num_cus) *rc = launch_sg_mode<128, 128, 2, 4, 3, 4, true, false, 0, KLIM>(p, t1);
+    else if (c.M % 64 == 0 && c.N % 64 == 0 && t2 >= num_cus) *rc = launch_sg_mode<64, 64, 2, 2, 4, 8, true, false, 0, KLIM>(p, t2);
+    else return false;
+    return true;
+}
+static bool sg_klim(const GemmCall &c, int klim, int *rc) {
+    // the k range of every tile is non-empty only when K spans the triangular operand's order
+    if (c.count != 1 || c.tA || c.tB || !sgemm_tiles_ok(c) || (klim <= 2 ? c.K != c.M : c.K != c.N)) return false;
+    switch (klim) {
+    case 1: return sg_klim_mode<1>(c, rc);
+    case 2: return sg_klim_mode<2>(c, rc);
+    case 3: return sg_klim_mode<3>(c, rc);
+    case 4: return sg_klim_mode<4>(c, rc);
+    }
+    return false;
+}
+
 // The part of an FP32 product in rows [m0, m0 + M) and columns [n0, n0 + N) of C, as a product of its own.
 static GemmCall sub_call(const GemmCall &c, int m0, int M, int n0, int N) {
     GemmCall s = c;
@@ -380,7 +450,10 @@ int launch_gemm_tri(const GemmCall &c, bool lower) {
     switch (c.type) {
     case GEN9BLAS_H:
     case GEN9BLAS_HS: return launch_tri_typed<f16>(c, lower);
-    case GEN9BLAS_S: return launch_tri_typed<float>(c, lower);
+    case GEN9BLAS_S: {
+        int rc = 0;
+        return sg_tri(c, lower, &rc) ? rc : launch_tri_typed<float>(c, lower);
+    }
     case GEN9BLAS_D: return launch_tri_typed<double>(c, lower);
     }
     G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "type %d unavailable", c.type);
@@ -435,7 +508,10 @@ int launch_gemm_klim(const GemmCall &c, int klim) {
     switch (c.type) {
     case GEN9BLAS_H:
     case GEN9BLAS_HS: return launch_klim_typed<f16>(c, klim);
-    case GEN9BLAS_S: return launch_klim_typed<float>(c, klim);
+    case GEN9BLAS_S: {
+        int rc = 0;
+        return sg_klim(c, klim, &rc) ? rc : launch_klim_typed<float>(c, klim);
+    }
     case GEN9BLAS_D: return launch_klim_typed<double>(c, klim);
     }
     G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "type %d unavailable", c.type);

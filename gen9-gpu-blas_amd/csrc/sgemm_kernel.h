@@ -24,6 +24,13 @@
 // - one barrier per k-step, before its last group of MFMAs: after it the wave issues the next stage's loads and its
 //   first fragment reads, then runs the last group;
 // - the workgroup → tile mapping gives each XCD a contiguous range of tiles in groups of 4 tile rows.
+// Two modes serve level-3 routines, as in the general kernel:
+// - TRI (1: lower, 2: upper): C is square, the grid holds only the T(T+1)/2 square tiles that meet the triangle, and
+//   diagonal tiles write only the elements inside it (SYRK, SYR2K);
+// - KLIM: each tile's k range is cut to where a triangular operand is non-zero (NN, TRMM on the explicit triangular
+//   matrix): 1 op(A) lower, k < m0 + BM; 2 op(A) upper, k >= m0; 3 op(B) lower, k >= n0; 4 op(B) upper,
+//   k < n0 + BN. Tiles are dispatched longest range first, without the XCD remap (every XCD gets long and short
+//   tiles alike).
 #pragma once
 #include "hgemm_kernel.h"
 #include <type_traits>
@@ -82,7 +89,7 @@ __device__ __forceinline__ f32x16 mma(unsigned b, unsigned a, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, b), __builtin_bit_cast(float, a), c, 0, 0, 0);
 }
 
-template <int BM, int BN, int WM, int WN, int NS, bool AK, bool BKC, int BLK = 1>
+template <int BM, int BN, int WM, int WN, int NS, bool AK, bool BKC, int BLK = 1, int TRI = 0, int KLIM = 0>
 __global__ void __launch_bounds__(WM *WN * 64) sgemm_kernel(Params p) {
     constexpr int NW = WM * WN, KB = 32;
     constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
@@ -94,6 +101,8 @@ __global__ void __launch_bounds__(WM *WN * 64) sgemm_kernel(Params p) {
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
     static_assert(NS >= 2 && (NS - 1) * LPS < 64, "loads in flight must fit vmcnt");
     static_assert(NS * SBYTES <= 160 * 1024, "stages must fit in LDS");
+    static_assert(TRI == 0 || BM == BN, "triangle mode: square tiles");
+    static_assert(KLIM == 0 || (TRI == 0 && AK && !BKC), "k-limited tiles: NN layout, no triangle");
     __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * SBYTES];
     G9_LDS unsigned char *lds = (G9_LDS unsigned char *)smem;
     const unsigned lds_addr = (unsigned)(uintptr_t)lds;
@@ -102,18 +111,47 @@ __global__ void __launch_bounds__(WM *WN * 64) sgemm_kernel(Params p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave % WM, wn = wave / WM;
 
-    int bid = blockIdx.x;
-    const int nt = p.tiles_m * p.tiles_n, nt8 = nt & ~7;
-    if (bid < nt8) bid = (bid & 7) * (nt8 >> 3) + (bid >> 3);
-    constexpr int GM = 4;
-    const int group = bid / (GM * p.tiles_n), first_m = group * GM;
-    const int gsz = min(p.tiles_m - first_m, GM);
-    const int in_group = bid % (GM * p.tiles_n);
-    const int m0 = (first_m + in_group % gsz) * BM, n0 = (in_group / gsz) * BN;
+    int bid = blockIdx.x, m0, n0;
+    if constexpr (KLIM != 0) {
+        if constexpr (KLIM <= 2) {   // the range depends on the tile row
+            const int tr = bid / p.tiles_n;
+            m0 = (KLIM == 1 ? p.tiles_m - 1 - tr : tr) * BM;
+            n0 = (bid % p.tiles_n) * BN;
+        } else {                     // on the tile column
+            const int tc = bid / p.tiles_m;
+            n0 = (KLIM == 4 ? p.tiles_n - 1 - tc : tc) * BN;
+            m0 = (bid % p.tiles_m) * BM;
+        }
+    } else {
+        const int nt = TRI ? p.tiles_m * (p.tiles_m + 1) / 2 : p.tiles_m * p.tiles_n, nt8 = nt & ~7;
+        if (bid < nt8) bid = (bid & 7) * (nt8 >> 3) + (bid >> 3);
+        if constexpr (TRI != 0) {
+            // tile bid of the lower triangle of tiles, row by row: (tr, tc) with tc <= tr; upper: transposed
+            int tr = (int)((__builtin_sqrtf(8.f * (float)bid + 1.f) - 1.f) * 0.5f);
+            while ((tr + 1) * (tr + 2) / 2 <= bid) tr++;
+            while (tr * (tr + 1) / 2 > bid) tr--;
+            const int tc = bid - tr * (tr + 1) / 2;
+            m0 = (TRI == 1 ? tr : tc) * BM;
+            n0 = (TRI == 1 ? tc : tr) * BN;
+        } else {
+            constexpr int GM = 4;
+            const int group = bid / (GM * p.tiles_n), first_m = group * GM;
+            const int gsz = min(p.tiles_m - first_m, GM);
+            const int in_group = bid % (GM * p.tiles_n);
+            m0 = (first_m + in_group % gsz) * BM;
+            n0 = (in_group / gsz) * BN;
+        }
+    }
+    // k range of this tile (KLIM), a multiple of 32 at both ends
+    int k0 = 0, k1 = p.K;
+    if constexpr (KLIM == 1) k1 = min(p.K, m0 + BM);
+    if constexpr (KLIM == 2) k0 = m0;
+    if constexpr (KLIM == 3) k0 = n0;
+    if constexpr (KLIM == 4) k1 = min(p.K, n0 + BN);
 
     const long long z = blockIdx.y;
-    const hg::f16 *A = reinterpret_cast<const hg::f16 *>(p.A + z * p.sA);
-    const hg::f16 *B = reinterpret_cast<const hg::f16 *>(p.B + z * p.sB);
+    const hg::f16 *A = reinterpret_cast<const hg::f16 *>(p.A + z * p.sA + (AK ? (long long)k0 : (long long)k0 * p.lda));
+    const hg::f16 *B = reinterpret_cast<const hg::f16 *>(p.B + z * p.sB + (BKC ? (long long)k0 : (long long)k0 * p.ldb));
     float *C = p.C + z * p.sC;
 
     LA la;
@@ -159,7 +197,7 @@ __global__ void __launch_bounds__(WM *WN * 64) sgemm_kernel(Params p) {
             for (int j = 0; j < TM; j++) acc[i][j] += part[i][j];
     };
 
-    const int nk = p.K / KB;
+    const int nk = (k1 - k0) / KB;
     // prologue: k-steps 0 .. NS-1 into stages 0 .. NS-1 (past the last k-step, the last one is loaded again into a
     // stage nobody reads, so every k-step issues the same number of loads), then wait for k-step 0
 #pragma unroll
@@ -214,8 +252,10 @@ __global__ void __launch_bounds__(WM *WN * 64) sgemm_kernel(Params p) {
 
     // Epilogue. Lane l holds D[n][m] of tile (i, j) for m = 32j + l % 32 and, in accumulator r, n = 32i + 8·(r / 4)
     // + 4·(l / 32) + r % 4: runs of 4 consecutive n, one 16-byte store each (alpha·acc + beta·C in FP32).
+    // On a diagonal tile of the triangle mode each element inside the triangle is stored on its own.
     const float alpha = p.alpha, beta = p.beta;
     const int h = lane >> 5;
+    const bool diag = TRI != 0 && m0 == n0;
 #pragma unroll
     for (int i = 0; i < TN; i++)
 #pragma unroll
@@ -223,7 +263,17 @@ __global__ void __launch_bounds__(WM *WN * 64) sgemm_kernel(Params p) {
             const int m = m0 + wm * WTM + 32 * j + (lane & 31);
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                float *cp = C + (long long)m * p.ldc + n0 + wn * WTN + 32 * i + 8 * q + 4 * h;
+                const int n = n0 + wn * WTN + 32 * i + 8 * q + 4 * h;
+                float *cp = C + (long long)m * p.ldc + n;
+                if (diag) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (TRI == 1 ? n + e <= m : n + e >= m) {
+                            const float x = alpha * acc[i][j][4 * q + e];
+                            cp[e] = beta != 0.f ? __builtin_fmaf(beta, cp[e], x) : x;
+                        }
+                    continue;
+                }
                 f32x4 o = beta != 0.f ? *reinterpret_cast<const f32x4 *>(cp) : f32x4{0.f, 0.f, 0.f, 0.f};
                 f32x4 v;
 #pragma unroll

@@ -155,3 +155,46 @@ def test_level3_device_operands(g9, torch_dev):
     torch.cuda.synchronize()
     Xr = np.linalg.solve(U, f64(B))
     assert np.abs(Xd.cpu().numpy() - Xr).max() / np.abs(Xr).max() <= 1e-4
+
+
+@pytest.mark.parametrize("N,K", [(1536, 96), (3968, 64)])
+def test_syrk_syr2k_fp32_whole_tiles(g9, N, K):
+    """FP32 SYRK / SYR2K large enough for the whole-tile kernel's triangle mode (N = 1536: 300 tiles of 64×64; N = 3968:
+    496 tiles of 128×128, which fill their last round better than 1953 of 64×64), both triangles and transposes, on small integers (every result exact, so a misplaced tile,
+    a diagonal-tile element written outside the triangle or a lost k-step shows up bit-exactly), alpha 1.5, beta 0.5 on
+    an integer C; the other triangle unchanged."""
+    rng = np.random.default_rng(6)
+    for uplo in "LU":
+        mask = np.tril(np.ones((N, N), bool)) if uplo == "L" else np.triu(np.ones((N, N), bool))
+        for tr in (False, True):
+            A = rng.integers(-2, 3, (K, N) if tr else (N, K)).astype(np.float32)
+            B = rng.integers(-2, 3, (K, N) if tr else (N, K)).astype(np.float32)
+            C0 = rng.integers(-4, 5, (N, N)).astype(np.float32)
+            oA, oB = (f64(A).T, f64(B).T) if tr else (f64(A), f64(B))
+            W = g9.syrk(A, uplo, tr, 1.5, 0.5, C0.copy())
+            assert np.array_equal(f64(W)[mask], (1.5 * oA @ oA.T + 0.5 * f64(C0))[mask]), f"syrk {uplo} t={tr}"
+            assert np.array_equal(W[~mask], C0[~mask]), "syrk changed the other triangle"
+            W = g9.syr2k(A, B, uplo, tr, 1.5, 0.5, C0.copy())
+            assert np.array_equal(f64(W)[mask], (1.5 * (oA @ oB.T + oB @ oA.T) + 0.5 * f64(C0))[mask]), f"syr2k {uplo} t={tr}"
+            assert np.array_equal(W[~mask], C0[~mask]), "syr2k changed the other triangle"
+
+
+@pytest.mark.parametrize("M,N,full", [(1024, 1024, True), (2048, 4096, False)])
+def test_trmm_fp32_whole_tiles(g9, M, N, full):
+    """FP32 TRMM large enough for the whole-tile kernel's k-limited mode (1024²: 64×64 tiles, every side, triangle,
+    transpose and diagonal; 2048×4096: 128×256 tiles, left side), on small integers: every result exact."""
+    rng = np.random.default_rng(7)
+    for side in ("LR" if full else "L"):
+        for uplo in "LU":
+            for ta in ((False, True) if full else (False,)):
+                for dg in ((False, True) if full else (False,)):
+                    n = M if side == "L" else N
+                    A = rng.integers(-2, 3, (n, n)).astype(np.float32)
+                    B = rng.integers(-2, 3, (M, N)).astype(np.float32)
+                    T = np.tril(f64(A)) if uplo == "L" else np.triu(f64(A))
+                    if dg:
+                        np.fill_diagonal(T, 1.0)
+                    T = T.T if ta else T
+                    W = g9.trmm(A, B, side, uplo, ta, dg, 1.5)
+                    P = T @ f64(B) if side == "L" else f64(B) @ T
+                    assert np.array_equal(f64(W), 1.5 * P), f"trmm {side}{uplo} tA={ta} diag={dg}"
