@@ -119,10 +119,11 @@ def test_gemm_config_sizes(g9, orc, torch_dev, kind, n):
 @pytest.mark.parametrize("K", [1000, 1024])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
 def test_sgemm_two_group_tiles(g9, orc, torch_dev, ta, tb, K):
-    """FP32 products whose 128×128 tiles fill whole rounds of CUs take 128×128 tiles with two k groups: 2000×2048
-    (256 tiles, edge tiles in m), alpha = 1.5, beta = 0.5, every layout, against float64 on sampled rows. K = 1000 is
-    not a multiple of the groups' 64-k step, so the second group's last block tile is partly past K and every tile
-    takes the checked loop; with K = 1024 the interior tiles take the unchecked fast loop in every layout."""
+    """2000×2048 FP32 products, alpha = 1.5, beta = 0.5, every layout, against float64 on sampled rows. K = 1000 (not a
+    multiple of 32) takes the general kernel's 128×128 tiles with two k groups, whose second group's last block tile
+    is partly past K, so every tile takes the checked loop; K = 1024 takes the FP32 whole-tile kernel on the
+    1984×2048 interior (64×64 tiles) and the general kernel on the 16-row bottom strip. The general kernel's
+    unchecked two-group loop at K = 1024 is covered by test_sgemm_generic_two_group_fast_loop."""
     torch = torch_dev
     M, N = 2000, 2048
     a = orc.uniform((K, M) if ta else (M, K), np.float32, orc.SEED_A)
@@ -135,6 +136,36 @@ def test_sgemm_two_group_tiles(g9, orc, torch_dev, ta, tb, K):
     mean, mx = _sampled_rows_error(W, opA, b, rows, 1.5, 0.5, c0, tB=bool(tb))
     assert mx <= MAX_E["S"], f"tA={ta} tB={tb} K={K}: max e {mx:.2e}"
     assert mean <= MEAN_E["S"], f"tA={ta} tB={tb} K={K}: mean e {mean:.2e}"
+
+
+def test_sgemm_generic_two_group_fast_loop(tmp_path):
+    """GEN9BLAS_SGEMM=generic keeps FP32 on the general kernel: 2000×2048×1024 then takes 128×128 tiles with two k
+    groups, whose interior tiles run the unchecked fast loop, in every layout, alpha = 1.5, beta = 0.5, against
+    float64 (full matrices, the reference metric). Runs in a child process because the variable is read once."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.realpath(__file__)))
+    script = tmp_path / "generic.py"
+    script.write_text(
+        "import sys, numpy as np\n"
+        f"sys.path.insert(0, {os.path.join(root, 'gen9-gpu-blas_amd')!r}); sys.path.insert(0, {os.path.join(root, 'oracle')!r})\n"
+        "import gen9blas as g, oracle as o\n"
+        "rng = np.random.default_rng(9)\n"
+        "M, N, K = 2000, 2048, 1024\n"
+        "for ta in (0, 1):\n"
+        "    for tb in (0, 1):\n"
+        "        u = rng.uniform(-1, 1, (M, K)).astype(np.float32); v = rng.uniform(-1, 1, (K, N)).astype(np.float32)\n"
+        "        c0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)\n"
+        "        U = np.ascontiguousarray(u.T).T if ta else u; V = np.ascontiguousarray(v.T).T if tb else v\n"
+        "        W = g.gemm(U, V, 1.5, 0.5, c0.copy())\n"
+        "        mean, mx = o.gemm_error(W, u, v, 1.5, 0.5, c0)\n"
+        "        assert mx <= 1e-6 and mean <= 1e-6, (ta, tb, mean, mx)\n"
+        "print('ok')\n")
+    env = dict(os.environ)
+    env["GEN9BLAS_SGEMM"] = "generic"
+    r = subprocess.run([sys.executable, str(script)], env=env, capture_output=True, text=True, timeout=200)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stderr[-2000:]
 
 
 def test_sgemm_odd_shape(g9, orc, torch_dev):
