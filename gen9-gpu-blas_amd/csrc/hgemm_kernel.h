@@ -331,6 +331,10 @@ __global__ void __launch_bounds__(WM *WN * 64) hgemm_kernel(Params p) {
             wait_vm<(NS - 2) * LPS>();
             wait_lgkm0();
             __syncthreads();
+            // the substep after the barrier runs at raised wave priority, so the MFMAs of the wave that leaves the
+            // barrier first issue ahead of the other wave's (n = 4096 1343-1350 → 1356-1358, n = 2048 860-863 →
+            // 869-872 TFLOP/s; raised before the barrier instead, or for the whole k-step: 1335-1348)
+            __builtin_amdgcn_s_setprio(1);
             {
                 constexpr int s = NSUB - 1;
                 const G9_LDS unsigned char *nxt = lds + nst * SBYTES;
@@ -354,6 +358,7 @@ __global__ void __launch_bounds__(WM *WN * 64) hgemm_kernel(Params p) {
                 la.advance(more);
                 lb.advance(more);
             }
+            __builtin_amdgcn_s_setprio(0);
             st = nst;
         }
     }

@@ -233,8 +233,11 @@ __global__ void __launch_bounds__(WM *WN * 64) sgemm_kernel(Params p) {
             const bool more = kt + NS + 1 < nk;   // the next issue loads k-step kt+NS+1, if it exists
             if (!more) { la.org -= la.step_k; lb.org -= lb.step_k; }
         }
+        // the group after the barrier runs at raised wave priority (n = 1024 102.7 → 107.5 TFLOP/s, n = 4096 unchanged)
+        __builtin_amdgcn_s_setprio(1);
         read_group(lds + nst * SBYTES, 0, 0);   // the last k-step reads a stage nobody uses (values unused)
         mfma_group(3, 1, false);
+        __builtin_amdgcn_s_setprio(0);
         if constexpr (b == BLK - 1) add_part();
         st = nst;
     };
