@@ -543,18 +543,24 @@ __device__ __forceinline__ bool needed(const Shape &s, int R0, int br, int C0, i
 }
 
 // x_r -= Σ_{c in [p, p+b)} A(r, c)·x_c for rows r of [r0, r1) (op(A) = A), 32 rows per part: in part vb a wave takes
-// 8 rows, its lanes the block's columns (b ≤ 128: two per lane), then the butterfly sums the 8 rows.
+// 8 rows, its lanes the block's columns (b ≤ BW: BW / 64 per lane), then the butterfly sums the 8 rows. The block's
+// solution x_c is read from xv (xf itself, or the separate solution vector of the inverse-based solve).
 constexpr int UPD_ROWS = 8 * (NT / 64), UPD_COLS = 64;   // rows per part of the two updates
-template <class T, int FMT>
+template <class T, int FMT, int BW = SB>
 __device__ __forceinline__ void update_rows(const Shape &s, const T *__restrict__ a, int p, int b, int r0, int r1,
-                                            typename Comp<T>::R *xf, int vb) {
+                                            typename Comp<T>::R *xf, const typename Comp<T>::R *xv, int vb) {
     using R = typename Comp<T>::R;
-    constexpr int RW = 8;
+    constexpr int RW = 8, NC = BW / 64;
     const int lane = threadIdx.x & 63;
     const int rbase = r0 + (vb * (NT / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * RW;
     if (rbase >= r1) return;
-    const int ca = p + lane, cb = p + 64 + lane;
-    const R x0 = lane < b ? xf[ca] : R(0), x1 = lane + 64 < b ? xf[cb] : R(0);
+    R xc[NC];
+#pragma unroll
+    for (int j = 0; j < NC; j++) xc[j] = lane + 64 * j < b ? xv[p + 64 * j + lane] : R(0);
+    // the butterfly below leaves row rbase + lane / (64 / RW) in the lanes lane % (64 / RW) = 0: its old value is
+    // loaded now, so the subtraction at the end waits for no load (no other workgroup of the launch writes these rows)
+    const int rown = rbase + lane / (64 / RW);
+    const R xold = rown < r1 ? xf[rown] : R(0);
     R t[RW];
 #pragma unroll
     for (int u = 0; u < RW; u++) {
@@ -563,26 +569,35 @@ __device__ __forceinline__ void update_rows(const Shape &s, const T *__restrict_
         stored_range(s, FMT == F_BAND, r, lo, hi);
         if (r >= r1) hi = lo - 1;
         const T *ar = a + row_start<FMT>(s, r);
-        const R e0 = lane < b && ca >= lo && ca <= hi ? (R)ar[ca] : R(0);
-        const R e1 = lane + 64 < b && cb >= lo && cb <= hi ? (R)ar[cb] : R(0);
-        t[u] = fma_r(e1, x1, e0 * x0);
+        R e[NC];
+#pragma unroll
+        for (int j = 0; j < NC; j++) {
+            const int c = p + 64 * j + lane;
+            e[j] = lane + 64 * j < b && c >= lo && c <= hi ? (R)ar[c] : R(0);
+        }
+        t[u] = e[0] * xc[0];
+#pragma unroll
+        for (int j = 1; j < NC; j++) t[u] = fma_r(e[j], xc[j], t[u]);
     }
+    asm volatile("" ::"v"(xold));   // xold's load stays with the others (see upd_rows_full)
     int base = 0;
     butterfly<0, RW>(t, lane, base);
-    if ((lane & (64 / RW - 1)) == 0 && rbase + base < r1) xf[rbase + base] -= t[0];
+    if ((lane & (64 / RW - 1)) == 0 && rbase + base < r1) xf[rbase + base] = xold - t[0];
 }
 
 // x_r -= Σ_{c in [p, p+b)} A(c, r)·x_c for rows r of [r0, r1) (op(A) = Aᵀ), 64 consecutive r per part: each wave
-// takes 32 of the block's rows c (all 32 loads in flight; neighbouring lanes read neighbouring elements of a row of
-// A), then wave 0 adds the 4 sums in wave order. Called by the whole workgroup (two barriers; `red` is free again
-// on return).
-template <class T, int FMT>
+// takes BW / 4 of the block's rows c (all of its loads in flight; neighbouring lanes read neighbouring elements of a
+// row of A), then wave 0 adds the 4 sums in wave order. Called by the whole workgroup (two barriers; `red` is free
+// again on return).
+template <class T, int FMT, int BW = SB>
 __device__ __forceinline__ void update_cols(const Shape &s, const T *__restrict__ a, int p, int b, int r0, int r1,
-                                            typename Comp<T>::R *xf, int vb, typename Comp<T>::R (*red)[64]) {
+                                            typename Comp<T>::R *xf, const typename Comp<T>::R *xv, int vb,
+                                            typename Comp<T>::R (*red)[64]) {
     using R = typename Comp<T>::R;
-    constexpr int G = NT / 64, CW = SB / G;
+    constexpr int G = NT / 64, CW = BW / G;
     const int lane = threadIdx.x & 63, q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = r0 + vb * UPD_COLS + lane;
+    const R xold = q == 0 && r < r1 ? xf[r] : R(0);   // loaded ahead of the sums (only this workgroup writes row r)
     R t = 0;
     if (r < r1) {
         R v[CW];
@@ -595,7 +610,7 @@ __device__ __forceinline__ void update_cols(const Shape &s, const T *__restrict_
         }
 #pragma unroll
         for (int u = 0; u < CW; u++)
-            if (q * CW + u < b) t = fma_r(v[u], xf[p + q * CW + u], t);
+            if (q * CW + u < b) t = fma_r(v[u], xv[p + q * CW + u], t);
     }
     red[q][lane] = t;
     __syncthreads();
@@ -603,7 +618,7 @@ __device__ __forceinline__ void update_cols(const Shape &s, const T *__restrict_
         R sum = red[0][lane];
 #pragma unroll
         for (int w = 1; w < G; w++) sum += red[w][lane];
-        xf[r] -= sum;
+        xf[r] = xold - sum;
     }
     __syncthreads();
 }
@@ -627,8 +642,8 @@ __global__ void __launch_bounds__(NT) solve_step(Shape s, const T *__restrict__ 
     __shared__ R red[NT / 64][64];
     __shared__ R xp[SB], rhs[SB];
     if (blockIdx.x > 0) {
-        if (trans) update_cols<T, FMT>(s, a, pp, pb, o0, o1, xf, blockIdx.x - 1, red);
-        else update_rows<T, FMT>(s, a, pp, pb, o0, o1, xf, blockIdx.x - 1);
+        if (trans) update_cols<T, FMT>(s, a, pp, pb, o0, o1, xf, xf, blockIdx.x - 1, red);
+        else update_rows<T, FMT>(s, a, pp, pb, o0, o1, xf, xf, blockIdx.x - 1);
         return;
     }
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -668,6 +683,229 @@ __global__ void __launch_bounds__(NT) solve_step(Shape s, const T *__restrict__ 
     }
     if (tid < b) rhs[tid] = own - sum;
     d.solve(s, trans, fwd, p, b, rhs, xf, raw);
+}
+
+// ---------------- inverse-based solve (full storage) ----------------
+// In solve order (index g is row g of A forward, n − 1 − g backward, so op(A) becomes lower triangular) the order
+// is cut into blocks of IB rows, q = 0 .. nbI − 1, the last one partial. The diagonal blocks D_q are inverted up
+// front, all at once: their 128-row diagonal blocks in FP64 (one launch), and for IB = 256 the lower-left quadrant
+// −inv(D₂)·C·inv(D₁) by two batched GEMMs; one more batched GEMM forms E_q = inv(D_q)·C_q, C_q being the block of
+// op(A) that couples block q to block q − 1. Step q is x_q = inv(D_q)·r_q − E_q·x_{q−1}, r_q being block q's
+// right-hand side after the updates of blocks ≤ q − 2: two IB × IB matrix-vector products, split over IB / 16
+// workgroups of 16 rows with no synchronisation between them, while the launch's other workgroups apply x_{q−1}
+// to the rows beyond block q (the one-block look-ahead of solve_step). The chain per block is a launch, the loads of
+// 16 rows of inv(D_q) and E_q and a 16-lane sum, where solve_step has the diagonal block's loads, its right-hand
+// side and a 128-step substitution. The solution goes to a second vector xs, since the solving workgroups read r_q
+// from xf while others write x_q. The reference substitutes (level12.c:303-347, level12.cl:493-548); the results
+// differ from substitution by rounding only.
+// Sum over each row of 16 lanes, left in every lane of the row, by DPP moves (quad_perm [1,0,3,2] and [2,3,0,1],
+// row_half_mirror, row_mirror); the order of the additions is fixed, and each lane's sum is the same value.
+__device__ __forceinline__ int dpp_move(int v, int ctrl) {
+    switch (ctrl) {   // the control must be a constant of the instruction
+    case 0: return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    case 1: return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    case 2: return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+    default: return __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+    }
+}
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) v += __builtin_bit_cast(float, dpp_move(__builtin_bit_cast(int, v), c));
+    return v;
+}
+__device__ __forceinline__ double row16_sum(double v) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const long long b = __builtin_bit_cast(long long, v);
+        const int lo = dpp_move((int)b, c), hi = dpp_move((int)(b >> 32), c);
+        v += __builtin_bit_cast(double, (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+    }
+    return v;
+}
+constexpr int INV_MIN = 1024;   // smallest order solved this way
+constexpr int INV_IB = 256;     // rows per block
+constexpr int INV_ROWS = 16;    // rows of x_q per solving workgroup
+
+// 128 × 128 tiles of D_q and C_q, in solve order, into Dg and Cg + q·IB² (row stride IB), zero padded: past the
+// order, D_q holds the identity and C_q zeros, so inv(D_q) and E_q keep the block's rows apart from the padding.
+// Block q = blockIdx.x; blockIdx.y < Q² (Q = IB / 128) is quadrant (y / Q, y % Q) of D_q (diagonal quadrants: the
+// triangle with the diagonal, or ones for a unit diagonal, which is not read; below: dense; above: zeros), the
+// others quadrant y − Q² of C_q (dense; zeros for q = 0). The region of A goes through LDS, read and written
+// coalesced.
+template <class T, int IB>
+__global__ void __launch_bounds__(NT) inv_gather(Shape s, const T *__restrict__ a, int trans, int fwd,
+                                                 typename Comp<T>::R *Dg, typename Comp<T>::R *Cg) {
+    using R = typename Comp<T>::R;
+    constexpr int Q = IB / SB, RPT = SB * SB / NT;
+    __shared__ R tile[SB][SB + 1];
+    const int n = s.nrows, q = blockIdx.x, tid = threadIdx.x, w = tid % SB;
+    const bool coup = blockIdx.y >= Q * Q;
+    const int y = coup ? blockIdx.y - Q * Q : blockIdx.y, qr = y / Q, qc = y % Q;
+    R *out = (coup ? Cg : Dg) + (ll)q * IB * IB + (ll)qr * SB * IB + qc * SB;
+    // mode 0: zeros, 1: dense, 2: lower triangle with the diagonal
+    const int mode = coup ? (q > 0 ? 1 : 0) : (qr == qc ? 2 : qr > qc ? 1 : 0);
+    const int G0 = q * IB + qr * SB, H0 = (coup ? q - 1 : q) * IB + qc * SB;   // solve-order row and column
+    const int kmax = min(max(n - G0, 0), SB), cmax = min(max(n - H0, 0), SB);
+    if (mode == 1 && kmax > 0 && cmax > 0) {
+        // tile[i][j] = A(ar0 + i, ac0 + j): op(A) = A: rows from the tile's rows; op(A) = Aᵀ: from its columns
+        const int gs = fwd ? G0 : n - G0 - kmax, hs = fwd ? H0 : n - H0 - cmax;
+        const int ar0 = trans ? hs : gs, nr = trans ? cmax : kmax, ac0 = trans ? gs : hs, nc = trans ? kmax : cmax;
+        T e[RPT];   // every load in flight before the first store to LDS (addresses clamped into the region)
+#pragma unroll
+        for (int u = 0; u < RPT; u++) {
+            const int i = u * (NT / SB) + tid / SB;
+            e[u] = a[(ll)(ar0 + min(i, nr - 1)) * s.ld + ac0 + min(w, nc - 1)];
+        }
+#pragma unroll
+        for (int u = 0; u < RPT; u++) tile[u * (NT / SB) + tid / SB][w] = (R)e[u];
+    }
+    if (mode == 2 && kmax > 0) {   // the diagonal tile: A rows and columns are the same range
+        const int gs = fwd ? G0 : n - G0 - kmax;
+        T e[RPT];
+#pragma unroll
+        for (int u = 0; u < RPT; u++) {
+            const int i = u * (NT / SB) + tid / SB;
+            e[u] = a[(ll)(gs + min(i, kmax - 1)) * s.ld + gs + min(w, kmax - 1)];
+        }
+#pragma unroll
+        for (int u = 0; u < RPT; u++) tile[u * (NT / SB) + tid / SB][w] = (R)e[u];
+    }
+    __syncthreads();
+    const int c = w, ic = fwd ? c : cmax - 1 - c;   // the column's offset in its A range
+    for (int k = tid / SB; k < SB; k += NT / SB) {
+        const int ik = fwd ? k : kmax - 1 - k;
+        R v = R(0);
+        if (k < kmax && c < cmax) {
+            const R e = trans ? tile[ic][ik] : tile[ik][ic];
+            if (mode == 1 || (mode == 2 && c < k)) v = e;
+            else if (mode == 2 && c == k) v = s.unit ? R(1) : e;
+        } else if (mode == 2 && k == c) {
+            v = R(1);
+        }
+        out[(ll)k * IB + c] = v;
+    }
+}
+
+// The updates of the inverse-based solve: x_r −= Σ_c op(A)(r, c)·x_c over a whole previous block c ∈ [p, p + BW)
+// of full storage, for rows r of [r0, r1). Every element they read lies inside the stored triangle (the rows are
+// after the block in solve order), so each lane loads without a condition, from a row clamped into [r0, r1), and
+// all of a wave's loads are in flight at once; results of clamped rows are not stored. op(A) = A: 32 rows per part,
+// a wave per 8 rows, BW / 64 columns per lane, a transposing butterfly over the 8 rows (row rbase + lane / 8 ends in
+// lanes lane % 8 = 0). op(A) = Aᵀ: 64 consecutive rows r per part, each wave BW / 4 of the block's rows c, the 4
+// waves' sums added in wave order by wave 0. No other workgroup of the launch writes rows [r0, r1), so the old
+// values are loaded with the rest.
+template <class T, int BW>
+__device__ __forceinline__ void upd_rows_full(const Shape &s, const T *__restrict__ a, int p, int r0, int r1,
+                                              typename Comp<T>::R *xf, const typename Comp<T>::R *xv, int vb) {
+    using R = typename Comp<T>::R;
+    constexpr int RW = 8, NC = BW / 64;
+    const int lane = threadIdx.x & 63;
+    const int rbase = r0 + (vb * (NT / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * RW;
+    if (rbase >= r1) return;
+    const int rown = rbase + lane / (64 / RW);
+    const R xold = xf[min(rown, r1 - 1)];
+    R xc[NC], e[RW][NC];
+#pragma unroll
+    for (int j = 0; j < NC; j++) xc[j] = xv[p + 64 * j + lane];
+#pragma unroll
+    for (int u = 0; u < RW; u++) {
+        const T *ar = a + (ll)min(rbase + u, r1 - 1) * s.ld + p + lane;
+#pragma unroll
+        for (int j = 0; j < NC; j++) e[u][j] = (R)ar[64 * j];
+    }
+    // keeps the load of xold issued with the others: left alone, the compiler sinks it to the store, one more round
+    // trip at the end of the launch's critical path
+    asm volatile("" ::"v"(xold));
+    R t[RW];
+#pragma unroll
+    for (int u = 0; u < RW; u++) {
+        t[u] = e[u][0] * xc[0];
+#pragma unroll
+        for (int j = 1; j < NC; j++) t[u] = fma_r(e[u][j], xc[j], t[u]);
+    }
+    int base = 0;
+    butterfly<0, RW>(t, lane, base);
+    if ((lane & (64 / RW - 1)) == 0 && rown < r1) xf[rown] = xold - t[0];
+}
+template <class T, int BW>
+__device__ __forceinline__ void upd_cols_full(const Shape &s, const T *__restrict__ a, int p, int r0, int r1,
+                                              typename Comp<T>::R *xf, const typename Comp<T>::R *xv, int vb,
+                                              typename Comp<T>::R (*red)[64]) {
+    using R = typename Comp<T>::R;
+    constexpr int G = NT / 64, CW = BW / G;
+    const int lane = threadIdx.x & 63, q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = r0 + vb * UPD_COLS + lane, rc = min(r, r1 - 1);
+    const R xold = xf[rc];
+    const T *ac = a + (ll)(p + q * CW) * s.ld + rc;
+    R v[CW];
+#pragma unroll
+    for (int u = 0; u < CW; u++) v[u] = (R)ac[(ll)u * s.ld];
+    R t = 0;
+#pragma unroll
+    for (int u = 0; u < CW; u++) t = fma_r(v[u], xv[p + q * CW + u], t);
+    red[q][lane] = t;
+    __syncthreads();
+    if (q == 0 && r < r1) {
+        R sum = red[0][lane];
+#pragma unroll
+        for (int w = 1; w < G; w++) sum += red[w][lane];
+        xf[r] = xold - sum;
+    }
+}
+
+// Step q of the inverse-based solve: block q covers rows [p, p + b) of A, block q − 1 rows [pp, pp + pb) (pb = 0:
+// the first step). Workgroups 0 .. IB / 16 − 1 form 16 rows each of x_q = Di·r_q − Eq·x_{q−1} (16 lanes per row, IB /
+// 16 columns per lane, then a fixed-order butterfly over the 16 lanes) into xs; the others apply x_{q−1} (in xs) to
+// rows [o0, o1) of xf.
+template <class T, int IB>
+__global__ void __launch_bounds__(NT) inv_step(Shape s, const T *__restrict__ a, int trans, int fwd, int pp, int pb, int p,
+                                               int b, int o0, int o1, const typename Comp<T>::R *__restrict__ Di,
+                                               const typename Comp<T>::R *__restrict__ Eq, typename Comp<T>::R *xf,
+                                               typename Comp<T>::R *xs) {
+    using R = typename Comp<T>::R;
+    constexpr int WGS = IB / INV_ROWS, L = NT / INV_ROWS, CPL = IB / L;   // solving workgroups, lanes per row, columns per lane
+    static_assert(L == 16 && CPL % 4 == 0, "16 lanes per row, whole 4-column chunks");
+    __shared__ R red[NT / 64][64];
+    if (blockIdx.x >= WGS) {
+        if (trans) upd_cols_full<T, IB>(s, a, pp, o0, o1, xf, xs, blockIdx.x - WGS, red);
+        else upd_rows_full<T, IB>(s, a, pp, o0, o1, xf, xs, blockIdx.x - WGS);
+        return;
+    }
+    // lane l of a row takes columns 64j + 4l .. 64j + 4l + 3: the 16 lanes of a row read 256 contiguous bytes of
+    // inv(D_q) and E_q per load
+    typedef R R4 __attribute__((ext_vector_type(4)));
+    constexpr int NJ = CPL / 4;
+    const int k = blockIdx.x * INV_ROWS + threadIdx.x / L, l = threadIdx.x % L;
+    R4 dv[NJ], ev[NJ];
+    R rv[NJ][4], xv[NJ][4];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int c0 = 4 * L * j + 4 * l;
+        dv[j] = *reinterpret_cast<const R4 *>(Di + (ll)k * IB + c0);
+        if (pb > 0) ev[j] = *reinterpret_cast<const R4 *>(Eq + (ll)k * IB + c0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            // indices clamped into the blocks (the first step has no previous block: pp = pb = 0, index pp)
+            const int c = c0 + i, cr = min(c, b - 1), cx = min(c, max(pb - 1, 0));
+            rv[j][i] = xf[fwd ? p + cr : p + b - 1 - cr];
+            xv[j][i] = pb > 0 ? xs[fwd ? pp + cx : pp + max(pb - 1 - cx, 0)] : R(0);
+            if (c >= b) rv[j][i] = R(0);
+            if (c >= pb) xv[j][i] = R(0);
+        }
+    }
+    R t = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) t = fma_r(dv[j][i], rv[j][i], t);
+    if (pb > 0) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) t = fma_r(-ev[j][i], xv[j][i], t);
+    }
+    t = row16_sum(t);
+    if (threadIdx.x % L == 0 && k < b) xs[fwd ? p + k : p + b - 1 - k] = t;
 }
 
 // ---------------- launchers ----------------
@@ -769,19 +1007,86 @@ static int launch_rank(int es, int fmt, const Shape &s, double alpha, const void
     });
 }
 
+// Work space of the inverse-based solve for order n: the solution vector, then D (later E), C and the inverses,
+// nbI·IB² each, and the products of the IB = 256 composition, nbI·128².
+template <class R>
+static size_t inv_bytes(int n) {
+    const size_t nbI = (size_t)(n + INV_IB - 1) / INV_IB, m2 = (size_t)INV_IB * INV_IB;
+    return (((size_t)n * sizeof(R) + 255) & ~(size_t)255) + (3 * nbI * m2 + nbI * SB * SB) * sizeof(R);
+}
+// The inverse-based solve of full storage (inv_gather, inv_step) in the work space w (inv_bytes).
+template <class T>
+static int solve_inv(const Shape &s, const T *a, int trans, int fwd, typename Comp<T>::R *xf, void *w) {
+    using R = typename Comp<T>::R;
+    constexpr int IB = INV_IB, QB = IB / SB;
+    const int n = s.nrows, nbI = (n + IB - 1) / IB, type = sizeof(R) == 8 ? GEN9BLAS_D : GEN9BLAS_S;
+    const ll m2 = (ll)IB * IB;
+    R *xs = (R *)w;
+    R *D = (R *)((char *)w + (((size_t)n * sizeof(R) + 255) & ~(size_t)255));
+    R *C = D + nbI * m2, *Di = C + nbI * m2, *Tm = Di + nbI * m2, *E = D;
+    hipLaunchKernelGGL((inv_gather<T, IB>), dim3(nbI, 2 * QB * QB), dim3(NT), 0, stream, s, a, trans, fwd, D, C);
+    G9_HIP(hipGetLastError());
+    // the 128-row diagonal blocks of every D_q, in FP64, into their places in inv(D_q) (zeros above them)
+    G9_TRY(launch_tri_inverse((int)sizeof(R), D, IB, m2, nbI * QB, Di, IB));
+    // count products C_z = alpha·A_z·B_z of M × K by K × N, (row stride, batch stride) of each operand given
+    const auto gemm = [&](int M, int N, int K, double alpha, const R *A, ll lda, ll sA, const R *B, ll ldb, ll sB, R *Cp,
+                          ll ldc, ll sC, int count) {
+        GemmCall g;
+        g.type = type;
+        g.tA = g.tB = 0;
+        g.M = M; g.N = N; g.K = K;
+        g.count = count;
+        g.alpha = alpha;
+        g.beta = 0.0;
+        g.A = A; g.lda = lda; g.sA = sA;
+        g.B = B; g.ldb = ldb; g.sB = sB;
+        g.C = Cp; g.ldc = ldc; g.sC = sC;
+        return launch_gemm(g);
+    };
+    if (QB == 2) {   // lower-left quadrant of inv(D_q) = [I1 0; K I2]⁻¹: −inv(I2)·K·inv(I1), K = D_q's lower-left
+        const ll h = SB, t2 = (ll)SB * SB;
+        G9_TRY(gemm(SB, SB, SB, 1.0, Di + h * (IB + 1), IB, m2, D + h * IB, IB, m2, Tm, SB, t2, nbI));
+        G9_TRY(gemm(SB, SB, SB, -1.0, Tm, SB, t2, Di, IB, m2, Di + h * IB, IB, m2, nbI));
+    }
+    if (nbI > 1) G9_TRY(gemm(IB, IB, IB, 1.0, Di + m2, IB, m2, C + m2, IB, m2, E + m2, IB, m2, nbI - 1));   // E_q, q ≥ 1
+    const int per = trans ? UPD_COLS : UPD_ROWS;
+    for (int q = 0; q < nbI; q++) {
+        const int g0 = q * IB, b = n - g0 < IB ? n - g0 : IB, p = fwd ? g0 : n - g0 - b;
+        int pp = 0, pb = 0, o0 = 0, o1 = 0;
+        if (q > 0) {   // the previous block (always whole) reaches every row after it in solve order
+            pb = IB;
+            pp = fwd ? g0 - IB : n - g0;
+            o0 = fwd ? p + b : 0;
+            o1 = fwd ? n : p;
+        }
+        const unsigned grid = IB / INV_ROWS + (o1 > o0 ? blocks(o1 - o0, per) : 0u);
+        hipLaunchKernelGGL((inv_step<T, IB>), dim3(grid), dim3(NT), 0, stream, s, a, trans, fwd, pp, pb, p, b, o0, o1,
+                           Di + q * m2, E + q * m2, xf, xs);
+        G9_HIP(hipGetLastError());
+    }
+    return 0;
+}
+
 // Solves op(A)·z = x in place. `lower`: op(A) is lower triangular (forward substitution); kb: rows below (forward)
 // or above (backward) a block that op(A) can reach, n for full and packed storage, the band width for a band.
 static int launch_solve(int es, int fmt, const Shape &s, const void *a, int trans, int lower, int kb, void *x, ll ix) {
     return by_type(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
         using R = typename Comp<T>::R;
-        const int n = s.nrows;
-        void *wp;
+        const int n = s.nrows, nb = (n + SB - 1) / SB;
+        const bool inv = fmt == F_FULL && n >= INV_MIN;
+        void *wp, *w2 = nullptr;
         G9_TRY(scratch(SLOT_T, (size_t)n * sizeof(R), &wp));
+        if (inv) G9_TRY(scratch(SLOT_X, inv_bytes<R>(n), &w2));
         R *xf = (R *)wp;
         hipLaunchKernelGGL((to_work<T, R>), dim3(blocks(n, NT)), dim3(NT), 0, stream, n, (const T *)x, ix, xf);
         G9_HIP(hipGetLastError());
-        const int nb = (n + SB - 1) / SB;
+        if (inv) {
+            G9_TRY(solve_inv<T>(s, (const T *)a, trans, lower, xf, w2));
+            hipLaunchKernelGGL((from_work<T, R>), dim3(blocks(n, NT)), dim3(NT), 0, stream, n, (const R *)w2, (T *)x, ix);
+            G9_HIP(hipGetLastError());
+            return 0;
+        }
         G9_TRY(by_fmt(fmt, [&](auto fc) -> int {
             constexpr int FMT = decltype(fc)::value;
             const int per = trans ? UPD_COLS : UPD_ROWS;

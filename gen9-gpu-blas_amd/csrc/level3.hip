@@ -125,77 +125,137 @@ __global__ void __launch_bounds__(256) trsm_store_kernel(const T *Y, T *B, ll ld
 }
 
 constexpr int TRSM_NB = 128;
-// Inverse of the diagonal block bi of L (rows and columns r0 .. r0+b-1, b ≤ TRSM_NB), in FP64, stored in the element
-// type into the inverted diagonal block of lb rows (lb = TRSM_NB or 2·TRSM_NB) that holds it: leaf p = r0 / lb at
-// Inv + p·lb², row stride lb, at row and column offset o = r0 − p·lb. The first 128-block of a leaf also writes zeros
-// right of itself (columns b .. lb−1 of its rows), the leaf's upper-right quadrant. The block is split into 32×32 sub-blocks: the four diagonal sub-blocks
-// are inverted first, thread j forming column j of its sub-block by substitution (X[j][j] = 1 / L[j][j],
-// X[i][j] = −(Σ_{k=j}^{i-1} L[i][k]·X[k][j]) / L[i][i], 8 loads of L in flight per step); the off-diagonal sub-blocks
-// then follow by distance d from the diagonal, X_ij = −inv(L_ii)·Σ_{k=j}^{i-1} L_ik·X_kj (i − j = d), one element per
-// thread at a time. The work per thread is balanced (a single column chain of the whole block would be 8128 FMAs
-// long); the sums differ from plain column substitution in FP64 rounding only. X and the sums live in LDS (154 KiB).
+// Inverse of the diagonal block bi of L (rows and columns r0 .. r0+b-1, b ≤ TRSM_NB, in the leaf p = r0 / lb of lb
+// rows whose element (i, j) is at L[p·bstride + i·ld + j]; the block's entries above the diagonal are zeros in L),
+// in FP64, stored in the element type into the inverted diagonal block of lb rows (lb = TRSM_NB or 2·TRSM_NB) that
+// holds it: leaf p = r0 / lb at Inv + p·lb², row stride lb, at row and column offset o = r0 − p·lb. The first
+// 128-block of a leaf also writes zeros right of itself (columns b .. lb−1 of its rows), the leaf's upper-right
+// quadrant. The block is split into 32×32 sub-blocks: the four diagonal sub-blocks are inverted first, thread j
+// forming column j of its sub-block by substitution (X[j][j] = 1 / L[j][j], X[i][j] = −(Σ_{k=j}^{i-1}
+// L[i][k]·X[k][j]) / L[i][i]) from copies of those sub-blocks in LDS (placed, with one round of loads, in regions of
+// X that are filled only later); the off-diagonal sub-blocks then follow by distance d from the diagonal,
+// X_ij = −inv(L_ii)·Σ_{k=j}^{i-1} L_ik·X_kj (i − j = d): for the sum a thread takes one row of L_i,j..i−1 (all
+// d·32 loads in flight) and 4 columns of X; for the product with inv(L_ii) a 4×4 tile of the result. The work per thread is balanced (a single column chain of the whole block would be
+// 8128 FMAs long); the sums differ from plain column substitution in FP64 rounding only. X and the sums live in LDS
+// (154 KiB).
 template <class T>
-__global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, int n, T *Inv, int lb) {
+__global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, ll ld, ll bstride, int n, T *Inv, int lb) {
     constexpr int S = 32, NSB = TRSM_NB / S;
+    static_assert(NSB == 4, "four diagonal sub-blocks, staged in the lower regions (1,0), (2,0), (3,0), (3,1)");
     __shared__ double X[TRSM_NB][TRSM_NB + 1];
     __shared__ double Sb[NSB - 1][S][S + 1];
     const int bi = blockIdx.x, r0 = bi * TRSM_NB, b = min(TRSM_NB, n - r0), t = threadIdx.x;
-    const T *Lb = L + (ll)r0 * n + r0;   // element (i, j) of the block
-    for (int e = t; e < TRSM_NB * TRSM_NB; e += 256) X[e / TRSM_NB][e % TRSM_NB] = 0.0;
+    const T *Lb = L + (ll)(r0 / lb) * bstride + (ll)(r0 % lb) * (ld + 1);   // element (i, j) of the block at Lb[i·ld + j]
+    // region of X holding the copy of diagonal sub-block s of L until phase d ≥ 1 overwrites it
+    const auto stage_row = [](int s) { return S * (s < 3 ? s + 1 : 3); };
+    const auto stage_col = [](int s) { return S * (s < 3 ? 0 : 1); };
+    {
+        constexpr int PER = NSB * S * S / 256;
+        T v[PER];   // every load in flight, from addresses clamped into the block
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int e = u * 256 + t, sb = e / (S * S), i = sb * S + (e / S) % S, k = sb * S + e % S;
+            v[u] = Lb[(ll)min(i, b - 1) * ld + min(k, b - 1)];
+        }
+        for (int e = t; e < TRSM_NB * TRSM_NB; e += 256) X[e / TRSM_NB][e % TRSM_NB] = 0.0;
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int e = u * 256 + t, sb = e / (S * S), ii = (e / S) % S, kk = e % S;
+            const int i = sb * S + ii, k = sb * S + kk;
+            X[stage_row(sb) + ii][stage_col(sb) + kk] = i < b && k < b ? (double)v[u] : 0.0;
+        }
+    }
     __syncthreads();
     if (t < TRSM_NB && t < b) {
-        const int j = t, e = min(b, (j / S + 1) * S);   // column j of its diagonal sub-block, rows up to e
-        X[j][j] = 1.0 / (double)Lb[(ll)j * n + j];
-        for (int i = j + 1; i < e; i++) {
-            const T *li = Lb + (ll)i * n;
+        // column j of diagonal sub-block sb in registers, rows i (local) at compile-time indices: x_i = 0 above the
+        // diagonal (i < jj), 1 / L(i, i) on it, −(Σ_{k<i} L(i, k)·x_k) / L(i, i) below, for rows inside the block
+        const int j = t, sb = j / S, jj = j % S, nrow = min(b - sb * S, S);
+        const double *Ls = &X[stage_row(sb)][stage_col(sb)];   // L(sb·32 + i, sb·32 + k) at Ls[i·(TRSM_NB + 1) + k]
+        double x[S];
+#pragma unroll
+        for (int i = 0; i < S; i++) {
+            const double *li = Ls + i * (TRSM_NB + 1);
             double s = 0.0;
-            int k = j;
-            for (; k + 8 <= i; k += 8) {
-                T lv[8];
 #pragma unroll
-                for (int u = 0; u < 8; u++) lv[u] = li[k + u];
-#pragma unroll
-                for (int u = 0; u < 8; u++) s = __builtin_fma((double)lv[u], X[k + u][j], s);
-            }
-            for (; k < i; k++) s = __builtin_fma((double)li[k], X[k][j], s);
-            X[i][j] = -s / (double)li[i];
+            for (int k = 0; k < i; k++) s = __builtin_fma(li[k], x[k], s);
+            const double v = i == jj ? 1.0 / li[i] : -s / li[i];
+            x[i] = i < jj || i >= nrow ? 0.0 : v;
         }
+#pragma unroll
+        for (int i = 0; i < S; i++) X[sb * S + i][j] = x[i];
     }
     __syncthreads();
-    for (int d = 1; d < NSB; d++) {
-        const int nblk = NSB - d;   // sub-blocks (j + d, j), j = 0 .. nblk - 1
-        for (int q = t; q < nblk * S * S; q += 256) {
-            const int j = q / (S * S), rr = (q / S) % S, cc = q % S;
-            const int row = (j + d) * S + rr, col = j * S + cc;
-            double s = 0.0;
-            if (row < b && col < b) {
-                const T *li = Lb + (ll)row * n;
-                for (int k = j * S; k < (j + d) * S; k += 8) {
-                    T lv[8];
+    const auto phase = [&](auto dc) {
+        constexpr int d = decltype(dc)::value, nblk = NSB - d, KW = d * S;   // sub-blocks (j + d, j), j < nblk
+        // item it of this thread: sub-block j, row rr, columns cc0 .. cc0 + 3; all items' loads in flight first
+        // (rows and columns clamped into the block: a valid row's columns j·32 .. row − 1 are all below b)
+        T lv[nblk][KW];
 #pragma unroll
-                    for (int u = 0; u < 8; u++) lv[u] = li[k + u];
+        for (int it = 0; it < nblk; it++) {
+            const int q = it * 256 + t, j = q / (S * S / 4), rr = (q / (S / 4)) % S;
+            const T *li = Lb + (ll)min((j + d) * S + rr, b - 1) * ld;
 #pragma unroll
-                    for (int u = 0; u < 8; u++) s = __builtin_fma((double)lv[u], X[k + u][col], s);
+            for (int u = 0; u < KW; u++) lv[it][u] = li[min(j * S + u, b - 1)];
+        }
+#pragma unroll
+        for (int it = 0; it < nblk; it++) {
+            const int q = it * 256 + t, j = q / (S * S / 4), rr = (q / (S / 4)) % S, cc0 = 4 * (q % (S / 4));
+            const int row = (j + d) * S + rr, col0 = j * S + cc0;
+            double sm[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int u = 0; u < KW; u++)
+#pragma unroll
+                for (int m = 0; m < 4; m++) sm[m] = __builtin_fma((double)lv[it][u], X[j * S + u][col0 + m], sm[m]);
+#pragma unroll
+            for (int m = 0; m < 4; m++) Sb[j][rr][cc0 + m] = row < b && col0 + m < b ? sm[m] : 0.0;
+        }
+        __syncthreads();
+        // X_(j+d, j) = −inv(L_(j+d, j+d))·Sb_j: 64 threads per sub-block j, each a 4×4 tile (rows 4·tr.., columns
+        // 4·tc..), 8 LDS reads per 16 FMAs; each element's sum runs over m in ascending order
+        {
+            const int j = t / 64, tr = (t / 8) % 8, tc = t % 8, i = j + d;
+            if (j < nblk) {
+                double acc[4][4] = {};
+#pragma unroll 4
+                for (int m = 0; m < S; m++) {
+                    double av[4], bv[4];
+#pragma unroll
+                    for (int r = 0; r < 4; r++) av[r] = X[i * S + 4 * tr + r][i * S + m];
+#pragma unroll
+                    for (int c = 0; c < 4; c++) bv[c] = Sb[j][m][4 * tc + c];
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+#pragma unroll
+                        for (int c = 0; c < 4; c++) acc[r][c] = __builtin_fma(av[r], bv[c], acc[r][c]);
                 }
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        const int row = i * S + 4 * tr + r, col = j * S + 4 * tc + c;
+                        if (row < b && col < b) X[row][col] = -acc[r][c];
+                    }
             }
-            Sb[j][rr][cc] = s;
         }
         __syncthreads();
-        for (int q = t; q < nblk * S * S; q += 256) {
-            const int j = q / (S * S), rr = (q / S) % S, cc = q % S, i = j + d;
-            const int row = i * S + rr, col = j * S + cc;
-            double x = 0.0;
-#pragma unroll 8
-            for (int m = 0; m < S; m++) x = __builtin_fma(X[row][i * S + m], Sb[j][m][cc], x);
-            if (row < b && col < b) X[row][col] = -x;
-        }
-        __syncthreads();
-    }
+    };
+    phase(std::integral_constant<int, 1>());
+    phase(std::integral_constant<int, 2>());
+    phase(std::integral_constant<int, 3>());
     const int p = r0 / lb, o = r0 - p * lb, w = o == 0 ? lb : b;
     T *out = Inv + (ll)p * lb * lb + (ll)o * lb + o;
-    for (int e = t; e < b * w; e += 256) {
-        const int i = e / w, j = e % w;
-        out[(ll)i * lb + j] = j < b ? (T)X[i][j] : T(0);
+    // thread t writes column t (w ≤ 256) of the block's rows, 8 rows' LDS reads at a time
+    const int jc = min(t, TRSM_NB - 1);
+    if (t < w) {
+        for (int i0 = 0; i0 < b; i0 += 8) {
+            double v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = X[min(i0 + u, TRSM_NB - 1)][jc];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (i0 + u < b) out[(ll)(i0 + u) * lb + t] = t < b ? (T)v[u] : T(0);
+        }
     }
 }
 
@@ -278,6 +338,23 @@ static int tri_product(int type, int lower, int trans, int N, int K, double alph
 }
 
 }  // namespace l3
+
+// The 128-row diagonal blocks of `count` / (lb / 128) lower-triangular leaves of lb rows for the level-2 solves: leaf
+// p's element (i, j) at L[p·bstride + i·ld + j] (es 4: float, 8: double); inverses into Inv as trsm_inv_kernel
+// places them (leaf p at Inv + p·lb², row stride lb, zeros above its first block's inverse).
+int launch_tri_inverse(int es, const void *L, long long ld, long long bstride, int count, void *Inv, int lb) {
+    using namespace l3;
+    const int n = count * TRSM_NB;
+    if (es == 8)
+        hipLaunchKernelGGL((trsm_inv_kernel<double>), dim3(count), dim3(256), 0, stream, (const double *)L, (ll)ld,
+                           (ll)bstride, n, (double *)Inv, lb);
+    else
+        hipLaunchKernelGGL((trsm_inv_kernel<float>), dim3(count), dim3(256), 0, stream, (const float *)L, (ll)ld,
+                           (ll)bstride, n, (float *)Inv, lb);
+    G9_HIP(hipGetLastError());
+    return 0;
+}
+
 }  // namespace g9
 
 using namespace g9;
@@ -445,7 +522,8 @@ int gen9blas_trsm(int type, int side, int uplo, int transA, int diag, int M, int
                            ops[0].ld, (T *)Ld, n, uplo == GEN9BLAS_LOWER, tr, diag != 0, rev);
         hipLaunchKernelGGL((trsm_y_kernel<T>), dim3(grid_for((ll)n * m)), dim3(256), 0, stream, (const T *)ops[1].dev,
                            ops[1].ld, (T *)Yd, n, m, left, rev, (S)alpha);
-        hipLaunchKernelGGL((trsm_inv_kernel<T>), dim3(nbl), dim3(256), 0, stream, (const T *)Ld, n, (T *)Iv, lb);
+        hipLaunchKernelGGL((trsm_inv_kernel<T>), dim3(nbl), dim3(256), 0, stream, (const T *)Ld, (ll)n, (ll)lb * (n + 1),
+                           n, (T *)Iv, lb);
         G9_HIP(hipGetLastError());
         return 0;
     }));

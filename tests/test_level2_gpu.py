@@ -7,7 +7,8 @@ Cases follow the reference's level-2 test (reference: lib/test_level12.py:98-146
 strided and negative-stride vectors; band shapes (M, N, KL, KU) and (n, K) as there. Bounds as there: error relative
 to |alpha|·|op(A)|·|x| + |beta·y|, FP32 1e-6, FP16 2e-3, FP64 1e-13; solutions relative to max|z|: FP32 1e-5,
 FP16 3e-3, FP64 1e-12. Device-resident cases at n = 4096 exercise the multi-block solves and both load paths of the
-product kernel (16-byte rows and an odd row stride).
+product kernel (16-byte rows and an odd row stride); orders below 1024 take the substituting solve, from 1024 up the
+solve on inverted diagonal blocks.
 """
 import numpy as np
 import pytest
@@ -99,6 +100,38 @@ def band_mask(M, N, KL, KU):
 
 def pack(D, uplo):
     return D[np.triu_indices(D.shape[0])] if uplo == "U" else D[np.tril_indices(D.shape[0])]
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("n", [1024, 1100])
+def test_trsv_blocked_inverse(g9, orc, dt, n):
+    """TRSV from order 1024 up runs on inverted diagonal blocks (x_q = inv(D_q)·r_q − E_q·x_(q-1), inverses in FP64):
+    n = 1024 is the smallest such order (8 whole blocks), n = 1100 ends on a partial block of 76 rows, which a
+    backward solve takes first. Both triangles, both transposes, unit and stored diagonals, a negative-stride x, and
+    the unreferenced triangle (and a unit diagonal) filled with huge values, which must not be read into the result."""
+    A = rng.uniform(-1, 1, (n, n)).astype(dt)
+    Ad = f64(A)
+    big = {np.float16: 6e4, np.float32: 1e30, np.float64: 1e300}[dt]
+    for uplo in "LU":
+        other = np.triu(np.ones((n, n), bool), 1) if uplo == "L" else np.tril(np.ones((n, n), bool), -1)
+        for trans in (False, True):
+            for diag in (False, True):
+                if diag:
+                    Ab = (Ad / n).astype(dt)
+                else:
+                    Ab = A.copy()
+                    np.fill_diagonal(Ab, np.where(np.diag(Ad) < 0, -1, 1) * n / 4 + np.diag(Ad))
+                Ob = orc.triangle(f64(Ab), uplo, diag)
+                Ob = Ob.T if trans else Ob
+                Ag = Ab.copy()
+                Ag[other] = big
+                if diag:
+                    np.fill_diagonal(Ag, big)
+                b = vector(n, dt, -1)
+                ref = orc.solve(Ob, f64(b))
+                g9.trsv(Ag, b, uplo=uplo, trans=trans, diag=diag)
+                check(f"trsv {uplo} trans={int(trans)} diag={int(diag)} n={n}", b, ref, np.max(np.abs(ref)),
+                      SOLVE_TOL[dt])
 
 
 @pytest.mark.parametrize("dt", DTYPES)
