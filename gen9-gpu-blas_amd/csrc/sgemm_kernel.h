@@ -31,6 +31,8 @@
 //   matrix): 1 op(A) lower, k < m0 + BM; 2 op(A) upper, k >= m0; 3 op(B) lower, k >= n0; 4 op(B) upper,
 //   k < n0 + BN. Tiles are dispatched longest range first, without the XCD remap (every XCD gets long and short
 //   tiles alike).
+// MSKIP: rows m < p.m_skip of C are computed but not stored (the edge strip of a product shifted up onto rows that
+// the interior tiles already wrote: every load stays inside A, and no C element is written twice).
 #pragma once
 #include "hgemm_kernel.h"
 #include <type_traits>
@@ -49,6 +51,7 @@ struct Params {
     long long lda, ldb, ldc, sA, sB, sC;
     int M, N, K, tiles_m, tiles_n;
     float alpha, beta;
+    int m_skip = 0;   // MSKIP: leading rows of C not stored
 };
 
 // Fragment reads of one operand for a wave's TT tiles of 32 rows (m or n) from wave row w0 (a multiple of 32): per
@@ -89,7 +92,8 @@ __device__ __forceinline__ f32x16 mma(unsigned b, unsigned a, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, b), __builtin_bit_cast(float, a), c, 0, 0, 0);
 }
 
-template <int BM, int BN, int WM, int WN, int NS, bool AK, bool BKC, int BLK = 1, int TRI = 0, int KLIM = 0>
+template <int BM, int BN, int WM, int WN, int NS, bool AK, bool BKC, int BLK = 1, int TRI = 0, int KLIM = 0,
+          bool MSKIP = false>
 __global__ void __launch_bounds__(WM *WN * 64) sgemm_kernel(Params p) {
     constexpr int NW = WM * WN, KB = 32;
     constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
@@ -264,6 +268,7 @@ __global__ void __launch_bounds__(WM *WN * 64) sgemm_kernel(Params p) {
 #pragma unroll
         for (int j = 0; j < TM; j++) {
             const int m = m0 + wm * WTM + 32 * j + (lane & 31);
+            if (MSKIP && m < p.m_skip) continue;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const int n = n0 + wn * WTN + 32 * i + 8 * q + 4 * h;
