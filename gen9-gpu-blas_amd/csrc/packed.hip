@@ -15,6 +15,7 @@
 #include "internal.h"
 #include "gen9blas_ml.h"
 #include "lds_dma.h"
+#include "wave.h"
 #include <new>
 
 struct gen9blas_packed_b {
@@ -239,6 +240,92 @@ __global__ void __launch_bounds__(SKS * 64) skinny_pb_lds_kernel(int M, int N, i
     }
 }
 
+// The same product on the VALU for small M: on the matrix cores a v_mfma_f32_16x16x4_f32 multiplies 16 activation
+// rows whatever M is (N·K/16 of them per call, about 4 µs of issue per SIMD at N = K = 4096), while FP32 FMAs cost
+// N·K·M. Shaped like the FP16 dot-product skinny kernel: a workgroup of KS waves owns RW consecutive weight rows, its
+// waves split K in chunks of 8 k per lane (16 bytes of each weight row, nontemporal, and 32 bytes of each activation
+// row, re-read from L2), every load of NC chunks issued before the first product; each weight is converted to FP32
+// once and multiplied into the MT activation rows (rows past M repeat the last one and are not stored). The RW·MT
+// sums of a lane are reduced across the wave by a transposing butterfly, the KS waves' sums added in LDS in wave
+// order. Requires K % 8 == 0 and 16-byte aligned activation rows (the launcher checks); packed rows hold zeros past
+// K up to their stride.
+template <int MT, int RW, int KS, int NC>
+__global__ void __launch_bounds__(KS * 64) skinny_pb_valu_kernel(int M, int N, int K, const float *__restrict__ A,
+                                                                  long long lda, const _Float16 *__restrict__ W,
+                                                                  long long ldw, float *__restrict__ C, long long ldc,
+                                                                  int *flag) {
+    constexpr int NV = RW * MT;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * RW;
+    const _Float16 *wr[RW];
+    const float *ar[MT];
+#pragma unroll
+    for (int r = 0; r < RW; r++) wr[r] = W + (long long)min(n0 + r, N - 1) * ldw;
+#pragma unroll
+    for (int m = 0; m < MT; m++) ar[m] = A + (long long)min(m, M - 1) * lda;
+    float v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) v[i] = 0.f;
+    constexpr int SUPER = NC * KS * 64 * 8;   // chunk j of lane l: k = k0 + ((j·KS + wv)·64 + l)·8 .. +7
+    const u32x4p zero = {0u, 0u, 0u, 0u};
+    for (int k0 = 0; k0 < K; k0 += SUPER) {
+        u32x4p wq[NC][RW], aq[NC][MT][2];
+#pragma unroll
+        for (int j = 0; j < NC; j++) {
+            const int k = k0 + ((j * KS + wv) * 64 + lane) * 8;
+            const bool in = k < K;
+#pragma unroll
+            for (int r = 0; r < RW; r++)
+                wq[j][r] = in ? __builtin_nontemporal_load(reinterpret_cast<const u32x4p *>(wr[r] + k)) : zero;
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                aq[j][m][0] = in ? *reinterpret_cast<const u32x4p *>(ar[m] + k) : zero;
+                aq[j][m][1] = in ? *reinterpret_cast<const u32x4p *>(ar[m] + k + 4) : zero;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NC; j++)
+#pragma unroll
+            for (int r = 0; r < RW; r++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const unsigned h2 = wq[j][r][e / 2];
+                    const float we = (float)__builtin_bit_cast(_Float16, (unsigned short)(e % 2 ? h2 >> 16 : h2 & 0xffffu));
+#pragma unroll
+                    for (int m = 0; m < MT; m++) {
+                        const unsigned ab = aq[j][m][e / 4][e % 4];
+                        v[r * MT + m] = __builtin_fmaf(we, __builtin_bit_cast(float, ab), v[r * MT + m]);
+                    }
+                }
+    }
+    int base = 0;
+    butterfly<0, NV>(v, lane, base);
+    constexpr int NF = Butterfly<NV>::per_lane;
+    const bool writer = (lane & (Butterfly<NV>::dup - 1)) == 0;
+    __shared__ float part[KS][NV];
+    if (writer)
+#pragma unroll
+        for (int i = 0; i < NF; i++) part[wv][base + i] = v[i];
+    __syncthreads();
+    for (int t = threadIdx.x; t < NV; t += KS * 64) {
+        const int n = n0 + t / MT, m = t % MT;
+        if (n >= N || m >= M) continue;
+        float s = part[0][t];
+#pragma unroll
+        for (int q = 1; q < KS; q++) s += part[q][t];
+        C[(long long)m * ldc + n] = s;
+        if (!__builtin_isfinite(s)) *flag = 1;   // every writer stores the same value
+    }
+}
+
+constexpr int PB_VALU_MAX_M = 4;   // largest M on skinny_pb_valu_kernel
+template <int MT, int RW, int KS, int NC>
+static void launch_pb_valu(int M, int N, int K, const float *A, long long lda, const _Float16 *W, long long ldw, float *C,
+                           long long ldc, int *flag) {
+    hipLaunchKernelGGL((skinny_pb_valu_kernel<MT, RW, KS, NC>), dim3((unsigned)((N + RW - 1) / RW)), dim3(KS * 64), 0,
+                       stream, M, N, K, A, lda, W, ldw, C, ldc, flag);
+}
+
 }  // namespace g9
 
 using namespace g9;
@@ -349,8 +436,16 @@ int gen9blas_gemm_pb_skinny(int M, const float *A, int lda, const gen9blas_packe
     const float *ad = (const float *)o[0].dev;
     const _Float16 *wd = (const _Float16 *)Bp->buf;
     float *cd = (float *)o[1].dev;
-    // the LDS-streaming kernel: whole 128-k groups, 16-byte activation rows, 32-bit per-lane offsets
-    if (K % 128 == 0 && avec && 16LL * (Bp->ld * 2 + o[0].ld * 4) < (1LL << 32)) {
+    // small M on the VALU (whole 8-k chunks, 16-byte activation rows). MI355X, 32 packed 4096² copies rotated, µs per
+    // synchronous call against the matrix-core kernel below: M = 1 19.0 against 21.6 (2 rows per workgroup, 4 waves;
+    // 1-8 rows, 2-8 waves, 1-4 chunks swept), M = 2 20.0 against 21.6 (4 rows, 8 waves), M = 4 21.5 against 21.9
+    // (8 rows, 8 waves); M = 8 on the VALU 25.9-44 against 22.5
+    if (M <= PB_VALU_MAX_M && K % 8 == 0 && avec) {
+        if (M <= 1) launch_pb_valu<1, 2, 4, 1>(M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
+        else if (M <= 2) launch_pb_valu<2, 4, 8, 1>(M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
+        else launch_pb_valu<4, 8, 8, 1>(M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
+    } else if (K % 128 == 0 && avec && 16LL * (Bp->ld * 2 + o[0].ld * 4) < (1LL << 32)) {
+        // the LDS-streaming kernel: whole 128-k groups, 16-byte activation rows, 32-bit per-lane offsets
         // MI355X, 32 packed 4096² copies rotated, µs per synchronous call (a trivial kernel's launch-and-wait round trip
         // is 11.3 µs of it): M = 1 and 4, 8 waves with two stages 21.7-21.9 (8 waves, three: 22.4-22.9; 4 waves with
         // three, five: 23.1-24.3; 2 waves with four, eight: 29-31); M = 16, 4 waves with two stages 23.7 (three:
