@@ -7,7 +7,7 @@ Cases follow the reference's level-2 test (reference: lib/test_level12.py:98-146
 strided and negative-stride vectors; band shapes (M, N, KL, KU) and (n, K) as there. Bounds as there: error relative
 to |alpha|·|op(A)|·|x| + |beta·y|, FP32 1e-6, FP16 2e-3, FP64 1e-13; solutions relative to max|z|: FP32 1e-5,
 FP16 3e-3, FP64 1e-12. Device-resident cases at n = 4096 exercise the multi-block solves and both load paths of the
-product kernel (16-byte rows and an odd row stride); orders below 1024 take the substituting solve, from 1024 up the
+product kernel (16-byte rows and an odd row stride); orders below 1280 take the substituting solve, from 1280 up the
 solve on inverted diagonal blocks.
 """
 import numpy as np
@@ -103,12 +103,13 @@ def pack(D, uplo):
 
 
 @pytest.mark.parametrize("dt", DTYPES)
-@pytest.mark.parametrize("n", [1024, 1100])
+@pytest.mark.parametrize("n", [1280, 1300])
 def test_trsv_blocked_inverse(g9, orc, dt, n):
-    """TRSV from order 1024 up runs on inverted diagonal blocks (x_q = inv(D_q)·r_q − E_q·x_(q-1), inverses in FP64):
-    n = 1024 is the smallest such order (8 whole blocks), n = 1100 ends on a partial block of 76 rows, which a
-    backward solve takes first. Both triangles, both transposes, unit and stored diagonals, a negative-stride x, and
-    the unreferenced triangle (and a unit diagonal) filled with huge values, which must not be read into the result."""
+    """TRSV from order 1280 up runs on inverted 256-row diagonal blocks (x_q = inv(D_q)·r_q − E_q·x_(q-1), inverses in
+    FP64): n = 1280 is the smallest such order (5 whole blocks), n = 1300 ends on a partial block of 20 rows (the
+    last in solve order, at the start of A for a backward solve). Both triangles, both transposes, unit and stored
+    diagonals, a negative-stride x, and the unreferenced triangle (and a unit diagonal) filled with huge values, which
+    must not be read into the result."""
     A = rng.uniform(-1, 1, (n, n)).astype(dt)
     Ad = f64(A)
     big = {np.float16: 6e4, np.float32: 1e30, np.float64: 1e300}[dt]
