@@ -321,7 +321,7 @@ def test_hgemm_whole_tile_kernel(g9, torch_dev, M, N, K, count):
 
 @pytest.mark.parametrize("M,N,K,count", [(1024, 1024, 96, 1), (2048, 2048, 64, 1), (4096, 4096, 160, 1),
                                          (1032, 1092, 64, 1), (512, 512, 64, 4), (1100, 1536, 96, 1),
-                                         (2100, 4096, 64, 1), (1102, 1536, 64, 2)])
+                                         (2100, 4096, 64, 1), (1102, 1536, 64, 2), (1024, 1024, 320, 1)])
 def test_sgemm_whole_tile_kernel(g9, torch_dev, M, N, K, count):
     """Shapes served by the FP32 whole-tile kernel (16-byte aligned operands, K a multiple of 32, whole tiles filling
     the CUs): 64×64 tiles with a k-step count below one 256-k block (n = 1024, K = 96), 128×128 tiles (n = 2048),
@@ -329,7 +329,8 @@ def test_sgemm_whole_tile_kernel(g9, torch_dev, M, N, K, count):
     1032×1092 with the 8-row and 4-column strips on the general kernel, and a batch of 4. Bottom strips over a width of
     whole 64-column tiles take 64×64 tiles shifted up onto the last 64 rows, storing only the strip's own rows: 12
     rows under 64×64 tiles (1100×1536), 52 rows under 128×256 tiles (2100×4096), and 14 rows (1102×1536, batch of 2)
-    where the shift would misalign a transposed A, so TN and TT keep the general kernel there. Every transpose layout,
+    where the shift would misalign a transposed A, so TN and TT keep the general kernel there; 1024² with K = 320
+    takes 64×64 tiles with 10 k-steps, a block shorter than the 8-step sum blocks after a whole one. Every transpose layout,
     through the C ABI on device memory. Small-integer inputs make every result exact (bit-equal to the integer
     product, so a misplaced element, k row, tile or strip shows up); alpha/beta are then checked against float64 with
     the SGEMM bound."""
