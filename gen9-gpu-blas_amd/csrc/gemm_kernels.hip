@@ -114,7 +114,8 @@ static int launch_layout(const GemmParams<typename Mma<T>::Sum> &p, int count) {
         // split-K pass. Measured (TFLOP/s, against the small tiles with split-K): FP32 NN n = 1024 71 → 82, TN 68 → 77,
         // n = 1000 38 → 56, 1024² × K 4096 81 → 98; FP64 n = 1024 44 → 52, n = 1536 38 → 48, 128×4096×128 (the
         // triangular solve's block products) 8.6 → 15.8. FP32 above num_cus tiles loses (n = 1280: 74 → 70), FP64
-        // does not.
+        // does not. Other FP64 shapes measured at n = 1024 / 1536 against 53.6 / 48.1: four k groups of 2×2 waves
+        // 54.0 / 45.1, four of one 64×64 wave 41.9 / 34.9, two of 1×2 waves 48.7, four of 2×1 waves 51.1.
         if constexpr (sizeof(T) >= 4) {
             const long long t64 = (long long)((p.M + 63) / 64) * ((p.N + 63) / 64) * count;
             if (splitk_forced() < 0 && t64 * 2 >= num_cus && (sizeof(T) == 8 || t64 <= num_cus))
