@@ -80,6 +80,15 @@ constexpr int NT = 256;
 // Rows per batch: 8 with 16 bytes per lane (V > 1: a wave has 8 KiB of loads outstanding), 16 with one element per
 // lane. From a sweep at n = 16384 FP32 (SYMV / TRMV / SPMV): 8 and 16 rows, 8 to 128 workgroups per CU.
 template <int V> constexpr int UB = V > 1 ? 8 : 16;
+// 16 bytes of a row from p: full storage keeps 16-byte aligned rows (nontemporal: the matrix is read once); band and
+// packed rows are only element-aligned, a 16-byte load that the GPU serves at any 4-byte alignment (the compiler
+// emits the same global_load_dwordx4 for a 4-byte-aligned 16-byte copy).
+template <int FMT> __device__ __forceinline__ u32x4 row16(const void *p) {
+    if constexpr (FMT == F_FULL) return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    u32x4 t;
+    __builtin_memcpy(&t, p, 16);
+    return t;
+}
 template <class T, int V, int FMT>
 __global__ void __launch_bounds__(NT) mv_kernel(Shape s, const T *__restrict__ a, const T *__restrict__ x, ll ix, int rpp, int dirs,
                                                 int skipdiag, typename Comp<T>::R *P, typename Comp<T>::R *Q) {
@@ -145,7 +154,7 @@ __global__ void __launch_bounds__(NT) mv_kernel(Shape s, const T *__restrict__ a
                 const T *ar = a + row_start<FMT>(s, r);
                 if constexpr (V > 1) {
                     if (c0 <= hi && c0 + V - 1 >= lo && c0 + V <= s.ncols) {
-                        const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(ar + c0));
+                        const u32x4 t = row16<FMT>(ar + c0);
                         __builtin_memcpy(el[u], &t, 16);
                     } else {
 #pragma unroll
@@ -182,7 +191,7 @@ __global__ void __launch_bounds__(NT) mv_kernel(Shape s, const T *__restrict__ a
         for (int u = 0; u < U; u++) {
             const T *ar = a + row_start<FMT>(s, i + u) + c0;
             if constexpr (V > 1) {
-                const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(ar));
+                const u32x4 t = row16<FMT>(ar);
                 __builtin_memcpy(el[u], &t, 16);
             } else {
                 el[u][0] = *ar;
@@ -951,7 +960,11 @@ static int launch_mv(int es, int fmt, const Shape &s, const void *a, const void 
     return by_type(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
         using R = typename Comp<T>::R;
-        const bool vec = fmt == F_FULL && (uintptr_t)a % 16 == 0 && (s.ld * (ll)sizeof(T)) % 16 == 0;
+        // 16 bytes per lane: full storage with 16-byte aligned rows; packed storage of 4- and 8-byte elements, whose rows
+        // are element-aligned only (row16)
+        const bool packed = fmt == F_PACKL || fmt == F_PACKU;
+        const bool vec = fmt == F_FULL ? (uintptr_t)a % 16 == 0 && (s.ld * (ll)sizeof(T)) % 16 == 0
+                                       : packed && sizeof(T) >= 4 && (uintptr_t)a % sizeof(T) == 0;
         const int V = vec ? VW<T> : 1, gw = 64 * V;
         ll parts, rpp;
         const ll groups = grid_2d(s, V, parts, rpp);
@@ -964,7 +977,7 @@ static int launch_mv(int es, int fmt, const Shape &s, const void *a, const void 
         const dim3 grid((unsigned)groups, (unsigned)parts);
         G9_TRY(by_fmt(fmt, [&](auto fc) -> int {
             constexpr int FMT = decltype(fc)::value;
-            if constexpr (FMT == F_FULL) {
+            if constexpr (FMT == F_FULL || ((FMT == F_PACKL || FMT == F_PACKU) && sizeof(T) >= 4)) {
                 if (vec) {
                     hipLaunchKernelGGL((mv_kernel<T, VW<T>, FMT>), grid, dim3(NT), 0, stream, s, ap, xp, ix, (int)rpp, dirs,
                                        skipdiag, P, Q);
