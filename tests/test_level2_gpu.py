@@ -251,6 +251,33 @@ def test_level2_device_n4096(g9, orc, torch_dev, dt, odd_ld):
         check(f"spmv {uplo}", g9.spmv(torch.from_numpy(Ap).cuda(), xd, uplo=uplo).cpu().numpy(), ref, scale, TOL[dt])
 
 
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_packed_products_unaligned_device(g9, orc, torch_dev, dt):
+    """Packed-storage products read 16 bytes per lane from rows that are only element-aligned: here the packed matrix
+    starts one element into its device buffer (4 or 8 bytes off a 16-byte boundary), n = 1500 so that whole column
+    groups take the unchecked path; SPMV and TPMV in both triangles against the oracle."""
+    torch = torch_dev
+    n = 1500
+    Dp = f64(rng.uniform(-1, 1, (n, n)).astype(dt))
+    x = vector(n, dt, 1)
+    xd = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    for uplo in "LU":
+        Tp = orc.triangle(Dp, uplo)
+        Ap = pack(Tp, uplo).astype(dt)
+        buf = torch.zeros(Ap.size + 1, dtype=torch.float32 if dt == np.float32 else torch.float64, device="cuda")
+        buf[1:] = torch.from_numpy(Ap).cuda()
+        Apd = buf[1:]
+        assert Apd.data_ptr() % 16 != 0
+        ref, scale = orc.mv(orc.symmetric(Tp, uplo), x)
+        check(f"spmv unaligned {uplo}", g9.spmv(Apd, xd, uplo=uplo).cpu().numpy(), ref, scale, TOL[dt])
+        for tr in (False, True):
+            Op = Tp.T if tr else Tp
+            v = xd.clone()
+            g9.tpmv(Apd, v, uplo=uplo, trans=tr)
+            ref, scale = orc.mv(Op, x)
+            check(f"tpmv unaligned {uplo} trans={tr}", v.cpu().numpy(), ref, scale, TOL[dt])
+
+
 def test_level2_errors(g9):
     """Status codes as in the reference (reference: lib/src/level12.c:267-519): lda < n and band widths are
     INVALID_ARG, a zero increment is INVALID_ARG, an unknown type UNSUPPORTED, an empty problem 0 with nothing
