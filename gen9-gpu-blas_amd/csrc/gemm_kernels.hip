@@ -151,18 +151,19 @@ static int launch_layout(const GemmParams<typename Mma<T>::Sum> &p, int count) {
 //   1.79-1.81; the same 8 waves on 32x32x16 MFMAs: 1166-1176); TN 1249, NT 1339, TT 1267 (32x32x16: 1180-1188);
 // - at least one 128×128 tile per CU: 128×128, 8 waves of 64×32 (2×4), three stages. n = 2048 NN 835 (4 waves of
 //   64×64 with 3 or 4 stages: 798-807; 32x32x16 tiles: 795), NT 845 (767), TN and TT 800-804 (800-802);
-// - fewer 128×128 tiles than CUs, with A k-contiguous: 32×128 tiles, 4 waves of 32×32, three stages, fragments read
-//   one k-step ahead: n = 1024 NN 385-386, NT 385 (reading inside the k-step: 369-371 and 363; four stages 359-370,
+// - fewer 128×128 tiles than CUs, with A k-contiguous: 64×64 tiles (below); before them 32×128 tiles, 4 waves of
+//   32×32, three stages, fragments read one k-step ahead: n = 1024 NN 385-386, NT 385 (reading inside the k-step:
+//   369-371 and 363; four stages 359-370,
 //   two 288-312; two k groups of 4 waves on separate rings, their sums added through LDS: 335-340; 32x32x16: 346).
 //   Time per call against K at M = N = 1024 is about 2-3 µs plus 0.26 µs per k-step of 64 (8 MFMAs per wave), so
 //   the k-step's latency chain (LDS reads, barrier), not its MFMAs, sets the rate; the read-ahead takes the LDS
 //   reads off that chain. The 32-row tile needs A k-contiguous (the transposed-A loader reads 128-row tiles).
 //   At n = 2048 (128×128 tiles) the read-ahead gives nothing (841-849 against 849-853): that size runs at the power
 //   limit (1.8-2.0 GHz).
-// - the same small products with B k-contiguous (NT): 64×64 tiles, 4 waves of 32×32, three stages, read-ahead: n = 1024
-//   399.9 against 385.9 for 32×128 (four stages 390.6, two 303.6, no read-ahead 378.1). Per k-step a CU moves 16 KiB
-//   from L2 into LDS instead of 20 KiB for the same flops; at n = 1024 the 256 CUs together pull about 20 TB/s. The
-//   transposed-B loader (NN) needs 128-wide rows, so NN keeps 32×128.
+// - the same small products on 64×64 tiles, 4 waves of 32×32, three stages, read-ahead: NT n = 1024 399.9 against
+//   385.9 for 32×128 (four stages 390.6, two 303.6, no read-ahead 378.1); NN 400.7 against 382.8 (four stages 394.2),
+//   its 64-wide mn-contiguous B rows swizzled by mnswz (hgemm_kernel.h). Per k-step a CU moves 16 KiB from L2 into
+//   LDS instead of 20 KiB for the same flops; at n = 1024 the 256 CUs together pull about 20 TB/s.
 template <int BM, int BN, int WM, int WN, int KB, int NS, bool AK, bool BKC, bool RA = false>
 static int launch_hg(const hg::Params &p0, int count) {
     hg::Params p = p0;
@@ -177,12 +178,10 @@ template <bool AK, bool BKC>
 static int launch_hg_layout(const hg::Params &p, int count) {
     if ((long long)(p.M / 256) * (p.N / 256) * count >= num_cus && p.M % 256 == 0 && p.N % 256 == 0)
         return launch_hg<256, 256, 2, 4, 64, 2, AK, BKC>(p, count);
+    // with A k-contiguous, below one 128×128 tile per CU: 64×64 tiles, 20 % fewer L2 → LDS bytes per flop than the
+    // 32×128 tiles of the same count (n = 1024 NN 382.8 → 400.7, NT 386 → 400 TFLOP/s)
     if constexpr (AK)
-        if ((long long)(p.M / 128) * (p.N / 128) * count < num_cus) {
-            // B k-contiguous (NT) also allows 64×64 tiles: 20 % fewer L2 → LDS bytes per flop than 32×128
-            if constexpr (BKC) return launch_hg<64, 64, 2, 2, 64, 3, AK, BKC, true>(p, count);
-            return launch_hg<32, 128, 1, 4, 64, 3, AK, BKC, true>(p, count);
-        }
+        if ((long long)(p.M / 128) * (p.N / 128) * count < num_cus) return launch_hg<64, 64, 2, 2, 64, 3, AK, BKC, true>(p, count);
     return launch_hg<128, 128, 2, 4, 64, 3, AK, BKC>(p, count);
 }
 // The whole-tile FP16 kernel applies when every operand is 16-byte aligned with 16-byte row strides, M and N are

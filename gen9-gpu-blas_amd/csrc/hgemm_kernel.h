@@ -28,7 +28,8 @@
 // - an mn-contiguous operand (A transposed, B not transposed) is held as KB rows of k, each BM (or BN) elements
 //   long, and read with ds_read_b64_tr_b16, which transposes 16-lane groups: lane j of a group reads 4 consecutive
 //   mn of one k-row, and lane i receives the i-th mn of the group's reads for 4 k-rows. Chunk c of row k sits at
-//   c ^ (4·(k & 3)), so the four rows of a group fall on distinct banks;
+//   c ^ mnswz(k): 4·(k & 3) for rows of 128 or more mn, 4·((k >> 1) & 1) for rows of 64 (8 chunks, two k-rows per
+//   256-byte bank row), so the four rows a group reads fall on distinct banks;
 // - operands are swapped in the MFMA (the B fragment is the first input), so each lane ends with runs of 4
 //   consecutive n of one row of C. n tiles come in pairs whose 16 fragment rows interleave in groups of 4 (rows
 //   4q..4q+3 of the even tile are n 8q..8q+3 of the pair, of the odd tile n 8q+4..8q+7), so a lane's outputs of the
@@ -69,9 +70,13 @@ struct Params {
 // Global → LDS loads of one operand tile: RT rows (m or n) × KB k, RT·KB·2 bytes, issued by NW waves (counted in FP16
 // elements; the FP32 kernel views its operands as FP16 pairs).
 // KC: stored k-contiguous (element (mn, k) at X[mn·ld + k]); otherwise mn-contiguous (element (mn, k) at X[k·ld + mn]).
-// MS: the mn-contiguous swizzle, chunk c of k-row k at c ^ (4·(k & 3)) for the FP16 transposing reads (MS = 0), or at
-// c ^ (8·((k >> 2) & 1)) for the FP32 reads of k-rows k and k + 4 by the two halves of a wave (MS = 1).
+// MS: the mn-contiguous swizzle, chunk c of k-row k at c ^ mnswz<RT>(k) for the FP16 transposing reads (MS = 0), or
+// at c ^ (8·((k >> 2) & 1)) for the FP32 reads of k-rows k and k + 4 by the two halves of a wave (MS = 1).
 // Each lane's byte offset from the tile origin is fixed for the whole kernel; the wave-uniform origin advances.
+template <int RT> __device__ __forceinline__ int mnswz(int k) {
+    static_assert(RT >= 64, "an mn-contiguous row holds at least 8 chunks");
+    return RT >= 128 ? 4 * (k & 3) : 4 * ((k >> 1) & 1);
+}
 template <int RT, int KB, int NW, bool KC, int MS = 0>
 struct Loader {
     static constexpr int NINST = RT * KB * 2 / 1024;       // 1 KiB instructions per tile
@@ -82,7 +87,7 @@ struct Loader {
                                                                           // instruction
     static_assert(NINST % NW == 0, "tile instructions must divide over the waves");
     static_assert(!KC || (RPIK * NW) % 32 == 0, "k-contiguous swizzle must repeat over a wave's instructions");
-    static_assert(KC || (RT >= 128 && (RPI * NW) % (MS ? 8 : 4) == 0),
+    static_assert(KC || ((RT >= 128 || (RT == 64 && MS == 0)) && (RPI * NW) % (MS ? 8 : 4) == 0),
                   "mn-contiguous swizzle must repeat over a wave's instructions");
     const char *org;      // wave-uniform: tile origin at the next k-step to load
     unsigned voff;        // this lane's byte offset for instruction 0
@@ -101,7 +106,7 @@ struct Loader {
         } else {
             // instruction j covers k rows RPI·j ..; lane L: row RPI·j + L / CPR, physical chunk L % CPR
             const int k = RPI * wave + lane / CPR;
-            const int c = (lane % CPR) ^ (MS ? 8 * ((k >> 2) & 1) : 4 * (k & 3));
+            const int c = (lane % CPR) ^ (MS ? 8 * ((k >> 2) & 1) : mnswz<RT>(k));
             org = reinterpret_cast<const char *>(X + mn0);
             voff = (unsigned)(((long long)k * ld + 8 * c) * 2);
             step_i = (long long)RPI * NW * ld * 2;
@@ -147,7 +152,8 @@ struct Frags {
 #pragma unroll
             for (int t = 0; t < TT; t++) {
                 const int P = w0 + (PAIRED ? 32 * (t >> 1) + 4 * (t & 1) + 8 * c : 16 * t + 4 * c);
-                off[t] = (8 * g + q) * (RT * 2) + (((P >> 3) ^ (4 * q)) << 4) + 2 * (P & 7);
+                // k-row 8g + q (+4, +32·s: the same swizzle)
+                off[t] = (8 * g + q) * (RT * 2) + (((P >> 3) ^ mnswz<RT>(q)) << 4) + 2 * (P & 7);
             }
         }
     }
