@@ -157,7 +157,7 @@ static int launch_layout(const GemmParams<typename Mma<T>::Sum> &p, int count) {
 //   two 288-312; two k groups of 4 waves on separate rings, their sums added through LDS: 335-340; 32x32x16: 346).
 //   Time per call against K at M = N = 1024 is about 2-3 µs plus 0.26 µs per k-step of 64 (8 MFMAs per wave), so
 //   the k-step's latency chain (LDS reads, barrier), not its MFMAs, sets the rate; the read-ahead takes the LDS
-//   reads off that chain. The 32-row tile needs A k-contiguous (the transposed-A loader reads 128-row tiles).
+//   reads off that chain.
 //   At n = 2048 (128×128 tiles) the read-ahead gives nothing (841-849 against 849-853): that size runs at the power
 //   limit (1.8-2.0 GHz).
 // - the same small products on 64×64 tiles, 4 waves of 32×32, three stages, read-ahead: NT n = 1024 399.9 against
@@ -178,10 +178,10 @@ template <bool AK, bool BKC>
 static int launch_hg_layout(const hg::Params &p, int count) {
     if ((long long)(p.M / 256) * (p.N / 256) * count >= num_cus && p.M % 256 == 0 && p.N % 256 == 0)
         return launch_hg<256, 256, 2, 4, 64, 2, AK, BKC>(p, count);
-    // with A k-contiguous, below one 128×128 tile per CU: 64×64 tiles, 20 % fewer L2 → LDS bytes per flop than the
-    // 32×128 tiles of the same count (n = 1024 NN 382.8 → 400.7, NT 386 → 400 TFLOP/s)
-    if constexpr (AK)
-        if ((long long)(p.M / 128) * (p.N / 128) * count < num_cus) return launch_hg<64, 64, 2, 2, 64, 3, AK, BKC, true>(p, count);
+    // below one 128×128 tile per CU: 64×64 tiles, every layout. With A k-contiguous they move 20 % fewer L2 → LDS bytes
+    // per flop than the 32×128 tiles of the same count (n = 1024 NN 382.8 → 400.7, NT 386 → 400 TFLOP/s); with A
+    // transposed they replace 128×128 tiles, 64 of them for 256 CUs at n = 1024 (TN 212.6 → 365.5, TT 215.3 → 393.1)
+    if ((long long)(p.M / 128) * (p.N / 128) * count < num_cus) return launch_hg<64, 64, 2, 2, 64, 3, AK, BKC, true>(p, count);
     return launch_hg<128, 128, 2, 4, 64, 3, AK, BKC>(p, count);
 }
 // The whole-tile FP16 kernel applies when every operand is 16-byte aligned with 16-byte row strides, M and N are

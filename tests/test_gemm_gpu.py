@@ -282,9 +282,9 @@ def test_gemm_exact_small_integers(g9, torch_dev):
                                          (1024, 1024, 64, 4), (1024, 1024, 192, 16)])
 def test_hgemm_whole_tile_kernel(g9, torch_dev, M, N, K, count):
     """Shapes served by the whole-tile FP16 kernel (M, N multiples of 128, K of 64, 16-byte aligned operands): fewer
-    128×128 tiles than CUs (A k-contiguous: 64×64 tiles, B read k-contiguous (NT) or through the 64-wide transposing
-    loader (NN), three LDS stages, fragments read a k-step ahead over an odd, even and single k-step count; 128×128
-    tiles with A transposed), 256 tiles of 128×128 over a batch of 4, and
+    128×128 tiles than CUs (64×64 tiles in every layout, the mn-contiguous operands through the 64-wide transposing
+    loader, three LDS stages, fragments read a k-step ahead over an odd, even and single k-step count), 256 tiles of
+    128×128 over a batch of 4, and
     256×256 tiles over a batch of 16, in every transpose
     layout, through the C ABI on device memory. Small-integer inputs make every result exact, so a misplaced 16-byte
     chunk, k row or tile shows up bit-exactly; alpha/beta are then checked against float64 with the HGEMM bound."""
