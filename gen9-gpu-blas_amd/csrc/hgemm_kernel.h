@@ -29,7 +29,9 @@
 //   long, and read with ds_read_b64_tr_b16, which transposes 16-lane groups: lane j of a group reads 4 consecutive
 //   mn of one k-row, and lane i receives the i-th mn of the group's reads for 4 k-rows. Chunk c of row k sits at
 //   c ^ mnswz(k): 4·(k & 3) for rows of 128 or more mn, 4·((k >> 1) & 1) for rows of 64 (8 chunks, two k-rows per
-//   256-byte bank row), so the four rows a group reads fall on distinct banks;
+//   256-byte bank row), so the four rows a group reads fall on distinct banks. A, when both operands are
+//   mn-contiguous (TN), takes xor 2·((k >> 3) & 1) on top: then the two groups one LDS cycle serves (k-rows 8g + 0..3
+//   and 8g + 8..11) read distinct banks too;
 // - operands are swapped in the MFMA (the B fragment is the first input), so each lane ends with runs of 4
 //   consecutive n of one row of C. n tiles come in pairs whose 16 fragment rows interleave in groups of 4 (rows
 //   4q..4q+3 of the even tile are n 8q..8q+3 of the pair, of the odd tile n 8q+4..8q+7), so a lane's outputs of the
@@ -70,12 +72,18 @@ struct Params {
 // Global → LDS loads of one operand tile: RT rows (m or n) × KB k, RT·KB·2 bytes, issued by NW waves (counted in FP16
 // elements; the FP32 kernel views its operands as FP16 pairs).
 // KC: stored k-contiguous (element (mn, k) at X[mn·ld + k]); otherwise mn-contiguous (element (mn, k) at X[k·ld + mn]).
-// MS: the mn-contiguous swizzle, chunk c of k-row k at c ^ mnswz<RT>(k) for the FP16 transposing reads (MS = 0), or
-// at c ^ (8·((k >> 2) & 1)) for the FP32 reads of k-rows k and k + 4 by the two halves of a wave (MS = 1).
+// MS: the mn-contiguous swizzle, chunk c of k-row k at c ^ mnswz<RT, false>(k) for the FP16 transposing reads
+// (MS = 0), c ^ mnswz<RT, true>(k) for those of A in the TN layout (MS = 2), or at c ^ (8·((k >> 2) & 1)) for the
+// FP32 reads of k-rows k and k + 4 by the two halves of a wave (MS = 1).
 // Each lane's byte offset from the tile origin is fixed for the whole kernel; the wave-uniform origin advances.
-template <int RT> __device__ __forceinline__ int mnswz(int k) {
+// X3: xor 2·bit 3 of k as well, so that lane groups 0 and 1 of a transposing read (k-rows 8g + 0..3), which one LDS
+// cycle serves together, use the two halves of the banks when each lane reads 8 bytes of 16 consecutive mn. Measured
+// for A in the TN layout (n = 1024 365 → 387, n = 2048 812-828 → 843-850 TFLOP/s, n = 4096 the same); in TT
+// (n = 4096 1321 → 1308) and for the paired n tiles of B, whose lanes read the first or the second 8 bytes of 4
+// chunks, so that their groups share banks either way (NN n = 1024 401 → 393-395), it is not used.
+template <int RT, bool X3 = false> __device__ __forceinline__ int mnswz(int k) {
     static_assert(RT >= 64, "an mn-contiguous row holds at least 8 chunks");
-    return RT >= 128 ? 4 * (k & 3) : 4 * ((k >> 1) & 1);
+    return (RT >= 128 ? 4 * (k & 3) : 4 * ((k >> 1) & 1)) ^ (X3 ? 2 * ((k >> 3) & 1) : 0);
 }
 template <int RT, int KB, int NW, bool KC, int MS = 0>
 struct Loader {
@@ -87,7 +95,7 @@ struct Loader {
                                                                           // instruction
     static_assert(NINST % NW == 0, "tile instructions must divide over the waves");
     static_assert(!KC || (RPIK * NW) % 32 == 0, "k-contiguous swizzle must repeat over a wave's instructions");
-    static_assert(KC || ((RT >= 128 || (RT == 64 && MS == 0)) && (RPI * NW) % (MS ? 8 : 4) == 0),
+    static_assert(KC || ((RT >= 128 || (RT == 64 && MS != 1)) && (RPI * NW) % (MS == 2 ? 16 : MS ? 8 : 4) == 0),
                   "mn-contiguous swizzle must repeat over a wave's instructions");
     const char *org;      // wave-uniform: tile origin at the next k-step to load
     unsigned voff;        // this lane's byte offset for instruction 0
@@ -106,7 +114,7 @@ struct Loader {
         } else {
             // instruction j covers k rows RPI·j ..; lane L: row RPI·j + L / CPR, physical chunk L % CPR
             const int k = RPI * wave + lane / CPR;
-            const int c = (lane % CPR) ^ (MS ? 8 * ((k >> 2) & 1) : mnswz<RT>(k));
+            const int c = (lane % CPR) ^ (MS == 1 ? 8 * ((k >> 2) & 1) : mnswz<RT, MS == 2>(k));
             org = reinterpret_cast<const char *>(X + mn0);
             voff = (unsigned)(((long long)k * ld + 8 * c) * 2);
             step_i = (long long)RPI * NW * ld * 2;
@@ -130,7 +138,7 @@ struct Loader {
 // tile and k32 substep one 16-byte fragment per lane, row lane % 16 and k 8·(lane / 16) .. +7. PAIRED (the first MFMA
 // input, n): tiles 2p and 2p+1 cover n 32p .. 32p+31 of the wave, fragment row r of tile t being n
 // 32·(t/2) + 4·(t%2) + 8·(r/4) + r%4; otherwise row r of tile t is 16t + r.
-template <int RT, int KB, int TT, bool KC, bool PAIRED>
+template <int RT, int KB, int TT, bool KC, bool PAIRED, bool X3 = false>
 struct Frags {
     static constexpr int NSUB = KB / 32;
     static constexpr int NOFF = KC ? 2 * NSUB : TT;
@@ -153,7 +161,7 @@ struct Frags {
             for (int t = 0; t < TT; t++) {
                 const int P = w0 + (PAIRED ? 32 * (t >> 1) + 4 * (t & 1) + 8 * c : 16 * t + 4 * c);
                 // k-row 8g + q (+4, +32·s: the same swizzle)
-                off[t] = (8 * g + q) * (RT * 2) + (((P >> 3) ^ mnswz<RT>(q)) << 4) + 2 * (P & 7);
+                off[t] = (8 * g + q) * (RT * 2) + (((P >> 3) ^ mnswz<RT, X3>(8 * g + q)) << 4) + 2 * (P & 7);
             }
         }
     }
@@ -183,7 +191,8 @@ __global__ void __launch_bounds__(WM *WN * 64) hgemm_kernel(Params p) {
     constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 16, TN = WTN / 16;
     constexpr int ABYTES = BM * KB * 2, BBYTES = BN * KB * 2, SBYTES = ABYTES + BBYTES;
     constexpr int NSUB = KB / 32;
-    using LA = Loader<BM, KB, NW, AK>;
+    constexpr bool AX3 = !AK && !BKC;   // TN: A's transposing reads take the bit-3 swizzle term
+    using LA = Loader<BM, KB, NW, AK, AX3 ? 2 : 0>;
     using LB = Loader<BN, KB, NW, BKC>;
     constexpr int LPS = LA::NI + LB::NI;   // loads per stage per wave
     static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32 (n tiles come in pairs)");
@@ -216,7 +225,7 @@ __global__ void __launch_bounds__(WM *WN * 64) hgemm_kernel(Params p) {
     LB lb;
     la.init(A, p.lda, m0, wave, lane);
     lb.init(B, p.ldb, n0, wave, lane);
-    Frags<BM, KB, TM, AK, false> fa;
+    Frags<BM, KB, TM, AK, false, AX3> fa;
     Frags<BN, KB, TN, BKC, true> fb;
     fa.init(wm * WTM, lane);
     fb.init(wn * WTN, lane);
