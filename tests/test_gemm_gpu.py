@@ -279,12 +279,12 @@ def test_gemm_exact_small_integers(g9, torch_dev):
 
 
 @pytest.mark.parametrize("M,N,K,count", [(256, 384, 320, 1), (128, 256, 2112, 1), (384, 256, 256, 1), (128, 128, 64, 1),
-                                         (1024, 1024, 64, 4), (1024, 1024, 192, 16)])
+                                         (1024, 1024, 64, 4), (1024, 1024, 320, 4), (1024, 1024, 192, 16)])
 def test_hgemm_whole_tile_kernel(g9, torch_dev, M, N, K, count):
     """Shapes served by the whole-tile FP16 kernel (M, N multiples of 128, K of 64, 16-byte aligned operands): fewer
     128×128 tiles than CUs (64×64 tiles in every layout, the mn-contiguous operands through the 64-wide transposing
     loader, three LDS stages, fragments read a k-step ahead over an odd, even and single k-step count), 256 tiles of
-    128×128 over a batch of 4, and
+    128×128 over a batch of 4 (one k-step, and five: the loaders' swizzles kept as they advance over k), and
     256×256 tiles over a batch of 16, in every transpose
     layout, through the C ABI on device memory. Small-integer inputs make every result exact, so a misplaced 16-byte
     chunk, k row or tile shows up bit-exactly; alpha/beta are then checked against float64 with the HGEMM bound."""
