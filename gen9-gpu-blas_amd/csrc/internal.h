@@ -75,10 +75,17 @@ G9_HIDDEN int mem_kind(const void *p, size_t bytes);
 // 1 if p .. p+bytes lies in one device allocation.
 G9_HIDDEN int is_device(const void *p, size_t bytes);
 // End of a call: in no-wait mode with every operand in place, returns at once; otherwise waits for the stream and
-// copies staged written operands back.
-G9_HIDDEN int finish(Operand *ops, int n);
+// copies staged written operands back (through wait_done when nothing is copied back and the caller queued no
+// device-to-host copy of its own: host_copy).
+G9_HIDDEN int finish(Operand *ops, int n, bool host_copy = false);
 // Waits for the stream (no copies). 0 or an error.
 G9_HIDDEN int wait_stream();
+// Waits for the stream through a completion word set by a kernel queued behind the call's work (falls back to
+// wait_stream); for calls that queued no device-to-host copy.
+G9_HIDDEN int wait_done();
+// 64 bytes of pinned host-coherent memory that kernels may write a call's scalar result into (read after wait_done),
+// or null when it could not be allocated.
+G9_HIDDEN void *result_slot();
 
 // Kernel timing for GEN9BLAS_PROFILE=1: events around the main kernels of a call.
 G9_HIDDEN void prof_begin();
@@ -128,10 +135,11 @@ G9_HIDDEN int launch_scal(int es, int n, double a, void *x, long long ox, long l
 G9_HIDDEN int launch_copy(int es, int n, const void *x, long long ox, long long ix, void *y, long long oy, long long iy);
 G9_HIDDEN int launch_rot(int es, int n, void *x, long long ox, long long ix, void *y, long long oy, long long iy,
                          double h11, double h12, double h21, double h22, int swap);
-// mode 0: Σ x·y, 1: Σ|x|, 2: Σ x² (FP64). Result written to *dev_result (device double).
+// mode 0: Σ x·y, 1: Σ|x|, 2: Σ x² (FP64). Result written to *result (a double in device memory or in the pinned
+// result slot).
 G9_HIDDEN int launch_reduce(int es, int mode, int n, const void *x, long long ox, long long ix, const void *y, long long oy,
-                            long long iy, double *dev_result);
-G9_HIDDEN int launch_iamax(int es, int n, const void *x, long long ox, long long ix, long long *dev_result);
+                            long long iy, double *result);
+G9_HIDDEN int launch_iamax(int es, int n, const void *x, long long ox, long long ix, long long *result);
 G9_HIDDEN int launch_gemv(int es, int trans, int M, int N, double alpha, const void *A, long long lda, const void *x, long long ox,
                           long long ix, double beta, void *y, long long oy, long long iy);
 G9_HIDDEN int launch_ger(int es, int M, int N, double alpha, const void *x, long long ox, long long ix, const void *y,

@@ -78,10 +78,12 @@ static int reduction(int type, int mode, int n, const void *x, int incx, const v
         no = 2;
     }
     // A result pointer in device memory receives the sum in place (no wait in no-wait mode); a host pointer is
-    // filled after the wait.
+    // filled after the wait, from the pinned result slot the final kernel writes (else through a device word and a
+    // copy).
     const bool dev_result = rkind == MEM_DEVICE;
-    void *res = result;
-    if (!dev_result) G9_TRY(scratch(SLOT_Q, 64, &res));
+    double *slot = dev_result ? nullptr : (double *)result_slot();
+    void *res = dev_result ? result : slot;
+    if (!res) G9_TRY(scratch(SLOT_Q, 64, &res));
     prof_begin();
     G9_TRY(launch_reduce(es, mode, n, o[0].dev, voff(n, incx), incx, mode == 0 ? o[1].dev : nullptr,
                          mode == 0 ? voff(n, incy) : 0, mode == 0 ? incy : 0, (double *)res));
@@ -89,12 +91,13 @@ static int reduction(int type, int mode, int n, const void *x, int incx, const v
     if (dev_result) {
         G9_TRY(finish(o, no));
     } else {
-        G9_HIP(hipMemcpyAsync(result, res, sizeof(double), hipMemcpyDeviceToHost, stream));
+        if (!slot) G9_HIP(hipMemcpyAsync(result, res, sizeof(double), hipMemcpyDeviceToHost, stream));
         const int saved = nowait;
         nowait = 0;   // the result goes through a host pointer: always wait
-        const int r = finish(o, no);
+        const int r = finish(o, no, !slot);
         nowait = saved;
         G9_TRY(r);
+        if (slot) *result = *(volatile double *)slot;
     }
     prof_collect(t0_);
     return 0;
@@ -174,14 +177,21 @@ int gen9blas_iamax(int type, int n, const void *x, int incx, int64_t *result) {
     Operand o[1];
     vec(o[0], x, n, incx, es);
     G9_TRY(resolve(o[0], SLOT_A, true, false, false));
-    void *res;
-    G9_TRY(scratch(SLOT_Q, 64, &res));
+    // the final kernel writes the index into the pinned result slot (else a device word, copied after)
+    long long *slot = (long long *)result_slot();
+    void *res = slot;
+    if (!res) G9_TRY(scratch(SLOT_Q, 64, &res));
     prof_begin();
     G9_TRY(launch_iamax(es, n, o[0].dev, voff(n, incx), incx, (long long *)res));
     prof_end();
     long long idx = 0;
-    G9_HIP(hipMemcpyAsync(&idx, res, sizeof idx, hipMemcpyDeviceToHost, stream));
-    G9_TRY(wait_stream());
+    if (slot) {
+        G9_TRY(wait_done());
+        idx = *(volatile long long *)slot;
+    } else {
+        G9_HIP(hipMemcpyAsync(&idx, res, sizeof idx, hipMemcpyDeviceToHost, stream));
+        G9_TRY(wait_stream());
+    }
     *result = idx;
     prof_collect(t0_);
     return 0;

@@ -441,7 +441,7 @@ int launch_rot(int es, int n, void *x, ll ox, ll ix, void *y, ll oy, ll iy, doub
     return elem<3>(es, n, h11, h12, h21, h22, x, ox, ix, y, oy, iy);
 }
 
-int launch_reduce(int es, int mode, int n, const void *x, ll ox, ll ix, const void *y, ll oy, ll iy, double *dev_result) {
+int launch_reduce(int es, int mode, int n, const void *x, ll ox, ll ix, const void *y, ll oy, ll iy, double *result) {
     return by_type(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
         const T *xp = (const T *)x + ox, *yp = y ? (const T *)y + oy : xp;
@@ -454,13 +454,13 @@ int launch_reduce(int es, int mode, int n, const void *x, ll ox, ll ix, const vo
         else if (mode == 1) hipLaunchKernelGGL((reduce_kernel<T, 1>), dim3(g), dim3(NT), 0, stream, n, xp, ix, yp, iy, (int)vec, part);
         else hipLaunchKernelGGL((reduce_kernel<T, 2>), dim3(g), dim3(NT), 0, stream, n, xp, ix, yp, iy, (int)vec, part);
         G9_HIP(hipGetLastError());
-        hipLaunchKernelGGL(reduce_final, dim3(1), dim3(NT), 0, stream, (int)g, (const double *)part, mode, dev_result);
+        hipLaunchKernelGGL(reduce_final, dim3(1), dim3(NT), 0, stream, (int)g, (const double *)part, mode, result);
         G9_HIP(hipGetLastError());
         return 0;
     });
 }
 
-int launch_iamax(int es, int n, const void *x, ll ox, ll ix, long long *dev_result) {
+int launch_iamax(int es, int n, const void *x, ll ox, ll ix, long long *result) {
     return by_type(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
         const T *xp = (const T *)x + ox;
@@ -472,7 +472,7 @@ int launch_iamax(int es, int n, const void *x, ll ox, ll ix, long long *dev_resu
         hipLaunchKernelGGL((iamax_kernel<T>), dim3(g), dim3(NT), 0, stream, n, xp, ix, pv, pi);
         G9_HIP(hipGetLastError());
         hipLaunchKernelGGL(iamax_final, dim3(1), dim3(NT), 0, stream, (int)g, (const double *)pv, (const long long *)pi,
-                           dev_result);
+                           result);
         G9_HIP(hipGetLastError());
         return 0;
     });

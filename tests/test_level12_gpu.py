@@ -158,3 +158,34 @@ def test_reduction_device_result(g9, orc, torch_dev):
         got = out.cpu().numpy()
         assert got[0] == g9.dot(xd, yd) and got[1] == g9.asum(xd) and got[2] == g9.nrm2(xd)
         assert abs(got[0] - orc.dot(x, y)) <= 1e-12 * float(np.abs(x) @ np.abs(y))
+
+
+@pytest.mark.parametrize("reps", [1, 40])
+def test_host_result_waits_for_queued_work(g9, torch_dev, reps):
+    """A host-result reduction issued right behind products queued in no-wait mode reads their finished output.
+    With one product the call waits by spinning on the completion word that a kernel queued behind its work sets;
+    40 FP32 products at n = 2048 put several ms of work ahead, so the spin gives up after 2 ms and falls back to
+    hipStreamSynchronize. C starts as NaN and the products are of small integers, so the FP64 sum of |C| is exact
+    and any read of an unfinished C shows."""
+    import ctypes
+    torch = torch_dev
+    n = 2048
+    r = np.random.default_rng(31)
+    a = r.integers(-2, 3, (n, n)).astype(np.float32)
+    b = r.integers(-2, 3, (n, n)).astype(np.float32)
+    ref = float(np.abs(a.astype(np.float64) @ b.astype(np.float64)).sum())
+    A, B = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    L = g9._lib
+    for trial in range(3):
+        C = torch.full((n, n), float("nan"), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        g9.set_nowait(True)
+        try:
+            for _ in range(reps):
+                rc = L.gen9blas_gemm(g9.GEN9BLAS_S, 0, 0, n, n, n, 1.0, ctypes.c_void_p(A.data_ptr()), n,
+                                     ctypes.c_void_p(B.data_ptr()), n, 0.0, ctypes.c_void_p(C.data_ptr()), n)
+                assert rc == 0, g9._lib.gen9blas_error()
+            got = g9.asum(C.reshape(-1))
+        finally:
+            g9.set_nowait(False)
+        assert got == ref, f"reps={reps} trial={trial}: {got} against {ref}"
