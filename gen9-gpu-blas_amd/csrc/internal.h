@@ -60,6 +60,7 @@ struct Operand {
     long long rows = 0, cols = 0;
     int es = 0;
     bool zc = false;             // caller's memory used in place
+    bool pinned = false;         // caller's host memory is page-locked: copied by DMA straight from or into it
     bool written = false;        // kernels write it: copy back after the wait when staged
 };
 // Resolves op (host, rows, cols, ld, es set by the caller) for the kernels. Device memory is used in place; host
@@ -70,7 +71,7 @@ struct Operand {
 G9_HIDDEN int resolve(Operand &op, int slot, bool copy_in, bool written, bool repitch);
 // Where p .. p+bytes lies: host memory (pageable or pinned, or NULL), inside one device (or managed) allocation, or in
 // device memory but running past the end of its allocation (an ld or increment too large for the buffer).
-enum { MEM_HOST = 0, MEM_DEVICE = 1, MEM_DEVICE_OVERRUN = 2 };
+enum { MEM_HOST = 0, MEM_DEVICE = 1, MEM_DEVICE_OVERRUN = 2, MEM_PINNED = 3 };   // MEM_PINNED: page-locked host memory
 G9_HIDDEN int mem_kind(const void *p, size_t bytes);
 // 1 if p .. p+bytes lies in one device allocation.
 G9_HIDDEN int is_device(const void *p, size_t bytes);

@@ -62,7 +62,7 @@ static int reduction(int type, int mode, int n, const void *x, int incx, const v
     const int ok = l12_es(type, &es);
     // a host result is 0 until the sum is known, as in the reference (reference: lib/src/level12.c:172)
     const int rkind = ok == GEN9BLAS_ERR_NO_DEVICE ? MEM_HOST : mem_kind(result, sizeof(double));
-    if (result && rkind == MEM_HOST) *result = 0;
+    if (result && (rkind == MEM_HOST || rkind == MEM_PINNED)) *result = 0;
     G9_TRY(ok);
     if (n <= 0) return 0;
     if (!incx || (mode == 0 && !incy)) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "vector increment 0");

@@ -457,3 +457,33 @@ def test_gemm_split_k(tmp_path):
         env["GEN9BLAS_SPLITK"] = forced
         r = subprocess.run([sys.executable, str(script)], env=env, capture_output=True, text=True, timeout=200)
         assert r.returncode == 0 and r.stdout.strip().endswith("ok"), f"GEN9BLAS_SPLITK={forced}: " + r.stderr[-2000:]
+
+
+def test_small_host_operands_bounce_and_pinned(g9):
+    """Small host operands. Pageable ones pass through the library's pinned bounce area: here views whose row gaps
+    make up most of their span, so their rows are re-pitched on the way in (A, and C for beta) and on the way back
+    (C), each span under 128 KiB. Page-locked ones (the module's `empty`) are copied by DMA straight from and into the
+    caller's memory. Both against float64, with C's gap columns left as they were."""
+    rng = np.random.default_rng(41)
+    M, N, K = 24, 56, 72
+    big_a = rng.standard_normal((M, 1000)).astype(np.float32)
+    A = big_a[:, :K]
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    big_c = np.full((M, 900), 7.0, np.float32)
+    C = big_c[:, :N]
+    ref = A.astype(np.float64) @ B.astype(np.float64)
+    scale = np.abs(A.astype(np.float64)) @ np.abs(B.astype(np.float64))
+    g9.gemm(A, B, alpha=1.0, beta=0.5, C=C)
+    e = np.abs(C.astype(np.float64) - (ref + 3.5)) / (scale + 3.5)
+    assert e.max() <= 1e-6, f"pageable, re-pitched: max e {e.max():.2e}"
+    assert np.all(big_c[:, N:] == 7.0), "gap columns of C changed"
+    Ap, Bp, Cp = g9.empty((M, K), np.float32), g9.empty((K, N), np.float32), g9.empty((M, N), np.float32)
+    Ap[:], Bp[:], Cp[:] = A, B, 1.0
+    for _ in range(3):
+        Cp[:] = 1.0
+        g9.gemm(Ap, Bp, alpha=2.0, beta=-1.0, C=Cp)
+        e = np.abs(Cp.astype(np.float64) - (2 * ref - 1.0)) / (2 * scale + 1.0)
+        assert e.max() <= 1e-6, f"page-locked: max e {e.max():.2e}"
+    W = g9.gemm(A, B)   # a new result, in page-locked memory
+    e = np.abs(W.astype(np.float64) - ref) / scale
+    assert e.max() <= 1e-6, f"new result: max e {e.max():.2e}"
