@@ -140,30 +140,47 @@ __global__ void __launch_bounds__(NT) mv_kernel(Shape s, const T *__restrict__ a
         if ((lane & (64 / U - 1)) == 0 && i + base < rend) Q[(ll)g * s.nrows + i + base] = rs[0];
     };
     // checked rows [r0, r1): an element is read only where stored, a 16-byte chunk whole when it meets the stored
-    // range inside the matrix's columns (its elements outside the range are masked when used)
+    // range inside the matrix's columns (its elements outside the range are masked when used). Full storage holds
+    // every column of every row, so there, when the whole column group lies inside the matrix (a wave-uniform test),
+    // every row's chunk is read whole, from rows clamped into [r0, r1), and all of a batch's loads are in flight
+    // together: a per-lane choice between a chunk and single elements written into the same registers had the
+    // compiler wait for each row's loads before the next row's (SYMV n = 16384: the diagonal blocks' rows then
+    // formed the kernel's tail)
+    const bool whole = FMT == F_FULL && V > 1 && g0 + 64 * V <= s.ncols;
     auto checked = [&](int r0, int r1) {
         for (int i = r0; i < r1; i += U) {
             T el[U][V];
             R xr[U];
+            if (whole) {
+                if constexpr (FMT == F_FULL && V > 1) {
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int r = i + u;
-                int lo, hi;
-                stored_range(s, band, r, lo, hi);
-                if (r >= r1) hi = lo - 1;
-                const T *ar = a + row_start<FMT>(s, r);
-                if constexpr (V > 1) {
-                    if (c0 <= hi && c0 + V - 1 >= lo && c0 + V <= s.ncols) {
-                        const u32x4 t = row16<FMT>(ar + c0);
+                    for (int u = 0; u < U; u++) {
+                        const u32x4 t = row16<FMT>(a + row_start<FMT>(s, min(i + u, r1 - 1)) + c0);
                         __builtin_memcpy(el[u], &t, 16);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < V; e++) el[u][e] = c0 + e >= lo && c0 + e <= hi ? ar[c0 + e] : T(0);
+                        xr[u] = (dirs & DIR_COL) && i + u < r1 ? (R)x[(ll)(i + u) * ix] : R(0);
                     }
-                } else {
-                    el[u][0] = c0 >= lo && c0 <= hi ? ar[c0] : T(0);
                 }
-                xr[u] = (dirs & DIR_COL) && r < r1 ? (R)x[(ll)r * ix] : R(0);
+            } else {
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const int r = i + u;
+                    int lo, hi;
+                    stored_range(s, band, r, lo, hi);
+                    if (r >= r1) hi = lo - 1;
+                    const T *ar = a + row_start<FMT>(s, r);
+                    if constexpr (V > 1) {
+                        if (c0 <= hi && c0 + V - 1 >= lo && c0 + V <= s.ncols) {
+                            const u32x4 t = row16<FMT>(ar + c0);
+                            __builtin_memcpy(el[u], &t, 16);
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < V; e++) el[u][e] = c0 + e >= lo && c0 + e <= hi ? ar[c0 + e] : T(0);
+                        }
+                    } else {
+                        el[u][0] = c0 >= lo && c0 <= hi ? ar[c0] : T(0);
+                    }
+                    xr[u] = (dirs & DIR_COL) && r < r1 ? (R)x[(ll)r * ix] : R(0);
+                }
             }
             R rs[U];
 #pragma unroll

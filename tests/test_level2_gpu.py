@@ -84,6 +84,31 @@ def test_full_storage(g9, orc, dt, n):
               np.abs(Ad) + 0.25 * (np.outer(np.abs(X), np.abs(Y)) + np.outer(np.abs(Y), np.abs(X))), tol)
 
 
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("n", [1000, 1100])
+def test_full_storage_unreferenced_nan(g9, orc, dt, n):
+    """SYMV and TRMV on full storage with NaN in the triangle they must not reference. Rows that meet a column group's
+    diagonal block read whole 16-byte chunks, the unreferenced part included, and mask those elements when used:
+    masking by selection keeps the NaN out, a multiplication by zero would not. n = 1000 and 1100 take whole column
+    groups and a partial last one (16-byte rows in FP32 and FP64; FP16 at n = 1100 takes single elements)."""
+    tol = TOL[dt]
+    A = rng.uniform(-1, 1, (n, n)).astype(dt)
+    Ad = f64(A)
+    for uplo in "LU":
+        other = np.triu(np.ones((n, n), bool), 1) if uplo == "L" else np.tril(np.ones((n, n), bool), -1)
+        An = A.copy()
+        An[other] = np.nan
+        x = vector(n, dt, 1)
+        ref, scale = orc.mv(orc.symmetric(Ad, uplo), x)
+        check(f"symv NaN {uplo} n={n}", g9.symv(An, x, uplo=uplo), ref, scale, tol)
+        for trans in (False, True):
+            xx = vector(n, dt, 2)
+            Op = orc.triangle(Ad, uplo, False)
+            ref, scale = orc.mv(Op.T if trans else Op, xx)
+            g9.trmv(An, xx, uplo=uplo, trans=trans)
+            check(f"trmv NaN {uplo} trans={int(trans)} n={n}", xx, ref, scale, tol)
+
+
 def to_band(D, KL, KU):
     M, N = D.shape
     P = np.zeros((M, KL + KU + 1), D.dtype)
