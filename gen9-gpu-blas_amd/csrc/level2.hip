@@ -257,15 +257,17 @@ __global__ void __launch_bounds__(NT) mv_kernel(Shape s, const T *__restrict__ a
 }
 
 // y_k = alpha·(Σ_band P[band][k] + Σ_group Q[group][k] (+ x_k for a unit diagonal)) + beta·y_k; y is not read when
-// beta = 0 (reference: level12.cl:280). A workgroup takes 64 outputs; wave q adds every 4th partial from the q-th
-// (loads issued 8 at a time), then wave 0 adds the 4 sums in wave order: a fixed order for every output.
+// beta = 0 (reference: level12.cl:280). A workgroup of FT threads takes 64 outputs; wave q adds every G-th partial
+// from the q-th (loads issued 8 at a time), then wave 0 adds the G sums in wave order: a fixed order for every output.
+// G = 16 waves: with 4, the 16384 outputs of an n = 16384 product kept about 8 KiB of loads in flight per CU.
+constexpr int FT = 1024;
 template <class T>
-__global__ void __launch_bounds__(NT) mv_finish(Shape s, int band, int ny, int dirs, int parts, int gw,
+__global__ void __launch_bounds__(FT) mv_finish(Shape s, int band, int ny, int dirs, int parts, int gw,
                                                 const typename Comp<T>::R *P, const typename Comp<T>::R *Q,
                                                 typename Comp<T>::R alpha, typename Comp<T>::R beta, const T *x, ll ix,
                                                 int add_x, T *y, ll iy) {
     using R = typename Comp<T>::R;
-    constexpr int G = NT / 64;
+    constexpr int G = FT / 64;
     const int lane = threadIdx.x & 63, q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int k = blockIdx.x * 64 + lane;
     auto sum = [&](const R *base, int first, int last, R t) {   // Σ base[j·ny], j = first + q, first + q + G, ... ≤ last
@@ -1006,7 +1008,7 @@ static int launch_mv(int es, int fmt, const Shape &s, const void *a, const void 
             return 0;
         }));
         G9_HIP(hipGetLastError());
-        hipLaunchKernelGGL((mv_finish<T>), dim3(blocks(ny, 64)), dim3(NT), 0, stream, s, (int)(fmt == F_BAND), ny, dirs,
+        hipLaunchKernelGGL((mv_finish<T>), dim3(blocks(ny, 64)), dim3(FT), 0, stream, s, (int)(fmt == F_BAND), ny, dirs,
                            (int)parts, gw, (const R *)P, (const R *)Q, (R)alpha, (R)beta, xp, ix, add_x, (T *)y, iy);
         G9_HIP(hipGetLastError());
         return 0;
