@@ -87,9 +87,10 @@ def test_full_storage(g9, orc, dt, n):
 @pytest.mark.parametrize("dt", DTYPES)
 @pytest.mark.parametrize("n", [1000, 1100])
 def test_full_storage_unreferenced_nan(g9, orc, dt, n):
-    """SYMV and TRMV on full storage with NaN in the triangle they must not reference. Rows that meet a column group's
-    diagonal block read whole 16-byte chunks, the unreferenced part included, and mask those elements when used:
-    masking by selection keeps the NaN out, a multiplication by zero would not. n = 1000 and 1100 take whole column
+    """SYMV, TRMV, SYR and SYR2 on full storage with NaN in the triangle they must not reference. Rows that meet a
+    column group's diagonal block read whole 16-byte chunks, the unreferenced part included, and mask those elements
+    when used (masking by selection keeps the NaN out, a multiplication by zero would not); the rank updates write
+    back only the referenced elements. n = 1000 and 1100 take whole column
     groups and a partial last one (16-byte rows in FP32 and FP64; FP16 at n = 1100 takes single elements)."""
     tol = TOL[dt]
     A = rng.uniform(-1, 1, (n, n)).astype(dt)
@@ -107,6 +108,19 @@ def test_full_storage_unreferenced_nan(g9, orc, dt, n):
             ref, scale = orc.mv(Op.T if trans else Op, xx)
             g9.trmv(An, xx, uplo=uplo, trans=trans)
             check(f"trmv NaN {uplo} trans={int(trans)} n={n}", xx, ref, scale, tol)
+        # rank updates read whole chunks too, but write only the referenced triangle: the NaN stay where they were
+        xs, ys = vector(n, dt, 1, 2), vector(n, dt, -3, 0)
+        X, Y = f64(xs), f64(ys)
+        ref_mask = ~other
+        for name, upd, ref, scale in (
+                ("syr", lambda M: g9.syr(-0.5, xs, M, uplo=uplo), Ad - 0.5 * np.outer(X, X),
+                 np.abs(Ad) + 0.5 * np.outer(np.abs(X), np.abs(X))),
+                ("syr2", lambda M: g9.syr2(0.25, xs, ys, M, uplo=uplo), Ad + 0.25 * (np.outer(X, Y) + np.outer(Y, X)),
+                 np.abs(Ad) + 0.25 * (np.outer(np.abs(X), np.abs(Y)) + np.outer(np.abs(Y), np.abs(X))))):
+            A1 = An.copy()
+            upd(A1)
+            check(f"{name} NaN {uplo} n={n}", A1[ref_mask], ref[ref_mask], scale[ref_mask], tol)
+            assert np.isnan(A1[other]).all(), f"{name} {uplo} n={n}: the unreferenced triangle was written"
 
 
 def to_band(D, KL, KU):
