@@ -82,7 +82,7 @@ G9_HIDDEN int finish(Operand *ops, int n, bool host_copy = false);
 // Waits for the stream (no copies). 0 or an error.
 G9_HIDDEN int wait_stream();
 // Waits for the stream through a completion word set by a kernel queued behind the call's work (falls back to
-// wait_stream); for calls that queued no device-to-host copy.
+// wait_stream); for calls whose device-to-host copies, if any, go into page-locked memory.
 G9_HIDDEN int wait_done();
 // 64 bytes of pinned host-coherent memory that kernels may write a call's scalar result into (read after wait_done),
 // or null when it could not be allocated.

@@ -459,14 +459,16 @@ __global__ void done_signal(unsigned *word, unsigned seq) {
     if (threadIdx.x == 0) __hip_atomic_store(word, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// Waits for the stream by spinning on a host-coherent word that a one-thread kernel, queued behind the call's work,
-// sets. MI355X, median of 2000 calls: a kernel and the signal 8.4 µs, a kernel and hipStreamSynchronize 11.0 µs.
-// Only for calls that queued no device-to-host copy (a copy into pageable memory may complete on the host after the
-// GPU's part). After 2 ms (a long queue ahead, or a fault that keeps the signal from coming) it falls back to
-// hipStreamSynchronize, which also reports kernel errors; so does a signal overtaken by another thread's (the word
-// then holds a later number, which also means this call's work is done).
+// The 64 bytes after the completion word's cache line: a call's scalar result, written by its last kernel.
 void *result_slot() { return done_word ? (void *)((char *)done_word + 128) : nullptr; }
 
+// Waits for the stream by spinning on a host-coherent word that a one-thread kernel, queued behind the call's work,
+// sets. MI355X, median of 2000 calls: a kernel and the signal 8.4 µs, a kernel and hipStreamSynchronize 11.0 µs.
+// Only for calls whose device-to-host copies, if any, land in page-locked memory (the bounce area, or the caller's
+// own): a copy into pageable memory may complete on the host after the GPU's part. After 2 ms (a long queue ahead,
+// or a fault that keeps the signal from coming) it falls back to hipStreamSynchronize, which also reports kernel
+// errors; so does a signal overtaken by another thread's (the word then holds a later number, which also means this
+// call's work is done).
 int wait_done() {
     if (!done_word) return wait_stream();
     const unsigned seq = __atomic_add_fetch(&done_seq, 1u, __ATOMIC_RELAXED);
