@@ -409,11 +409,18 @@ def _equal_lengths(*vs):
     return vs
 
 
+SMALL_RESULT = 128 << 10   # bytes: host results up to this size are plain NumPy arrays
+
+
 def _new(shape, t, like):
-    """A new result: on the device of `like` if that is a GPU tensor, else in pinned host memory."""
+    """A new result: on the device of `like` if that is a GPU tensor; else in host memory, pinned (copied back by
+    one DMA) above SMALL_RESULT bytes, and a plain NumPy array below, which the library copies back through its own
+    pinned bounce area (a pinned block costs more Python time than such a copy saves)."""
     d = _operand(like)
     if d.on_gpu:
         return _torch_module().empty(tuple(shape), dtype=_torch_dtype(t), device=d.obj.device)
+    if int(np.prod(shape, dtype=np.int64)) * np.dtype(t).itemsize <= SMALL_RESULT:
+        return np.empty(shape, t)
     return empty(shape, t)
 
 

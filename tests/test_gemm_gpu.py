@@ -484,6 +484,6 @@ def test_small_host_operands_bounce_and_pinned(g9):
         g9.gemm(Ap, Bp, alpha=2.0, beta=-1.0, C=Cp)
         e = np.abs(Cp.astype(np.float64) - (2 * ref - 1.0)) / (2 * scale + 1.0)
         assert e.max() <= 1e-6, f"page-locked: max e {e.max():.2e}"
-    W = g9.gemm(A, B)   # a new result, in page-locked memory
+    W = g9.gemm(A, B)   # a new small result: a plain NumPy array, copied back through the bounce area
     e = np.abs(W.astype(np.float64) - ref) / scale
     assert e.max() <= 1e-6, f"new result: max e {e.max():.2e}"
