@@ -83,6 +83,44 @@ def test_gemm_reference_cases(g9, orc, torch_dev, kind, M, N, K, al, be):
             assert orc.gemm_diff(W, R, opA, opB, al, be, C0) <= 2 * bound, f"GPU vs oracle {tag}"
 
 
+def _random_cases(seed, count):
+    """Seeded random shapes: each of M, N, K is small (1-79), a multiple of 64 (the tile classes), within 3 of one
+    (edge strips, short k-steps), or in 80-699; with a type, layout, alpha, beta and operand residency."""
+    r = np.random.default_rng(seed)
+
+    def dim():
+        c = int(r.integers(0, 4))
+        if c == 0:
+            return int(r.integers(1, 80))
+        if c == 1:
+            return 64 * int(r.integers(1, 12))
+        if c == 2:
+            return max(1, 64 * int(r.integers(1, 12)) + int(r.integers(-3, 4)))
+        return int(r.integers(80, 700))
+    cases = []
+    for _ in range(count):
+        M, N, K = dim(), dim(), dim()
+        cases.append((str(r.choice(["H", "HS", "S", "D"])), M, N, K, float(r.choice([1.0, -0.5, 2.0])),
+                      float(r.choice([0.0, 0.0, 1.0, -1.5])), int(r.integers(0, 2)), int(r.integers(0, 2)),
+                      bool(r.integers(0, 2))))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_cases(2026, 256), ids=lambda c: "-".join(str(v) for v in c))
+def test_gemm_random_shapes(g9, orc, torch_dev, case):
+    """256 seeded random products across the dispatch's size classes (the skinny kernels, 64×64 / 128×128 / 256×256
+    whole tiles and their edge strips, split-K, the general kernel), every type and layout, host and device
+    operands, against float64 with the reference test's bounds."""
+    kind, M, N, K, al, be, ta, tb, dev = case
+    W, opA, opB, C0, zc = _run_case(g9, torch_dev, kind, M, N, K, al, be, ta, tb, dev, seed=M * 7919 + N * 31 + K)
+    mean, mx = orc.gemm_error(W, opA, opB, al, be, C0)
+    bmean, bmax = case_bounds(kind, K)
+    tag = f"{kind} M={M} N={N} K={K} a={al} b={be} tA={ta} tB={tb} dev={dev}"
+    assert mx <= bmax, f"{tag}: max e {mx:.2e}"
+    assert mean <= bmean, f"{tag}: mean e {mean:.2e}"
+    assert zc == (7 if dev else 0), f"{tag}: zero-copy bits {zc:03b}"
+
+
 def _sampled_rows_error(W, A, B, rows, alpha=1.0, beta=0.0, C0=None, tB=False):
     """Reference metric on sampled rows of C = alpha·A·op(B) + beta·C0 (float64)."""
     a64 = A[rows].astype(np.float64)
