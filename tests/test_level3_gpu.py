@@ -198,3 +198,86 @@ def test_trmm_fp32_whole_tiles(g9, M, N, full):
                     W = g9.trmm(A, B, side, uplo, ta, dg, 1.5)
                     P = T @ f64(B) if side == "L" else f64(B) @ T
                     assert np.array_equal(f64(W), 1.5 * P), f"trmm {side}{uplo} tA={ta} diag={dg}"
+
+
+def _l3_cases(seed, count):
+    """Seeded random level-3 calls: operation, type, side / triangle / transpose / unit diagonal, and dimensions that
+    are small (1-79), multiples of 64 (the whole-tile classes of the GEMMs underneath), within 3 of one, or 80-599."""
+    r = np.random.default_rng(seed)
+
+    def dim():
+        c = int(r.integers(0, 4))
+        if c == 0:
+            return int(r.integers(1, 80))
+        if c == 1:
+            return 64 * int(r.integers(1, 10))
+        if c == 2:
+            return max(1, 64 * int(r.integers(1, 10)) + int(r.integers(-3, 4)))
+        return int(r.integers(80, 600))
+    out = []
+    for _ in range(count):
+        out.append((str(r.choice(["symm", "syrk", "syr2k", "trmm", "trsm"])), int(r.integers(0, 4)), dim(), dim(),
+                    str(r.choice(["L", "R"])), str(r.choice(["L", "U"])), bool(r.integers(0, 2)), bool(r.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("case", _l3_cases(2027, 120), ids=lambda c: "-".join(str(v) for v in c))
+def test_level3_random(g9, case):
+    """120 seeded random SYMM / SYRK / SYR2K / TRMM / TRSM calls in every type, against the float64 closed forms with
+    the bounds of the tests above (TRSM: solution error on a well-conditioned triangle)."""
+    op, ti, M, N, side, uplo, ta, dg = case
+    kind, dt, acc, tol = TYPES[ti]
+    rng = np.random.default_rng(M * 1009 + N * 17 + ti)
+    tag = f"{op} {kind} {M}x{N} side={side} uplo={uplo} t={ta} diag={dg}"
+    n = M if side == "L" else N
+    if op == "symm":
+        S = rng.uniform(-1, 1, (n, n)).astype(dt)
+        Ss = np.tril(f64(S)) + np.tril(f64(S), -1).T if uplo == "L" else np.triu(f64(S)) + np.triu(f64(S), 1).T
+        B, C0 = rng.uniform(-1, 1, (M, N)).astype(dt), rng.uniform(-1, 1, (M, N)).astype(dt)
+        W = g9.symm(S, B, side, uplo, -0.5, 1.5, C0.copy(), accurate=acc)
+        P = Ss @ f64(B) if side == "L" else f64(B) @ Ss
+        Pa = np.abs(Ss) @ np.abs(f64(B)) if side == "L" else np.abs(f64(B)) @ np.abs(Ss)
+        _check(W, -0.5 * P + 1.5 * f64(C0), 0.5 * Pa + 1.5 * np.abs(f64(C0)), tol, tag=tag)
+    elif op in ("syrk", "syr2k"):
+        Nn, K = M, N
+        mask = np.tril(np.ones((Nn, Nn), bool)) if uplo == "L" else np.triu(np.ones((Nn, Nn), bool))
+        A = rng.uniform(-1, 1, (K, Nn) if ta else (Nn, K)).astype(dt)
+        B = rng.uniform(-1, 1, (K, Nn) if ta else (Nn, K)).astype(dt)
+        C0 = rng.uniform(-1, 1, (Nn, Nn)).astype(dt)
+        oA, oB = (f64(A).T, f64(B).T) if ta else (f64(A), f64(B))
+        if op == "syrk":
+            W = g9.syrk(A, uplo, ta, 0.7, -0.3, C0.copy(), accurate=acc)
+            ref, scale = 0.7 * oA @ oA.T - 0.3 * f64(C0), 0.7 * np.abs(oA) @ np.abs(oA).T + 0.3 * np.abs(f64(C0))
+        else:
+            W = g9.syr2k(A, B, uplo, ta, 0.7, -0.3, C0.copy(), accurate=acc)
+            ref = 0.7 * (oA @ oB.T + oB @ oA.T) - 0.3 * f64(C0)
+            scale = 0.7 * (np.abs(oA) @ np.abs(oB).T + np.abs(oB) @ np.abs(oA).T) + 0.3 * np.abs(f64(C0))
+        _check(W, ref, scale, tol, mask, tag)
+        assert np.array_equal(W[~mask], C0[~mask]), f"{tag}: the other triangle changed"
+    elif op == "trmm":
+        A, B = rng.uniform(-1, 1, (n, n)).astype(dt), rng.uniform(-1, 1, (M, N)).astype(dt)
+        T = np.tril(f64(A)) if uplo == "L" else np.triu(f64(A))
+        if dg:
+            np.fill_diagonal(T, 1.0)
+        T = T.T if ta else T
+        W = g9.trmm(A, B, side, uplo, ta, dg, -2.0, accurate=acc)
+        P = T @ f64(B) if side == "L" else f64(B) @ T
+        Pa = np.abs(T) @ np.abs(f64(B)) if side == "L" else np.abs(f64(B)) @ np.abs(T)
+        _check(W, -2.0 * P, 2.0 * Pa, tol, tag=tag)
+    else:
+        stol = {"D": 1e-12, "S": 1e-4, "H": 5e-3, "HS": 5e-3}[kind]
+        A = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+        A[np.diag_indices(n)] = n if not dg else 0.5
+        if dg:
+            A *= 1.0 / n
+            A[np.diag_indices(n)] = 123.0
+        B = rng.uniform(-1, 1, (M, N)).astype(np.float32)
+        A, B = A.astype(dt), B.astype(dt)
+        T = np.tril(f64(A)) if uplo == "L" else np.triu(f64(A))
+        if dg:
+            np.fill_diagonal(T, 1.0)
+        T = T.T if ta else T
+        Xr = np.linalg.solve(T, 2.0 * f64(B)) if side == "L" else np.linalg.solve(T.T, 2.0 * f64(B).T).T
+        X = f64(g9.trsm(A, B, side, uplo, ta, dg, 2.0, accurate=acc))
+        e = np.abs(X - Xr).max() / max(np.abs(Xr).max(), 1e-300)
+        assert e <= stol, f"{tag}: {e:.1e}"
