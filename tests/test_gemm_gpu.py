@@ -121,6 +121,44 @@ def test_gemm_random_shapes(g9, orc, torch_dev, case):
     assert zc == (7 if dev else 0), f"{tag}: zero-copy bits {zc:03b}"
 
 
+def _skinny_cases(seed, count):
+    """Seeded skinny products C = A·Wᵀ (A not transposed, B stored N×K): M from 1 to 16 (or N, when swapped), the
+    other side and K small, a multiple of 64 or 256 (the matrix-core skinny kernel takes K in 256-k groups), or in
+    80-1999."""
+    r = np.random.default_rng(seed)
+
+    def dim(big):
+        c = int(r.integers(0, 4))
+        if c == 0:
+            return int(r.integers(1, 80))
+        if c == 1:
+            return 64 * int(r.integers(1, 32))
+        if c == 2:
+            return 256 * int(r.integers(1, 9))
+        return int(r.integers(80, 2000 if big else 700))
+    out = []
+    for _ in range(count):
+        m, other, K = int(r.integers(1, 17)), dim(True), dim(False)
+        M, N = (m, other) if r.integers(0, 4) else (other, m)
+        out.append((str(r.choice(["H", "HS", "S", "D"])), M, N, K, float(r.choice([1.0, -0.75])),
+                    float(r.choice([0.0, 0.0, 1.0, 0.5])), bool(r.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("case", _skinny_cases(2028, 128), ids=lambda c: "-".join(str(v) for v in c))
+def test_skinny_random_shapes(g9, orc, torch_dev, case):
+    """128 seeded random skinny products (one side at most 16, A not transposed, B stored N×K: the skinny kernels, or
+    the roles swapped when N is the small side), every type, host and device, against float64 with the reference
+    test's bounds."""
+    kind, M, N, K, al, be, dev = case
+    W, opA, opB, C0, zc = _run_case(g9, torch_dev, kind, M, N, K, al, be, 0, 1, dev, seed=M * 131 + N * 7 + K)
+    mean, mx = orc.gemm_error(W, opA, opB, al, be, C0)
+    bmean, bmax = case_bounds(kind, K)
+    tag = f"{kind} M={M} N={N} K={K} a={al} b={be} dev={dev}"
+    assert mx <= bmax, f"{tag}: max e {mx:.2e}"
+    assert mean <= bmean, f"{tag}: mean e {mean:.2e}"
+
+
 def _sampled_rows_error(W, A, B, rows, alpha=1.0, beta=0.0, C0=None, tB=False):
     """Reference metric on sampled rows of C = alpha·A·op(B) + beta·C0 (float64)."""
     a64 = A[rows].astype(np.float64)
