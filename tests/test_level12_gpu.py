@@ -189,3 +189,72 @@ def test_host_result_waits_for_queued_work(g9, torch_dev, reps):
         finally:
             g9.set_nowait(False)
         assert got == ref, f"reps={reps} trial={trial}: {got} against {ref}"
+
+
+
+def _l12_cases(seed, count):
+    """Seeded random level-1/2 calls: operation, type, sizes (1-2999, often small), vector strides (negative ones
+    on the host only: torch has no negative strides), a column offset for A's view, and residency."""
+    r = np.random.default_rng(seed)
+
+    def size():
+        return int(r.integers(1, 64)) if r.integers(0, 2) else int(r.integers(64, 3000))
+    out = []
+    for _ in range(count):
+        dev = bool(r.integers(0, 2))
+        steps = [1, 2] if dev else [1, 2, -1, -3]
+        out.append((str(r.choice(["gemv_n", "gemv_t", "axpy", "dot", "ger"])), int(r.integers(0, 3)), size(), size(),
+                    int(r.choice(steps)), int(r.choice(steps)), int(r.integers(0, 6)), dev))
+    return out
+
+
+@pytest.mark.parametrize("case", _l12_cases(2029, 150), ids=lambda c: "-".join(str(v) for v in c))
+def test_level12_random(g9, torch_dev, case):
+    """150 seeded random GEMV (N and T, on a submatrix view), AXPY, DOT and GER calls in every type, with strided and
+    reversed vectors, host or device, against float64 with the bounds above."""
+    op, ti, M, N, sx, sy, off, dev = case
+    dt = [np.float16, np.float32, np.float64][ti]
+    tol = TOL[dt]
+    r = np.random.default_rng(M * 7 + N * 13 + ti)
+
+    def vec(n, step):
+        """(float64 copy of the values, the operand): a strided view of a host array, or of its device copy."""
+        base = r.uniform(-1, 1, n * abs(step) + 2).astype(dt)
+        v = base[1:1 + n * abs(step):abs(step)]
+        v = v[::-1] if step < 0 else v
+        if dev:
+            return v.astype(np.float64), torch_dev.from_numpy(base).cuda()[1:1 + n * step:step]
+        return v.astype(np.float64), v
+
+    def host(t):
+        return t.cpu().numpy() if hasattr(t, "cpu") else t
+    tag = f"{op} {np.dtype(dt).name} {M}x{N} sx={sx} sy={sy} off={off} dev={dev}"
+    big = r.uniform(-1, 1, (M, N + off + 3)).astype(dt)
+    Ad = big[:, off:off + N].astype(np.float64)
+    Abig = torch_dev.from_numpy(big.copy()).cuda() if dev else big.copy()
+    A = Abig[:, off:off + N]
+    if op in ("gemv_n", "gemv_t"):
+        tr = op == "gemv_t"
+        X, x = vec(M if tr else N, sx)
+        Y, y = vec(N if tr else M, sy)
+        g9.gemv(A, x, alpha=0.75, beta=-1.25, y=y, trans=tr)
+        opA = Ad.T if tr else Ad
+        check(tag, host(y), 0.75 * opA @ X - 1.25 * Y, 0.75 * np.abs(opA) @ np.abs(X) + 1.25 * np.abs(Y), tol)
+    elif op == "axpy":
+        X, x = vec(M, sx)
+        Y, y = vec(M, sy)
+        g9.axpy(-1.5, x, y)
+        check(tag, host(y), Y - 1.5 * X, np.abs(Y) + 1.5 * np.abs(X), tol)
+    elif op == "dot":
+        X, x = vec(M, sx)
+        Y, y = vec(M, sy)
+        got = g9.dot(x, y)
+        assert abs(got - float(X @ Y)) <= 1e-6 * max(float(np.abs(X) @ np.abs(Y)), 1e-30), tag
+    else:
+        X, x = vec(M, sx)
+        Y, y = vec(N, sy)
+        g9.ger(0.5, x, y, A)
+        W = host(Abig)
+        check(tag, W[:, off:off + N], Ad + 0.5 * np.outer(X, Y), np.abs(Ad) + 0.5 * np.outer(np.abs(X), np.abs(Y)),
+              tol)
+        assert np.array_equal(W[:, :off], big[:, :off]) and np.array_equal(W[:, off + N:], big[:, off + N:]), tag
