@@ -334,3 +334,89 @@ def test_level2_errors(g9):
     assert L.gen9blas_spmv(7, 0, 4, 1.0, p, px, 1, 0.0, px, 1) == -2
     assert L.gen9blas_tpsv(1, 0, 0, 0, 0, None, None, 1) == 0
     assert L.gen9blas_syr2(1, 0, -1, 1.0, None, 1, None, 1, None, 1) == 0
+
+
+def _l2_cases(seed, count):
+    """Seeded random level-2 calls on full, band and packed storage: operation, type, order (small, near a multiple
+    of 64, mid-sized, or 1280-1399 for the solves on inverted blocks), band width, triangle, transpose, unit diagonal
+    and x's stride."""
+    r = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        op = str(r.choice(["symv", "trmv", "trsv", "sbmv", "tbmv", "tbsv", "spmv", "tpmv", "tpsv"]))
+        c = int(r.integers(0, 4))
+        n = (int(r.integers(1, 80)) if c == 0 else max(1, 64 * int(r.integers(1, 16)) + int(r.integers(-3, 4)))
+             if c == 1 else int(r.integers(80, 1000)) if c == 2 else int(r.integers(1280, 1400)))
+        out.append((op, int(r.integers(0, 3)), n, int(r.integers(0, 40)), str(r.choice(["L", "U"])),
+                    bool(r.integers(0, 2)), bool(r.integers(0, 2)), int(r.choice([1, 2, -1, -3]))))
+    return out
+
+
+@pytest.mark.parametrize("case", _l2_cases(2030, 120), ids=lambda c: "-".join(str(v) for v in c))
+def test_level2_random(g9, orc, case):
+    """120 seeded random products and solves on full, band and packed storage in every type, against the oracle's
+    float64 restatement of each storage format, with the bounds above (solves on well-conditioned triangles)."""
+    op, ti, n, K, uplo, tr, dg, sx = case
+    dt = DTYPES[ti]
+    tol = TOL[dt]
+    r = np.random.default_rng(n * 31 + K * 7 + ti)
+
+    def vec(step):
+        base = r.uniform(-1, 1, n * abs(step) + 2).astype(dt)
+        v = base[1:1 + n * abs(step):abs(step)]
+        return v[::-1] if step < 0 else v
+    tag = f"{op} {np.dtype(dt).name} n={n} K={K} {uplo} tr={tr} diag={dg} incx={sx}"
+    D = f64(r.uniform(-1, 1, (n, n)).astype(dt))
+    K = min(K, max(n - 1, 0))
+    KL, KU = (0, K) if uplo == "U" else (K, 0)
+    solve = op.endswith("sv")
+    if solve:   # well conditioned: small off-diagonal entries, diagonal 1..2
+        D = D / max(n if op != "tbsv" else K, 1) / 4
+        np.fill_diagonal(D, 1 + np.abs(np.diag(D)) * 4)
+        D = f64(D.astype(dt))
+    x = vec(sx)
+    X = f64(x)
+    if op in ("symv", "trmv", "trsv"):
+        A = D.astype(dt)
+        T = orc.triangle(D, uplo, dg)
+        if op == "symv":
+            ref, scale = orc.mv(orc.symmetric(D, uplo), x, 1.5)
+            check(tag, g9.symv(A, x, uplo=uplo, alpha=1.5), ref, scale, tol)
+        elif op == "trmv":
+            ref, scale = orc.mv(T.T if tr else T, x)
+            g9.trmv(A, x, uplo=uplo, trans=tr, diag=dg)
+            check(tag, x, ref, scale, tol)
+        else:
+            ref = orc.solve(T.T if tr else T, X)
+            g9.trsv(A, x, uplo=uplo, trans=tr, diag=dg)
+            check(tag, x, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+    elif op in ("sbmv", "tbmv", "tbsv"):
+        Tb = D * band_mask(n, n, KL, KU)
+        P = to_band(Tb, KL, KU).astype(dt)
+        T = orc.triangle(orc.band_dense(P, n, n, KL, KU), uplo, dg)
+        if op == "sbmv":
+            ref, scale = orc.mv(orc.symmetric(Tb, uplo), x, -0.5)
+            check(tag, g9.sbmv(P, x, K, uplo=uplo, alpha=-0.5), ref, scale, tol)
+        elif op == "tbmv":
+            ref, scale = orc.mv(T.T if tr else T, x)
+            g9.tbmv(P, x, K, uplo=uplo, trans=tr, diag=dg)
+            check(tag, x, ref, scale, tol)
+        else:
+            ref = orc.solve(T.T if tr else T, X)
+            g9.tbsv(P, x, K, uplo=uplo, trans=tr, diag=dg)
+            check(tag, x, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+    else:
+        Tp = orc.triangle(D, uplo)
+        Ap = pack(Tp, uplo).astype(dt)
+        T = orc.triangle(orc.packed_dense(Ap, n, uplo), uplo, dg)
+        if op == "spmv":
+            ref, scale = orc.mv(orc.symmetric(Tp, uplo), x, 0.25)
+            check(tag, g9.spmv(Ap, x, uplo=uplo, alpha=0.25), ref, scale, tol)
+        elif op == "tpmv":
+            ref, scale = orc.mv(T.T if tr else T, x)
+            g9.tpmv(Ap, x, uplo=uplo, trans=tr, diag=dg)
+            check(tag, x, ref, scale, tol)
+        else:
+            ref = orc.solve(T.T if tr else T, X)
+            g9.tpsv(Ap, x, uplo=uplo, trans=tr, diag=dg)
+            check(tag, x, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
