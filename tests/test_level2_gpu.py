@@ -142,11 +142,11 @@ def pack(D, uplo):
 
 
 @pytest.mark.parametrize("dt", DTYPES)
-@pytest.mark.parametrize("n", [1280, 1300])
+@pytest.mark.parametrize("n", [1280, 1300, 4100])
 def test_trsv_blocked_inverse(g9, orc, dt, n):
     """TRSV from order 1280 up runs on inverted 256-row diagonal blocks (x_q = inv(D_q)·r_q − E_q·x_(q-1), inverses in
     FP64): n = 1280 is the smallest such order (5 whole blocks), n = 1300 ends on a partial block of 20 rows (the
-    last in solve order, at the start of A for a backward solve). Both triangles, both transposes, unit and stored
+    last in solve order, at the start of A for a backward solve), n = 4100 on one of 4 rows after 16 whole blocks. Both triangles, both transposes, unit and stored
     diagonals, a negative-stride x, and the unreferenced triangle (and a unit diagonal) filled with huge values, which
     must not be read into the result."""
     A = rng.uniform(-1, 1, (n, n)).astype(dt)
