@@ -201,8 +201,8 @@ int is_device(const void *p, size_t bytes) { return mem_kind(p, bytes) == MEM_DE
 // device), or copy chunk i out while chunks i+1.. are in flight (back to the host). A 2D transfer (re-pitched rows)
 // is chunked by whole rows. GEN9BLAS_STAGE=0 leaves every transfer to hipMemcpy.
 namespace stage {
-// 4 chunks of 8 MiB and 6 threads: HGEMM n = 4096 on pageable buffers 2.33 ms per call (3 × 8 MiB, 4 threads: 2.48;
-// 2 MiB chunks: 2.74; unstaged: 4.2-6.6)
+// 4 chunks of 8 MiB and 6 threads: HGEMM n = 4096 on pageable buffers 2.30-2.33 ms per call (3 × 8 MiB, 4 threads:
+// 2.48; 8 threads: 2.30-2.31, 12: 2.36-2.37; 2 MiB chunks: 2.74; unstaged: 4.2-6.6)
 constexpr size_t CHUNK = 8u << 20, MIN_BYTES = 4u << 20;
 constexpr int NBUF = 4, NTHREADS = 6;
 static char *buf[NBUF];
