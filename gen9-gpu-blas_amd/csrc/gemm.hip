@@ -76,6 +76,88 @@ static void describe(Operand &o, const void *p, long long rows, long long cols, 
     }
 }
 
+// A single product whose C lies in pageable host memory and spans at least two pinned chunks (HGEMM n = 4096: 32 MiB)
+// is computed in row panels of at most one chunk of C each, so that copies and kernels overlap: panel p's kernel
+// runs while panel p + 1's inputs come in, and panel p's rows of C go back while the next inputs move and the host
+// copies out the panel before. A comes in panel by panel when its panel rows are contiguous (not transposed,
+// pageable, not re-pitched); B, and an A that is not, come in whole first. C comes in per panel when beta ≠ 0 or its
+// rows have gaps, which the copy back must keep. Each panel is the product over a band of rows, as run_gemm's bands
+// are, with the same kernels. With GEN9BLAS_PROFILE the reported time spans the panels' copies too. `taken` is false
+// when the product does not qualify (nothing is done then).
+constexpr size_t PANEL_MIN = 16u << 20;
+static int gemm_panels(bool &taken, int type, int tA, int tB, int M, int N, int K, double alpha, const void *A, int lda,
+                       const void *B, int ldb, double beta, void *C, int ldc, double t0) {
+    taken = false;
+    const size_t es = elem_size(type);
+    const size_t cspan = ((size_t)(M - 1) * ldc + N) * es, cdense = (size_t)M * N * es;
+    if (cspan < PANEL_MIN || cspan > 2 * cdense || mem_kind(C, cspan) != MEM_HOST) return 0;
+    const size_t chunk = out_chunk(), rowb = (size_t)ldc * es;
+    const long long pr = chunk ? (long long)(chunk / rowb) / 256 * 256 : 0;   // rows per panel
+    if (pr < 256 || pr >= M) return 0;
+    taken = true;
+    const size_t aspan = tA ? 0 : ((size_t)(M - 1) * lda + K) * es;
+    const bool pa = !tA && aspan <= 2 * (size_t)M * K * es && mem_kind(A, aspan) == MEM_HOST;
+    const bool c_in = beta != 0.0 || ldc != N;
+
+    Operand ops[3];
+    describe(ops[0], A, tA ? K : M, tA ? M : K, lda, 0, 1, (int)es);
+    describe(ops[1], B, tB ? N : K, tB ? K : N, ldb, 0, 1, (int)es);
+    describe(ops[2], C, M, N, ldc, 0, 1, (int)es);
+    G9_TRY(resolve(ops[0], SLOT_A, !pa, false, !pa));
+    G9_TRY(resolve(ops[1], SLOT_B, true, false, true));
+    G9_TRY(resolve(ops[2], SLOT_C, false, false, false));   // pageable, not re-pitched: ld = ldc, filled per panel
+    last_zc = (ops[0].zc ? 1 : 0) | (ops[1].zc ? 2 : 0);
+    char *Ad = (char *)ops[0].dev, *Cd = (char *)ops[2].dev;
+    const long long Ald = ops[0].ld;
+    auto rows_of = [&](long long p) { return M - p * pr < pr ? M - p * pr : pr; };
+    auto cbytes = [&](long long p) { return ((size_t)(rows_of(p) - 1) * ldc + N) * es; };
+    const long long np = (M + pr - 1) / pr;
+    auto issue = [&](long long p) -> int {   // panel p: its inputs on the second stream, then its kernel
+        const long long i0 = p * pr, rows = rows_of(p);
+        const size_t co = (size_t)i0 * ldc * es;
+        if (pa) {
+            const size_t ao = (size_t)i0 * lda * es;
+            G9_TRY(stage_in(Ad + ao, (const char *)A + ao, ((size_t)(rows - 1) * lda + K) * es));
+        }
+        if (c_in) G9_TRY(stage_in(Cd + co, (const char *)C + co, cbytes(p)));
+        if (pa || c_in) G9_TRY(stage_in_ready());
+        GemmCall g;
+        g.type = type;
+        g.tA = tA; g.tB = tB;
+        g.M = (int)rows; g.N = N; g.K = K;
+        g.count = 1;
+        g.alpha = alpha;
+        g.beta = beta;
+        g.A = Ad + (size_t)(tA ? i0 : i0 * Ald) * es; g.lda = Ald; g.sA = 0;
+        g.B = ops[1].dev; g.ldb = ops[1].ld; g.sB = 0;
+        g.C = Cd + co; g.ldc = ldc; g.sC = 0;
+        G9_TRY(run_gemm(g));
+        return out_mark((int)(p & 1));
+    };
+    auto host_c = [&](long long p) { return (char *)C + (size_t)p * pr * ldc * es; };
+    // Second stream: A0 A1 C0 A2 C1 A3 C2 C3 (each result queued behind the next panel's inputs, which do not wait
+    // for its kernel); the host copies C(p - 1) out while C(p) and A(p + 1) move.
+    auto run = [&]() -> int {
+        prof_begin();
+        G9_TRY(issue(0));
+        for (long long p = 0; p < np; p++) {
+            if (p + 1 < np) G9_TRY(issue(p + 1));
+            G9_TRY(out_start((int)(p & 1), Cd + (size_t)p * pr * ldc * es, cbytes(p)));
+            if (p > 0) G9_TRY(out_finish((int)((p - 1) & 1), host_c(p - 1), cbytes(p - 1)));
+        }
+        G9_TRY(out_finish((int)((np - 1) & 1), host_c(np - 1), cbytes(np - 1)));
+        prof_end();
+        return wait_stream();
+    };
+    const int r = run();
+    if (r) {
+        out_drain();
+        return r;
+    }
+    prof_collect(t0);
+    return 0;
+}
+
 int gemm_impl(int type, int tA, int tB, int M, int N, int K, double alpha, const void *A, int lda, long long sA,
                      const void *B, int ldb, long long sB, double beta, void *C, int ldc, long long sC, int count) {
     const double t0 = now_s();
@@ -89,6 +171,13 @@ int gemm_impl(int type, int tA, int tB, int M, int N, int K, double alpha, const
         G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "gemm: leading dimension too small (lda %d, ldb %d, ldc %d)", lda, ldb, ldc);
     if (count > 1 && (sA < 0 || sB < 0 || sC < 0)) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "gemm_batched: negative stride");
     const int es = elem_size(type);
+    const int mn = M < N ? M : N;
+    const bool skinny = count == 1 && mn <= skinny_threshold(type) && !tA && tB;
+    if (count == 1 && !skinny) {
+        bool taken;
+        const int r = gemm_panels(taken, type, tA, tB, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, t0);
+        if (taken) return r;
+    }
 
     Operand ops[3];
     describe(ops[0], A, tA ? K : M, tA ? M : K, lda, sA, count, es);
@@ -103,8 +192,7 @@ int gemm_impl(int type, int tA, int tB, int M, int N, int K, double alpha, const
     const long long Ld = count == 1 ? ops[0].ld : lda, Bld = count == 1 ? ops[1].ld : ldb, Cld = count == 1 ? ops[2].ld : ldc;
 
     prof_begin();
-    const int mn = M < N ? M : N;
-    if (count == 1 && mn <= skinny_threshold(type) && !tA && tB) {
+    if (skinny) {
         // both streamed operands K-contiguous: C = alpha·a·wᵀ + beta·C with the small side as a
         SkinnyCall s;
         s.type = type;

@@ -81,6 +81,20 @@ G9_HIDDEN int is_device(const void *p, size_t bytes);
 G9_HIDDEN int finish(Operand *ops, int n, bool host_copy = false);
 // Waits for the stream (no copies). 0 or an error.
 G9_HIDDEN int wait_stream();
+// Copies beside the kernels, on a second stream (available when out_chunk() > 0). stage_in: pageable host bytes
+// into device memory, through the pinned ring when large (returns once the host side is copied; the DMA is queued);
+// stage_in_ready: work queued on the library stream from now on waits for the inputs queued so far. out_chunk() is
+// the most one result piece may hold (0: not available); out_mark(q) marks the work queued so far on the library
+// stream; out_start(q, dev, bytes) queues the piece, once that marked work is done, into pinned chunk q (0 or 1);
+// out_finish(q, host, bytes) waits for it and copies it to the host. out_drain() waits for the second stream (after an error, before buffers it may still
+// read are reused).
+G9_HIDDEN int stage_in(void *dev, const void *host, size_t bytes);
+G9_HIDDEN int stage_in_ready();
+G9_HIDDEN size_t out_chunk();
+G9_HIDDEN int out_mark(int q);
+G9_HIDDEN int out_start(int q, const void *dev, size_t bytes);
+G9_HIDDEN int out_finish(int q, void *host, size_t bytes);
+G9_HIDDEN void out_drain();
 // Waits for the stream through a completion word set by a kernel queued behind the call's work (falls back to
 // wait_stream); for calls whose device-to-host copies, if any, go into page-locked memory.
 G9_HIDDEN int wait_done();

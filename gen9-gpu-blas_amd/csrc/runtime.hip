@@ -208,6 +208,7 @@ constexpr int NBUF = 4, NTHREADS = 6;
 static char *buf[NBUF];
 static hipEvent_t done[NBUF];
 static bool used[NBUF];
+static int cursor;  // next chunk to fill: consecutive transfers go round the ring instead of waiting on chunk 0
 static int state;   // 0: not set up, 1: on, -1: off
 
 // A pool of NTHREADS - 1 copy threads; the caller runs part 0 of each job. Never destroyed: the threads wait on the
@@ -303,43 +304,45 @@ static void plan(size_t width, size_t rows, size_t pitch, size_t &unit, size_t &
         per_chunk = CHUNK / pitch;
     }
 }
-// host (row stride hpitch) → device (row stride dpitch), rows of width bytes; enqueued on the library stream
+// host (row stride hpitch) → device (row stride dpitch), rows of width bytes; enqueued on stream s
 static char *bounce_take(size_t bytes);
-static int h2d(char *dev, size_t dpitch, const char *host, size_t hpitch, size_t width, size_t rows, bool pinned) {
+static int h2d(char *dev, size_t dpitch, const char *host, size_t hpitch, size_t width, size_t rows, bool pinned,
+               hipStream_t s) {
     const size_t total = rows == 1 ? width : rows * dpitch;
     if (pinned) {   // page-locked: one asynchronous DMA straight from the caller's memory
-        if (rows == 1) G9_HIP(hipMemcpyAsync(dev, host, width, hipMemcpyHostToDevice, stream));
-        else G9_HIP(hipMemcpy2DAsync(dev, dpitch, host, hpitch, width, rows, hipMemcpyHostToDevice, stream));
+        if (rows == 1) G9_HIP(hipMemcpyAsync(dev, host, width, hipMemcpyHostToDevice, s));
+        else G9_HIP(hipMemcpy2DAsync(dev, dpitch, host, hpitch, width, rows, hipMemcpyHostToDevice, s));
         return 0;
     }
     if (char *bb = bounce_take(rows == 1 ? width : rows * width)) {   // small: through the pinned bounce area
         if (rows == 1) {
             memcpy(bb, host, width);
-            G9_HIP(hipMemcpyAsync(dev, bb, width, hipMemcpyHostToDevice, stream));
+            G9_HIP(hipMemcpyAsync(dev, bb, width, hipMemcpyHostToDevice, s));
         } else {
             for (size_t r = 0; r < rows; r++) memcpy(bb + r * width, host + r * hpitch, width);
-            G9_HIP(hipMemcpy2DAsync(dev, dpitch, bb, width, width, rows, hipMemcpyHostToDevice, stream));
+            G9_HIP(hipMemcpy2DAsync(dev, dpitch, bb, width, width, rows, hipMemcpyHostToDevice, s));
         }
         return 0;
     }
     if (total < MIN_BYTES || !on() || (rows > 1 && dpitch > CHUNK)) {
-        if (rows == 1) G9_HIP(hipMemcpyAsync(dev, host, width, hipMemcpyHostToDevice, stream));
-        else G9_HIP(hipMemcpy2DAsync(dev, dpitch, host, hpitch, width, rows, hipMemcpyHostToDevice, stream));
+        if (rows == 1) G9_HIP(hipMemcpyAsync(dev, host, width, hipMemcpyHostToDevice, s));
+        else G9_HIP(hipMemcpy2DAsync(dev, dpitch, host, hpitch, width, rows, hipMemcpyHostToDevice, s));
         return 0;
     }
     size_t unit, units, per;
     plan(width, rows, dpitch, unit, units, per);
-    int b = 0;
+    int b = cursor;
     for (size_t u0 = 0; u0 < units; u0 += per) {
         const size_t n = units - u0 < per ? units - u0 : per;
         if (used[b]) G9_HIP(hipEventSynchronize(done[b]));   // the DMA that last read this chunk has finished
         if (rows == 1) pcopy(buf[b], 0, host + u0, 0, n, 1);
         else pcopy(buf[b], dpitch, host + u0 * hpitch, hpitch, width, n);
-        G9_HIP(hipMemcpyAsync(dev + u0 * unit, buf[b], n * unit, hipMemcpyHostToDevice, stream));
-        G9_HIP(hipEventRecord(done[b], stream));
+        G9_HIP(hipMemcpyAsync(dev + u0 * unit, buf[b], n * unit, hipMemcpyHostToDevice, s));
+        G9_HIP(hipEventRecord(done[b], s));
         used[b] = true;
         b = b + 1 == NBUF ? 0 : b + 1;
     }
+    cursor = b;
     return 0;
 }
 // device (row stride dpitch) → host (row stride hpitch); returns once the data is in host memory
@@ -369,6 +372,29 @@ static int d2h(char *host, size_t hpitch, const char *dev, size_t dpitch, size_t
 static bool d2h_staged(size_t width, size_t rows, size_t dpitch) {
     const size_t total = rows == 1 ? width : rows * dpitch;
     return total >= MIN_BYTES && on() && !(rows > 1 && dpitch > CHUNK);
+}
+
+// A second stream (default flags and priority) for copies that run beside the library stream's kernels: inputs
+// through the ring above, and results, in pieces of at most one chunk, each into one of two pinned chunks of its own.
+// The kernels wait for the inputs, and the results for the kernels, through events; the DMA engine then never waits
+// for a kernel it does not depend on.
+static hipStream_t ostream;
+static char *obuf[2];
+static hipEvent_t kdone[2], odone[2], iready;
+static bool oused[2];
+static int ostate;   // 0: not set up, 1: on, -1: off
+static bool out_on() {
+    if (ostate == 0) {
+        ostate = on() && hipStreamCreate(&ostream) == hipSuccess &&
+                 hipEventCreateWithFlags(&iready, hipEventDisableTiming) == hipSuccess ? 1 : -1;
+        for (int q = 0; q < 2 && ostate > 0; q++)
+            if (hipHostMalloc((void **)&obuf[q], CHUNK, hipHostMallocDefault) != hipSuccess ||
+                hipEventCreateWithFlags(&kdone[q], hipEventDisableTiming) != hipSuccess ||
+                hipEventCreateWithFlags(&odone[q], hipEventDisableTiming) != hipSuccess)
+                ostate = -1;
+        if (ostate < 0) (void)hipGetLastError();   // no second direction: results go back after the whole product
+    }
+    return ostate > 0;
 }
 
 // Small transfers (at most SMALL bytes) go through a pinned bounce area instead: the host copies into it (or out of
@@ -435,14 +461,51 @@ int resolve(Operand &op, int slot, bool copy_in, bool written, bool repitch) {
         G9_TRY(scratch(slot, pitch * (size_t)op.rows, &op.dev));
         if (copy_in)
             G9_TRY(stage::h2d((char *)op.dev, pitch, (const char *)op.host, (size_t)op.caller_ld * es, (size_t)op.cols * es,
-                              (size_t)op.rows, op.pinned));
+                              (size_t)op.rows, op.pinned, stream));
         return 0;
     }
     op.ld = op.caller_ld;
     G9_TRY(scratch(slot, span, &op.dev));
     // the copy back rewrites the whole span: gap elements of a written operand must hold the caller's values
     if (written && span > dense) copy_in = true;
-    if (copy_in) G9_TRY(stage::h2d((char *)op.dev, span, (const char *)op.host, span, span, 1, op.pinned));
+    if (copy_in) G9_TRY(stage::h2d((char *)op.dev, span, (const char *)op.host, span, span, 1, op.pinned, stream));
+    return 0;
+}
+
+size_t out_chunk() { return stage::out_on() ? stage::CHUNK : 0; }
+
+int out_mark(int q) {
+    G9_HIP(hipEventRecord(stage::kdone[q], stream));
+    return 0;
+}
+
+int out_start(int q, const void *dev, size_t bytes) {
+    using namespace stage;
+    if (oused[q]) G9_HIP(hipEventSynchronize(odone[q]));   // the piece last in this chunk has left it
+    G9_HIP(hipStreamWaitEvent(ostream, kdone[q], 0));
+    G9_HIP(hipMemcpyAsync(obuf[q], dev, bytes, hipMemcpyDeviceToHost, ostream));
+    G9_HIP(hipEventRecord(odone[q], ostream));
+    oused[q] = true;
+    return 0;
+}
+
+int out_finish(int q, void *host, size_t bytes) {
+    G9_HIP(hipEventSynchronize(stage::odone[q]));
+    stage::pcopy((char *)host, 0, stage::obuf[q], 0, bytes, 1);
+    return 0;
+}
+
+void out_drain() {
+    if (stage::ostate > 0) (void)hipStreamSynchronize(stage::ostream);
+}
+
+int stage_in(void *dev, const void *host, size_t bytes) {
+    return stage::h2d((char *)dev, bytes, (const char *)host, bytes, bytes, 1, false, stage::ostream);
+}
+
+int stage_in_ready() {
+    G9_HIP(hipEventRecord(stage::iready, stage::ostream));
+    G9_HIP(hipStreamWaitEvent(stream, stage::iready, 0));
     return 0;
 }
 

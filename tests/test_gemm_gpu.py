@@ -324,6 +324,74 @@ def test_host_operands_staged(g9):
     assert np.array_equal(big_c[mask], keep[mask]), "write outside the C slice"
 
 
+def test_host_products_in_row_panels(g9, torch_dev):
+    """Products whose C is pageable and spans two or more 8 MiB pinned chunks run in row panels of at most one chunk
+    of C: each panel's rows go back on a second stream while the next panel's inputs come in. Covered: 4 FP16 panels
+    of 1024 rows (A in panels); FP32 with transposed A (staged whole), transposed B, beta = 2 and C a column slice
+    whose row gaps must survive the copy back, 6 panels with a last one of 40 rows; FP64 with page-locked A and a
+    last panel of 252 rows; accurate FP16 in 2 panels. Small integers make the first two exact. The FP16 results must
+    equal the same product on device buffers bit for bit (each panel is a band of rows, tiled like the whole); FP64
+    meets the float64 bound, and so does its difference from the device result, as a 512-row panel may take tiles
+    that split K differently from the whole product's."""
+    torch = torch_dev
+    rng = np.random.default_rng(43)
+
+    def ints(shape, dt, lim):
+        return rng.integers(-lim, lim + 1, shape).astype(dt)
+
+    def on_device(A, B, alpha, beta, C0, accurate=False):
+        Ad = _to_dev(torch, A.T).t() if A.flags.f_contiguous and not A.flags.c_contiguous else _to_dev(torch, A)
+        Bd = _to_dev(torch, B.T).t() if B.flags.f_contiguous and not B.flags.c_contiguous else _to_dev(torch, B)
+        Cd = _to_dev(torch, C0)
+        g9.gemm(Ad, Bd, alpha, beta, Cd, accurate=accurate)
+        torch.cuda.synchronize()
+        return Cd.cpu().numpy()
+
+    # FP16, NN, 4096 x 4096 x 1024 in {-1, 0, 1}: every sum is an integer of at most 1024, exact in FP16
+    A, B = ints((4096, 1024), np.float16, 1), ints((1024, 4096), np.float16, 1)
+    C = np.zeros((4096, 4096), np.float16)
+    g9.gemm(A, B, 1.0, 0.0, C)
+    ref = A.astype(np.int64) @ B.astype(np.int64)
+    assert np.array_equal(C.astype(np.int64), ref), "FP16 panels"
+    assert np.array_equal(C, on_device(A, B, 1.0, 0.0, np.zeros_like(C))), "FP16 panels against device buffers"
+
+    # FP32, A and B transposed views, C a 2600 x 3000 slice of 2600 x 3100 (gaps), beta = 2
+    at, bt = ints((700, 2600), np.float32, 2), ints((3000, 700), np.float32, 2)
+    A, B = at.T, bt.T
+    big_c = ints((2600, 3100), np.float32, 2)
+    keep = big_c.copy()
+    C = big_c[:, :3000]
+    g9.gemm(A, B, 1.0, 2.0, C)
+    ref = A.astype(np.int64) @ B.astype(np.int64) + 2 * keep[:, :3000].astype(np.int64)
+    assert np.array_equal(C.astype(np.int64), ref), "FP32 panels, transposed, beta = 2"
+    assert np.all(big_c[:, 3000:] == keep[:, 3000:]), "gap columns of C changed"
+    assert np.array_equal(C, on_device(A, B, 1.0, 2.0, keep[:, :3000].copy())), "FP32 panels against device buffers"
+
+    # FP64, page-locked A, pageable B and C, alpha = -0.5, beta = 0.25
+    A = g9.empty((2300, 300), np.float64)
+    A[:] = rng.uniform(-1, 1, A.shape)
+    B = rng.uniform(-1, 1, (300, 2048))
+    C0 = rng.uniform(-1, 1, (2300, 2048))
+    C = C0.copy()
+    g9.gemm(A, B, -0.5, 0.25, C)
+    rows = np.unique(np.r_[0, 511, 512, 2047, 2048, 2299, rng.integers(0, 2300, 40)])
+    mean, mx = _sampled_rows_error(C, np.asarray(A), B, rows, alpha=-0.5, beta=0.25, C0=C0)
+    assert mx <= MAX_E["D"], f"FP64 panels: max e {mx:.2e}"
+    scale = 0.5 * (np.abs(np.asarray(A)) @ np.abs(B)) + 0.25 * np.abs(C0)
+    d = np.abs(C - on_device(np.asarray(A), B, -0.5, 0.25, C0)) / scale
+    assert d.max() <= MAX_E["D"], f"FP64 panels against device buffers: {d.max():.2e}"
+
+    # accurate FP16, 4096 x 2048 x 512 on N(0, 1): C is 16 MiB, two panels of 2048 rows
+    A = rng.standard_normal((4096, 512)).astype(np.float16)
+    B = rng.standard_normal((512, 2048)).astype(np.float16)
+    C = np.zeros((4096, 2048), np.float16)
+    g9.gemm(A, B, 1.0, 0.0, C, accurate=True)
+    rows = np.unique(np.r_[0, 2047, 2048, 4095, rng.integers(0, 4096, 40)])
+    mean, mx = _sampled_rows_error(C, A, B, rows)
+    assert mx <= case_bounds("HS", 512)[1] and mean <= case_bounds("HS", 512)[0], f"HS panels: {mean:.2e} / {mx:.2e}"
+    assert np.array_equal(C, on_device(A, B, 1.0, 0.0, np.zeros_like(C), accurate=True)), "HS panels against device"
+
+
 def test_gemm_beta_zero_does_not_read_c(g9, torch_dev):
     """beta = 0: C is not read, NaN in C does not propagate (reference: lib/gen9blas.h:133 semantics for C)."""
     for dt in (np.float16, np.float32, np.float64):
