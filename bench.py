@@ -39,8 +39,8 @@ GEMM_CASES = {
     "dgemm_n1024": ("D", 1024), "dgemm_n4096": ("D", 4096),
     "sgemm_odd_3000x11008x4096_tB_beta05": ("S", None),
 }
-QUICK = ("hgemm_n4096", "hgemm_accurate_n4096", "hbm_read_1GiB", "skinny")
-OTHER_CASES = ("hgemm_n4096_host", "hbm_read_1GiB", "skinny", "skinny_read_floor", "packed_decode", "level3_n4096",
+QUICK = ("hgemm_n4096", "hgemm_accurate_n4096", "hbm_read_1GiB", "skinny", "skinny_kn")
+OTHER_CASES = ("hgemm_n4096_host", "hbm_read_1GiB", "skinny", "skinny_kn", "skinny_read_floor", "packed_decode", "level3_n4096",
                "saxpy_2^26", "sdot_2^26", "sgemv_16384", "level2_16384", "copy_256MiB", "calibration", "mfma_ceiling")
 CALIB_LIB = os.path.join(ROOT, "gen9-gpu-blas_amd", "libgen9blas_calib.so")   # calibration kernels (calib/calibrate.hip)
 
@@ -238,8 +238,8 @@ def main():
             res["copy_256MiB"] = hbm_fracs({"ms": round(ms, 4), "GBs": round(8.0 * n / (ms * 1e-3) / 1e9, 1)})
             log("copy_256MiB", res["copy_256MiB"])
         del xd, yd
-    # ---------------- skinny C = A·Wᵀ, W 4096² fp16, 32 rotated copies (1 GiB) ----------------
-    if cases & {"skinny", "skinny_read_floor"}:
+    # ---------------- skinny C = A·Wᵀ, W 4096² fp16, 32 rotated copies (1 GiB); then W stored K×N ----------------
+    if cases & {"skinny", "skinny_kn", "skinny_read_floor"}:
         K = N = 4096
         ncopy = 32
         Wd = torch.empty((ncopy, N, K), dtype=torch.float16, device=dev)
@@ -262,7 +262,31 @@ def main():
             byts = 2.0 * N * K + 2.0 * M * K + 2.0 * M * N
             sk[f"M{M}"] = hbm_fracs({"us_per_call": round(ms * 1e3, 2), "GBs": round(byts / (ms * 1e-3) / 1e9, 1)})
             log("skinny", M, sk[f"M{M}"])
-        res["skinny_fp16_4096x4096"] = sk
+        if sk:
+            res["skinny_fp16_4096x4096"] = sk
+        if "skinny_kn" in cases:
+            # the same products with W stored K×N (row-major x·W, weights contiguous along N): the same 32 copies,
+            # transposed on the device
+            Wkn = Wd.transpose(1, 2).contiguous()
+            torch.cuda.synchronize()
+            wq = [Wkn[c].data_ptr() for c in range(ncopy)]
+            skn = {}
+            for M in (1, 2, 4, 8, 16):
+                Ad = to_dev(np.random.default_rng(1).standard_normal((M, K), dtype=np.float32).astype(np.float16))
+                Cd = torch.empty((M, N), dtype=torch.float16, device=dev)
+                state = {"j": 0}
+
+                def fn():
+                    j = state["j"]
+                    state["j"] = (j + 1) % ncopy
+                    check(L.gen9blas_gemm(0, 0, 0, M, N, K, d(1.0), p(Ad.data_ptr()), K, p(wq[j]), N, d(0.0),
+                                          p(Cd.data_ptr()), N))
+                ms = timed(fn, k=kshort, w=max(warm, 32))
+                byts = 2.0 * N * K + 2.0 * M * K + 2.0 * M * N
+                skn[f"M{M}"] = hbm_fracs({"us_per_call": round(ms * 1e3, 2), "GBs": round(byts / (ms * 1e-3) / 1e9, 1)})
+                log("skinny_kn", M, skn[f"M{M}"])
+            res["skinny_kn_fp16_4096x4096"] = skn
+            del Wkn
         if "skinny_read_floor" in cases:
             # the floor of one skinny call: a pure read of the same 32 MiB weight copy per call, over the same 32
             # rotated copies, by the calibration streaming-read kernel (one kernel per call, as the skinny product) with
@@ -524,7 +548,41 @@ def main():
         "cpu_baseline": cpu,
         "results": res,
     }
+    summary = config_summary(res)
+    line["summary"] = summary   # last key: the end of the line (what a tail keeps) holds every configuration
     print(json.dumps(line), flush=True)
+    for s in summary:
+        log(s)
+
+
+def config_summary(res):
+    """One short line per BASELINE configuration measured (GPU rate, fraction of its roofline, the CPU path's rate),
+    printed last so that a truncated log still holds every configuration."""
+    cpu = res.get("cpu_path", {})
+
+    def cpu_of(key, unit):
+        v = cpu.get(key)
+        return f" | cpu {v['value']:g} {unit}" if v else ""
+    out = []
+    for name, (kind, n) in GEMM_CASES.items():
+        r = res.get(name)
+        if r:
+            cname = name.replace("_accurate", "")
+            out.append(f"{name} {r['tflops']:.1f} TF/s {r['frac_of_peak']:.3f} of peak{cpu_of(cname, 'TF/s')}")
+    hbm = res.get("measured_hbm_GBs", {}).get("GBs")
+    if hbm:
+        out.append(f"measured_hbm {hbm:.0f} GB/s")
+    for M, r in res.get("skinny_fp16_4096x4096", {}).items():
+        out.append(f"skinny_{M} {r['us_per_call']:.2f} us {r['GBs']:.0f} GB/s {r.get('frac_of_measured_hbm', 0):.3f} of "
+                   f"hbm{cpu_of('skinny_' + M, 'us')}")
+    for M, r in res.get("skinny_kn_fp16_4096x4096", {}).items():
+        out.append(f"skinny_kn_{M} {r['us_per_call']:.2f} us {r['GBs']:.0f} GB/s {r.get('frac_of_measured_hbm', 0):.3f} "
+                   f"of hbm")
+    for key in ("saxpy_2^26", "sdot_2^26", "sgemv_N_16384", "sgemv_T_16384"):
+        r = res.get(key)
+        if r:
+            out.append(f"{key} {r['GBs']:.0f} GB/s {r.get('frac_of_measured_hbm', 0):.3f} of hbm{cpu_of(key, 'GB/s')}")
+    return out
 
 
 def cpu_baselines(budget_s=40.0):

@@ -29,7 +29,8 @@ HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC", "-fvisibilit
              "-Wall", "-Wno-unused-function"]
 HIP_SOURCES = ["runtime.hip", "gemm.hip", "gemm_kernels.hip", "skinny.hip", "level12.hip", "level12_kernels.hip",
                "packed.hip", "level3.hip", "level2.hip", "noalloc.hip"]
-HEADERS = ["internal.h", "skinny_kernel.h", "gemm_kernel.h", "hgemm_kernel.h", "lds_dma.h", "wave.h"]
+# every header of csrc/ counts as a dependency of every object: a new header cannot be left out
+HEADERS = sorted(f for f in os.listdir(CSRC) if f.endswith(".h"))
 
 
 def _run(cmd):

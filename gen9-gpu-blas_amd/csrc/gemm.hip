@@ -4,7 +4,8 @@
 // - type check first (UNSUPPORTED), then non-positive dimensions return 0 without work;
 // - a single product with min(M, N) ≤ the skinny threshold (16 by default, GEN9BLAS_SKINNY=n overrides, never for
 //   FP64) takes the skinny kernel, with the roles of A and B swapped when N < M (Cᵀ = op(B)ᵀ·op(A)ᵀ, C written
-//   through swapped strides) — here when both streamed operands are K-contiguous, otherwise the MFMA kernel;
+//   through swapped strides), in every layout: weights contiguous along K or along N, the small operand transposed
+//   or not;
 // - everything else runs the MFMA kernel. It reads every transpose layout directly and fuses alpha/beta, so the
 //   reference's pack kernels, padded work buffers and separate epilogue have no counterpart here;
 // - GEN9BLAS_MAX_LAUNCH_MS (opt-in; the reference's default of 100 ms guarded against i915 preemption resets, which
@@ -172,7 +173,7 @@ int gemm_impl(int type, int tA, int tB, int M, int N, int K, double alpha, const
     if (count > 1 && (sA < 0 || sB < 0 || sC < 0)) G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "gemm_batched: negative stride");
     const int es = elem_size(type);
     const int mn = M < N ? M : N;
-    const bool skinny = count == 1 && mn <= skinny_threshold(type) && !tA && tB;
+    const bool skinny = count == 1 && mn <= skinny_threshold(type);
     if (count == 1 && !skinny) {
         bool taken;
         const int r = gemm_panels(taken, type, tA, tB, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, t0);
@@ -193,7 +194,8 @@ int gemm_impl(int type, int tA, int tB, int M, int N, int K, double alpha, const
 
     prof_begin();
     if (skinny) {
-        // both streamed operands K-contiguous: C = alpha·a·wᵀ + beta·C with the small side as a
+        // C = alpha·a·wᵀ + beta·C with the small side as a (reference: lib/src/gemm.c:207-221): a = op(A), w = op(B)ᵀ,
+        // or for N < M a = op(B)ᵀ, w = op(A), C written through swapped strides
         SkinnyCall s;
         s.type = type;
         s.K = K;
@@ -202,13 +204,13 @@ int gemm_impl(int type, int tA, int tB, int M, int N, int K, double alpha, const
         s.C = ops[2].dev;
         if (M <= N) {
             s.M = M; s.N = N;
-            s.a = ops[0].dev; s.sam = Ld;
-            s.w = ops[1].dev; s.swn = Bld;
+            s.a = ops[0].dev; s.sam = tA ? 1 : Ld; s.sak = tA ? Ld : 1;        // op(A)[m][k]
+            s.w = ops[1].dev; s.swn = tB ? Bld : 1; s.swk = tB ? 1 : Bld;      // op(B)[k][n]
             s.scm = Cld; s.scn = 1;
         } else {
             s.M = N; s.N = M;
-            s.a = ops[1].dev; s.sam = Bld;
-            s.w = ops[0].dev; s.swn = Ld;
+            s.a = ops[1].dev; s.sam = tB ? Bld : 1; s.sak = tB ? 1 : Bld;      // op(B)ᵀ[n][k]
+            s.w = ops[0].dev; s.swn = tA ? 1 : Ld; s.swk = tA ? Ld : 1;        // op(A)[m][k]
             s.scm = 1; s.scn = Cld;
         }
         G9_TRY(launch_skinny(s));

@@ -55,7 +55,7 @@ static int splitk_forced() {
 }
 
 // Split-K slices for a single product of `tiles` tiles: doubled while the slices still leave at most one workgroup
-// per CU and each slice keeps at least 4 k-steps, up to 8.
+// per CU and each slice keeps at least 4 k-steps, up to 8. Without a forced split, s > 1 implies tiles · s ≤ CUs.
 // Splitting changes only the FP32 (FP64) summation order: each slice sums its k-range, the slices are then added in
 // order, and alpha/beta and the rounding to the element type are applied once.
 static int splitk_slices(long long tiles, int K, int BK, int count) {
@@ -79,6 +79,7 @@ static int launch_t(GemmParams<typename Mma<T>::Sum> p, int count) {
     const int split = KG > 1 ? 1 : splitk_slices(tiles, p.K, BK, count);
     const dim3 block(C.WM * C.WN * 64 * KG);
     if (split > 1) {
+        static_assert((size_t)C.BM * C.BN * sizeof(S) <= SPLITK_TILE_BYTES_MAX, "split tile beyond the work-space bound");
         p.kper = ((p.K + split - 1) / split + BK - 1) / BK * BK;
         const int ns = (p.K + p.kper - 1) / p.kper;
         void *P;

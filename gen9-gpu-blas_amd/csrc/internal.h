@@ -46,6 +46,10 @@ G9_HIDDEN int scratch(int slot, size_t bytes, void **p);
 // placed at `base` if they fit in `bytes`, and every other request (staging of host operands, other work buffers)
 // fails with INVALID_ARG. set_fixed_workspace(nullptr, 0) returns to the growing buffers.
 G9_HIDDEN void set_fixed_workspace(void *base, size_t bytes, const char *who);
+// Largest split-K partial tile, in bytes: the FP16 256×256 tile of FP32 sums and the FP64 256×128 tile of FP64 sums.
+// A split of s > 1 slices is chosen only while tiles · s ≤ CUs, so the slices of one product never exceed
+// CUs × this many bytes (the launch asserts every split tile against it).
+constexpr size_t SPLITK_TILE_BYTES_MAX = 256 * 256 * 4;
 // Set-up of the no-allocation entry point on `dev` (called by init with `dev` current): finds the device address of
 // its static work space. A failure is kept and reported by that entry point only.
 G9_HIDDEN void noalloc_setup(int dev);
@@ -136,12 +140,12 @@ G9_HIDDEN int launch_tri_inverse(int es, const void *L, long long ld, long long 
 G9_HIDDEN int gemm_impl(int type, int tA, int tB, int M, int N, int K, double alpha, const void *A, int lda, long long sA,
                         const void *B, int ldb, long long sB, double beta, void *C, int ldc, long long sC, int count);
 struct SkinnyCall {
-    int type;                      // GEN9BLAS_H / HS / S
-    int M, N, K;                   // C (M×N) = alpha·a·wᵀ + beta·C, a M×K, w N×K, both K-contiguous
+    int type;                                // GEN9BLAS_H / HS / S
+    int M, N, K;                             // C (M×N) = alpha·a·wᵀ + beta·C, a M×K, w N×K
     double alpha, beta;
-    const void *a; long long sam;  // a[m][k] = a[m·sam + k]
-    const void *w; long long swn;  // w[n][k] = w[n·swn + k]
-    void *C; long long scm, scn;   // C[m][n] = C[m·scm + n·scn]
+    const void *a; long long sam, sak = 1;   // a[m][k] = a[m·sam + k·sak]
+    const void *w; long long swn, swk = 1;   // w[n][k] = w[n·swn + k·swk]; swk = 1 (K-contiguous) or swn = 1
+    void *C; long long scm, scn;             // C[m][n] = C[m·scm + n·scn]
 };
 G9_HIDDEN int launch_skinny(const SkinnyCall &c);
 // Level 1/2: element i of a vector is at p[o + i·inc], o = (n-1)·(-inc) for inc < 0.

@@ -1,6 +1,6 @@
 """Child process of test_skinny_gpu.py::test_skinny_forced_threshold: runs with GEN9BLAS_SKINNY=64 in its environment
-(read once, when the library first dispatches), so every product with min(M, N) ≤ 64 and both streamed operands
-K-contiguous takes a skinny kernel, M tiles of 16 rows included.
+(read once, when the library first dispatches), so every product with min(M, N) ≤ 64 takes a skinny kernel, in every
+layout, M tiles of 16 rows included.
 
 Cases follow the reference's skinny test (reference: lib/test_skinny.py:38-63): its shapes (M = 17, 33, 64 beyond the
 default threshold), both weight layouts and transposed views, the role swap for small N, alpha/beta into a slice of a

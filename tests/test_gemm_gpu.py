@@ -309,7 +309,7 @@ def test_host_operands_staged(g9):
     C0 = rng.integers(-2, 3, (3000, 3000)).astype(np.float32)
     C = C0.copy()
     g9.gemm(A, B, 1.0, 2.0, C)
-    ref = A.astype(np.int64) @ B.astype(np.int64) + 2 * C0.astype(np.int64)
+    ref = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.int64) + 2 * C0.astype(np.int64)
     assert np.array_equal(C.astype(np.int64), ref), "whole spans"
     big_a = rng.integers(-2, 3, (3000, 3000)).astype(np.float32)
     big_c = rng.integers(-2, 3, (3000, 3000)).astype(np.float32)
@@ -317,7 +317,7 @@ def test_host_operands_staged(g9):
     A2, C2 = big_a[:, 1000:2000], big_c[:, 500:1500]
     B2 = B[:1000, :1000].copy()
     g9.gemm(A2, B2, 1.0, 2.0, C2)
-    ref = A2.astype(np.int64) @ B2.astype(np.int64) + 2 * keep[:, 500:1500].astype(np.int64)
+    ref = (A2.astype(np.float64) @ B2.astype(np.float64)).astype(np.int64) + 2 * keep[:, 500:1500].astype(np.int64)
     assert np.array_equal(big_c[:, 500:1500].astype(np.int64), ref), "re-pitched rows"
     mask = np.ones(big_c.shape, bool)
     mask[:, 500:1500] = False
@@ -351,7 +351,7 @@ def test_host_products_in_row_panels(g9, torch_dev):
     A, B = ints((4096, 1024), np.float16, 1), ints((1024, 4096), np.float16, 1)
     C = np.zeros((4096, 4096), np.float16)
     g9.gemm(A, B, 1.0, 0.0, C)
-    ref = A.astype(np.int64) @ B.astype(np.int64)
+    ref = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.int64)
     assert np.array_equal(C.astype(np.int64), ref), "FP16 panels"
     assert np.array_equal(C, on_device(A, B, 1.0, 0.0, np.zeros_like(C))), "FP16 panels against device buffers"
 
@@ -362,7 +362,7 @@ def test_host_products_in_row_panels(g9, torch_dev):
     keep = big_c.copy()
     C = big_c[:, :3000]
     g9.gemm(A, B, 1.0, 2.0, C)
-    ref = A.astype(np.int64) @ B.astype(np.int64) + 2 * keep[:, :3000].astype(np.int64)
+    ref = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.int64) + 2 * keep[:, :3000].astype(np.int64)
     assert np.array_equal(C.astype(np.int64), ref), "FP32 panels, transposed, beta = 2"
     assert np.all(big_c[:, 3000:] == keep[:, 3000:]), "gap columns of C changed"
     assert np.array_equal(C, on_device(A, B, 1.0, 2.0, keep[:, :3000].copy())), "FP32 panels against device buffers"
@@ -411,7 +411,7 @@ def test_gemm_exact_small_integers(g9, torch_dev):
         for (M, N, K) in [(5, 7, 3), (257, 130, 200), (300, 520, 129)]:
             a = rng.integers(-3, 4, (M, K)).astype(dt)
             b = rng.integers(-3, 4, (K, N)).astype(dt)
-            ref = a.astype(np.int64) @ b.astype(np.int64)
+            ref = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.int64)
             if dt == np.float16 and np.abs(ref).max() > 2048:
                 continue
             for ta in (0, 1):
@@ -586,7 +586,7 @@ def test_gemm_split_k(tmp_path):
         "            for tb in (0, 1):\n"
         "                a = rng.integers(-2, 3, (M, K)).astype(dt); b = rng.integers(-2, 3, (K, N)).astype(dt)\n"
         "                A = np.ascontiguousarray(a.T).T if ta else a; B = np.ascontiguousarray(b.T).T if tb else b\n"
-        "                ref = a.astype(np.int64) @ b.astype(np.int64)\n"
+        "                ref = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.int64)\n"
         "                if np.abs(ref).max() <= 2048 or dt != np.float16:\n"
         "                    assert np.array_equal(g.gemm(A, B).astype(np.int64), ref), (dt, M, N, K, ta, tb)\n"
         "                u = rng.uniform(-1, 1, (M, K)).astype(dt); v = rng.uniform(-1, 1, (K, N)).astype(dt)\n"

@@ -9,103 +9,113 @@ restatement (reference: lib/kernels/level12.cl:189-214): both are FP64 sums of e
 import numpy as np
 import pytest
 
+from l12_util import assert_close, strided
+
 pytestmark = pytest.mark.gpu
 
 TOL = {np.float32: 1e-6, np.float16: 2e-3, np.float64: 1e-13}
+REDUCTION_TOL = 1e-6   # FP64 sums on the GPU, returned as float64
 rng = np.random.default_rng(11)
 
+# (inc_x, inc_y, lead of x): the reference's stride cases (reference: lib/test_level12.py:49); y always starts one
+# element into its array
+STRIDES = [(1, 1, 0), (1, 1, 1), (3, -2, 5), (-1, 1, 2)]
 
-def check(name, W, ref, scale, tol):
-    e = float(np.max(np.abs(np.asarray(W, np.float64) - ref) / np.maximum(scale, 6.2e-5 if tol > 1e-5 else 1e-30)))
-    assert e <= tol, f"{name}: {e:.1e} > {tol:.0e}"
+
+def _both(X, Y):
+    return np.concatenate([X, Y])
 
 
-def vector(n, dt, step=1, shift=0):
-    base = rng.uniform(-1, 1, n * abs(step) + shift + 3).astype(dt)
-    v = base[shift:shift + n * abs(step):abs(step)]
-    return v[::-1] if step < 0 else v
+# Level-1 calls on the pair (x, y), each from the same starting values X, Y (float64): what the call is, which
+# operand(s) it leaves its result in ("y", "xy": x then y, "ret": the return value), and the float64 result with its
+# error scale. Tolerance: the type's for vectors, 0 for pure data movement, REDUCTION_TOL for the FP64 sums.
+LEVEL1 = [
+    ("axpy", lambda g, x, y: g.axpy(0.75, x, y), "y", lambda X, Y: (0.75 * X + Y, 0.75 * abs(X) + abs(Y)), None),
+    ("scal", lambda g, x, y: g.scal(-1.5, y), "y", lambda X, Y: (-1.5 * Y, 1.5 * abs(Y)), None),
+    ("copy", lambda g, x, y: g.copy(x, y), "y", lambda X, Y: (X, 1.0), 0.0),
+    ("swap", lambda g, x, y: g.swap(x, y), "xy", lambda X, Y: (_both(Y, X), 1.0), 0.0),
+    ("rot", lambda g, x, y: g.rot(x, y, 0.6, 0.8), "xy",
+     lambda X, Y: (_both(0.6 * X + 0.8 * Y, 0.6 * Y - 0.8 * X), _both(abs(X) + abs(Y), abs(X) + abs(Y))), None),
+    ("dot", lambda g, x, y: g.dot(x, y), "ret", lambda X, Y: (X @ Y, abs(X) @ abs(Y)), REDUCTION_TOL),
+    ("asum", lambda g, x, y: g.asum(x), "ret", lambda X, Y: (abs(X).sum(), abs(X).sum()), REDUCTION_TOL),
+    ("nrm2", lambda g, x, y: g.nrm2(x), "ret", lambda X, Y: (np.sqrt(X @ X), np.sqrt(X @ X)), REDUCTION_TOL),
+]
 
 
 @pytest.mark.parametrize("dt", [np.float32, np.float16, np.float64])
 @pytest.mark.parametrize("n", [1, 5, 255, 256, 1000, 100003])
 def test_level1(g9, orc, dt, n):
-    tol = TOL[dt]
-    for kx, ky, px in ((1, 1, 0), (1, 1, 1), (3, -2, 5), (-1, 1, 2)):
-        label = f"{np.dtype(dt).name} n={n} strides {kx},{ky} shift {px}"
-        x, y = vector(n, dt, kx, px), vector(n, dt, ky, 1)
+    """Every level-1 call of the table on every stride case; iamax exact; the dot product also against the
+    oracle's FP64 restatement."""
+    for inc_x, inc_y, lead in STRIDES:
+        x, y = strided(rng, n, dt, inc_x, lead), strided(rng, n, dt, inc_y, 1)
         X, Y = x.astype(np.float64), y.astype(np.float64)
-        g9.axpy(0.75, x, y)
-        check("axpy " + label, y, 0.75 * X + Y, 0.75 * abs(X) + abs(Y), tol)
-        y[:] = Y
-        g9.scal(-1.5, y)
-        check("scal " + label, y, -1.5 * Y, 1.5 * abs(Y), tol)
-        y[:] = Y
-        g9.copy(x, y)
-        check("copy " + label, y, X, 1, 0)
-        y[:] = Y
-        g9.swap(x, y)
-        check("swap " + label, np.concatenate([x, y]), np.concatenate([Y, X]), 1, 0)
+        where = f"{np.dtype(dt).name} n={n} inc {inc_x},{inc_y} lead {lead}"
+        for name, call, out, expect, tol in LEVEL1:
+            x[:], y[:] = X, Y
+            ret = call(g9, x, y)
+            got = {"y": y, "xy": _both(x, y), "ret": ret}[out]
+            ref, scale = expect(X, Y)
+            assert_close(f"{name} {where}", got, ref, scale, TOL[dt] if tol is None else tol)
         x[:], y[:] = X, Y
-        g9.rot(x, y, 0.6, 0.8)
-        check("rot " + label, np.concatenate([x, y]), np.concatenate([0.6 * X + 0.8 * Y, 0.6 * Y - 0.8 * X]),
-              np.concatenate([abs(X) + abs(Y)] * 2), tol)
-        x[:], y[:] = X, Y
-        d = g9.dot(x, y)
-        check("dot " + label, d, X @ Y, abs(X) @ abs(Y), 1e-6)
-        assert abs(d - orc.dot(x, y)) <= 1e-12 * max(1.0, abs(X) @ abs(Y)), "dot vs oracle " + label
-        check("asum " + label, g9.asum(x), abs(X).sum(), abs(X).sum(), 1e-6)
-        check("nrm2 " + label, g9.nrm2(x), np.linalg.norm(X), np.linalg.norm(X), 1e-6)
-        assert g9.iamax(x) == int(np.argmax(abs(X))), "iamax " + label
+        assert abs(g9.dot(x, y) - orc.dot(x, y)) <= 1e-12 * max(1.0, abs(X) @ abs(Y)), "dot vs oracle " + where
+        assert g9.iamax(x) == int(np.argmax(abs(X))), "iamax " + where
 
 
 @pytest.mark.parametrize("dt", [np.float32, np.float16, np.float64])
 def test_level1_shared_pages(g9, dt):
+    """Operands that share an array: y right behind x, and dot(x, x)."""
     v = rng.uniform(-1, 1, 3000).astype(dt)
     V = v.astype(np.float64)
     g9.axpy(2.0, v[:1000], v[1000:2000])
-    check("axpy shared pages", v[1000:2000], 2 * V[:1000] + V[1000:2000], 3, TOL[dt])
+    assert_close("axpy shared pages", v[1000:2000], 2 * V[:1000] + V[1000:2000], 3, TOL[dt])
     v[:] = V
-    check("dot x·x", g9.dot(v, v), V @ V, V @ V, 1e-6)
+    assert_close("dot x·x", g9.dot(v, v), V @ V, V @ V, REDUCTION_TOL)
+
+
+# GEMV calls on one M×N matrix A (reference: lib/test_level12.py:72-88 for the cases): (label, op(A) as passed, the
+# trans flag, alpha, beta, x's (inc, lead), y's (inc, lead) or None for a new vector).
+GEMV = [
+    ("N", lambda A: A, False, 1.5, 0.0, (1, 0), None),
+    ("N beta", lambda A: A, False, 0.5, -2.0, (1, 0), (2, 0)),
+    ("T flag", lambda A: A, True, 0.5, 1.0, (-2, 3), (1, 0)),
+    ("A.T view", lambda A: A.T, False, 1.0, 0.0, (1, 0), None),
+]
 
 
 @pytest.mark.parametrize("dt", [np.float32, np.float16, np.float64])
 @pytest.mark.parametrize("M,N", [(1, 1), (7, 3), (64, 64), (257, 1031), (1000, 2), (3, 5000), (2048, 1536)])
 def test_gemv_ger(g9, orc, dt, M, N):
+    """The GEMV table against the oracle's float64 product and scale, GER with a reversed y, and the oracle's own
+    restatement of the reference GEMV under the same bound."""
     tol = TOL[dt]
     A = rng.uniform(-1, 1, (M, N)).astype(dt)
     Ad = A.astype(np.float64)
-    x, xt = vector(N, dt), vector(M, dt, -2, 3)
-    y0, yt0 = vector(M, dt, 2), vector(N, dt)
-    Y0, YT0 = y0.astype(np.float64), yt0.astype(np.float64)
-    y = g9.gemv(A, x, alpha=1.5)
-    check(f"gemv N {M}x{N}", y, 1.5 * Ad @ x.astype(np.float64), 1.5 * abs(Ad) @ abs(x.astype(np.float64)), tol)
-    g9.gemv(A, x, alpha=0.5, beta=-2.0, y=y0)
-    check(f"gemv N beta {M}x{N}", y0, 0.5 * Ad @ x.astype(np.float64) - 2 * Y0,
-          0.5 * abs(Ad) @ abs(x.astype(np.float64)) + 2 * abs(Y0), tol)
-    g9.gemv(A, xt, alpha=0.5, beta=1.0, y=yt0, trans=True)
-    Xt = xt.astype(np.float64)
-    check(f"gemv T {M}x{N}", yt0, 0.5 * Ad.T @ Xt + YT0, 0.5 * abs(Ad.T) @ abs(Xt) + abs(YT0), tol)
-    xv = vector(M, dt)
-    Xv = xv.astype(np.float64)
-    yv = g9.gemv(A.T, xv)
-    check(f"gemv A.T {M}x{N}", yv, Ad.T @ Xv, abs(Ad.T) @ abs(Xv), tol)
-    xg, yg = vector(M, dt, 1, 1), vector(N, dt, -3, 0)
+    for label, view, trans, alpha, beta, xs, ys in GEMV:
+        Av = view(A)
+        Op = view(Ad).T if trans else view(Ad)
+        x = strided(rng, Op.shape[1], dt, *xs)
+        y = strided(rng, Op.shape[0], dt, *ys) if ys else None
+        ref, scale = orc.mv(Op, x, alpha, beta, y)
+        got = g9.gemv(Av, x, alpha=alpha, beta=beta, y=y, trans=trans)
+        assert_close(f"gemv {label} {M}x{N}", got, ref, scale, tol)
+    xg, yg = strided(rng, M, dt, 1, 1), strided(rng, N, dt, -3, 0)
     Xg, Yg = xg.astype(np.float64), yg.astype(np.float64)
-    A2 = A.copy()
-    g9.ger(-0.5, xg, yg, A2)
-    check(f"ger {M}x{N}", A2, Ad - 0.5 * np.outer(Xg, Yg), abs(Ad) + 0.5 * np.outer(abs(Xg), abs(Yg)), tol)
-    # the oracle's restatement of the reference GEMV meets the same bound
+    Aw = A.copy()
+    g9.ger(-0.5, xg, yg, Aw)
+    assert_close(f"ger {M}x{N}", Aw, Ad - 0.5 * np.outer(Xg, Yg), abs(Ad) + 0.5 * np.outer(abs(Xg), abs(Yg)), tol)
     if M * N <= 1 << 20:
-        R = orc.gemv(A, x, alpha=1.5)
-        check(f"oracle gemv N {M}x{N}", R, 1.5 * Ad @ x.astype(np.float64), 1.5 * abs(Ad) @ abs(x.astype(np.float64)), tol)
+        x = strided(rng, N, dt)
+        ref, scale = orc.mv(Ad, x, 1.5)
+        assert_close(f"oracle gemv N {M}x{N}", orc.gemv(A, x, alpha=1.5), ref, scale, tol)
 
 
 @pytest.mark.parametrize("dt", [np.float32, np.float16, np.float64])
-def test_gemv_submatrix(g9, dt):
+def test_gemv_submatrix(g9, orc, dt):
+    """A submatrix view (row stride beyond its width) whose x is a row of the same array."""
     B = rng.uniform(-1, 1, (300, 400)).astype(dt)
-    Bd = B.astype(np.float64)
-    y = g9.gemv(B[10:200, 5:305], B[0, :300])
-    check("gemv submatrix", y, Bd[10:200, 5:305] @ Bd[0, :300], abs(Bd[10:200, 5:305]) @ abs(Bd[0, :300]), TOL[dt])
+    ref, scale = orc.mv(B[10:200, 5:305].astype(np.float64), B[0, :300])
+    assert_close("gemv submatrix", g9.gemv(B[10:200, 5:305], B[0, :300]), ref, scale, TOL[dt])
 
 
 def test_level2_config_device(g9, orc, torch_dev):
@@ -239,12 +249,12 @@ def test_level12_random(g9, torch_dev, case):
         Y, y = vec(N if tr else M, sy)
         g9.gemv(A, x, alpha=0.75, beta=-1.25, y=y, trans=tr)
         opA = Ad.T if tr else Ad
-        check(tag, host(y), 0.75 * opA @ X - 1.25 * Y, 0.75 * np.abs(opA) @ np.abs(X) + 1.25 * np.abs(Y), tol)
+        assert_close(tag, host(y), 0.75 * opA @ X - 1.25 * Y, 0.75 * np.abs(opA) @ np.abs(X) + 1.25 * np.abs(Y), tol)
     elif op == "axpy":
         X, x = vec(M, sx)
         Y, y = vec(M, sy)
         g9.axpy(-1.5, x, y)
-        check(tag, host(y), Y - 1.5 * X, np.abs(Y) + 1.5 * np.abs(X), tol)
+        assert_close(tag, host(y), Y - 1.5 * X, np.abs(Y) + 1.5 * np.abs(X), tol)
     elif op == "dot":
         X, x = vec(M, sx)
         Y, y = vec(M, sy)
@@ -255,6 +265,6 @@ def test_level12_random(g9, torch_dev, case):
         Y, y = vec(N, sy)
         g9.ger(0.5, x, y, A)
         W = host(Abig)
-        check(tag, W[:, off:off + N], Ad + 0.5 * np.outer(X, Y), np.abs(Ad) + 0.5 * np.outer(np.abs(X), np.abs(Y)),
+        assert_close(tag, W[:, off:off + N], Ad + 0.5 * np.outer(X, Y), np.abs(Ad) + 0.5 * np.outer(np.abs(X), np.abs(Y)),
               tol)
         assert np.array_equal(W[:, :off], big[:, :off]) and np.array_equal(W[:, off + N:], big[:, off + N:]), tag

@@ -13,23 +13,14 @@ solve on inverted diagonal blocks.
 import numpy as np
 import pytest
 
+from l12_util import assert_close, band_store, dominant_triangle, in_band, packed_store, strided
+
 pytestmark = pytest.mark.gpu
 
 TOL = {np.float32: 1e-6, np.float16: 2e-3, np.float64: 1e-13}
 SOLVE_TOL = {np.float32: 1e-5, np.float16: 3e-3, np.float64: 1e-12}
 DTYPES = [np.float32, np.float16, np.float64]
 rng = np.random.default_rng(12)
-
-
-def check(name, W, ref, scale, tol):
-    e = float(np.max(np.abs(np.asarray(W, np.float64) - ref) / np.maximum(scale, 6.2e-5 if tol > 1e-5 else 1e-30)))
-    assert e <= tol, f"{name}: {e:.1e} > {tol:.0e}"
-
-
-def vector(n, dt, step=1, shift=0):
-    base = rng.uniform(-1, 1, n * abs(step) + shift + 3).astype(dt)
-    v = base[shift:shift + n * abs(step):abs(step)]
-    return v[::-1] if step < 0 else v
 
 
 def f64(a):
@@ -44,43 +35,39 @@ def test_full_storage(g9, orc, dt, n):
     Ad = f64(A)
     for uplo in "LU":
         S = orc.symmetric(Ad, uplo)
-        x, y0 = vector(n, dt, -2, 1), vector(n, dt, 3)
+        x, y0 = strided(rng, n, dt, -2, 1), strided(rng, n, dt, 3)
         ref, scale = orc.mv(S, x, 0.5, 2.0, y0)
         g9.symv(A, x, uplo=uplo, alpha=0.5, beta=2.0, y=y0)
-        check(f"symv {uplo} n={n}", y0, ref, scale, tol)
+        assert_close(f"symv {uplo} n={n}", y0, ref, scale, tol)
         ref, scale = orc.mv(orc.symmetric(Ad.T, uplo), x)
-        check(f"symv A.T {uplo} n={n}", g9.symv(A.T, x, uplo=uplo), ref, scale, tol)
+        assert_close(f"symv A.T {uplo} n={n}", g9.symv(A.T, x, uplo=uplo), ref, scale, tol)
         for trans in (False, True):
             for diag in (False, True):
                 label = f"{uplo} trans={int(trans)} diag={int(diag)} n={n}"
                 Op = orc.triangle(Ad, uplo, diag)
                 Op = Op.T if trans else Op
-                xx = vector(n, dt, 2)
+                xx = strided(rng, n, dt, 2)
                 ref, scale = orc.mv(Op, xx)
                 g9.trmv(A, xx, uplo=uplo, trans=trans, diag=diag)
-                check("trmv " + label, xx, ref, scale, tol)
-                # solve: well conditioned (large diagonal; with a unit diagonal, small off-diagonal entries)
-                if diag:
-                    Ab = (Ad / n).astype(dt)
-                else:
-                    Ab = A.copy()
-                    np.fill_diagonal(Ab, np.where(np.diag(Ad) < 0, -1, 1) * n / 4 + np.diag(Ad))
+                assert_close("trmv " + label, xx, ref, scale, tol)
+                # solve: a diagonally dominant triangle (well conditioned in every type)
+                Ab = dominant_triangle(A, diag)
                 Ob = orc.triangle(f64(Ab), uplo, diag)
                 Ob = Ob.T if trans else Ob
-                b = vector(n, dt, -1)
+                b = strided(rng, n, dt, -1)
                 ref = orc.solve(Ob, f64(b))
                 g9.trsv(Ab, b, uplo=uplo, trans=trans, diag=diag)
-                check("trsv " + label, b, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
-        xs, ys = vector(n, dt, 1, 2), vector(n, dt, -3, 0)
+                assert_close("trsv " + label, b, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+        xs, ys = strided(rng, n, dt, 1, 2), strided(rng, n, dt, -3, 0)
         X, Y = f64(xs), f64(ys)
         mask = np.tril(np.ones((n, n), bool)) if uplo == "L" else np.triu(np.ones((n, n), bool))
         A1 = A.copy()
         g9.syr(-0.5, xs, A1, uplo=uplo)
-        check(f"syr {uplo} n={n}", A1, np.where(mask, Ad - 0.5 * np.outer(X, X), Ad),
+        assert_close(f"syr {uplo} n={n}", A1, np.where(mask, Ad - 0.5 * np.outer(X, X), Ad),
               np.abs(Ad) + 0.5 * np.outer(np.abs(X), np.abs(X)), tol)
         A2 = A.copy()
         g9.syr2(0.25, xs, ys, A2, uplo=uplo)
-        check(f"syr2 {uplo} n={n}", A2, np.where(mask, Ad + 0.25 * (np.outer(X, Y) + np.outer(Y, X)), Ad),
+        assert_close(f"syr2 {uplo} n={n}", A2, np.where(mask, Ad + 0.25 * (np.outer(X, Y) + np.outer(Y, X)), Ad),
               np.abs(Ad) + 0.25 * (np.outer(np.abs(X), np.abs(Y)) + np.outer(np.abs(Y), np.abs(X))), tol)
 
 
@@ -99,17 +86,17 @@ def test_full_storage_unreferenced_nan(g9, orc, dt, n):
         other = np.triu(np.ones((n, n), bool), 1) if uplo == "L" else np.tril(np.ones((n, n), bool), -1)
         An = A.copy()
         An[other] = np.nan
-        x = vector(n, dt, 1)
+        x = strided(rng, n, dt, 1)
         ref, scale = orc.mv(orc.symmetric(Ad, uplo), x)
-        check(f"symv NaN {uplo} n={n}", g9.symv(An, x, uplo=uplo), ref, scale, tol)
+        assert_close(f"symv NaN {uplo} n={n}", g9.symv(An, x, uplo=uplo), ref, scale, tol)
         for trans in (False, True):
-            xx = vector(n, dt, 2)
+            xx = strided(rng, n, dt, 2)
             Op = orc.triangle(Ad, uplo, False)
             ref, scale = orc.mv(Op.T if trans else Op, xx)
             g9.trmv(An, xx, uplo=uplo, trans=trans)
-            check(f"trmv NaN {uplo} trans={int(trans)} n={n}", xx, ref, scale, tol)
+            assert_close(f"trmv NaN {uplo} trans={int(trans)} n={n}", xx, ref, scale, tol)
         # rank updates read whole chunks too, but write only the referenced triangle: the NaN stay where they were
-        xs, ys = vector(n, dt, 1, 2), vector(n, dt, -3, 0)
+        xs, ys = strided(rng, n, dt, 1, 2), strided(rng, n, dt, -3, 0)
         X, Y = f64(xs), f64(ys)
         ref_mask = ~other
         for name, upd, ref, scale in (
@@ -119,26 +106,8 @@ def test_full_storage_unreferenced_nan(g9, orc, dt, n):
                  np.abs(Ad) + 0.25 * (np.outer(np.abs(X), np.abs(Y)) + np.outer(np.abs(Y), np.abs(X))))):
             A1 = An.copy()
             upd(A1)
-            check(f"{name} NaN {uplo} n={n}", A1[ref_mask], ref[ref_mask], scale[ref_mask], tol)
+            assert_close(f"{name} NaN {uplo} n={n}", A1[ref_mask], ref[ref_mask], scale[ref_mask], tol)
             assert np.isnan(A1[other]).all(), f"{name} {uplo} n={n}: the unreferenced triangle was written"
-
-
-def to_band(D, KL, KU):
-    M, N = D.shape
-    P = np.zeros((M, KL + KU + 1), D.dtype)
-    for i in range(M):
-        for j in range(max(0, i - KL), min(N, i + KU + 1)):
-            P[i, KL + j - i] = D[i, j]
-    return P
-
-
-def band_mask(M, N, KL, KU):
-    i, j = np.indices((M, N))
-    return (j - i >= -KL) & (j - i <= KU)
-
-
-def pack(D, uplo):
-    return D[np.triu_indices(D.shape[0])] if uplo == "U" else D[np.tril_indices(D.shape[0])]
 
 
 @pytest.mark.parametrize("dt", DTYPES)
@@ -156,22 +125,58 @@ def test_trsv_blocked_inverse(g9, orc, dt, n):
         other = np.triu(np.ones((n, n), bool), 1) if uplo == "L" else np.tril(np.ones((n, n), bool), -1)
         for trans in (False, True):
             for diag in (False, True):
-                if diag:
-                    Ab = (Ad / n).astype(dt)
-                else:
-                    Ab = A.copy()
-                    np.fill_diagonal(Ab, np.where(np.diag(Ad) < 0, -1, 1) * n / 4 + np.diag(Ad))
+                Ab = dominant_triangle(A, diag)
                 Ob = orc.triangle(f64(Ab), uplo, diag)
                 Ob = Ob.T if trans else Ob
                 Ag = Ab.copy()
                 Ag[other] = big
                 if diag:
                     np.fill_diagonal(Ag, big)
-                b = vector(n, dt, -1)
+                b = strided(rng, n, dt, -1)
                 ref = orc.solve(Ob, f64(b))
                 g9.trsv(Ag, b, uplo=uplo, trans=trans, diag=diag)
-                check(f"trsv {uplo} trans={int(trans)} diag={int(diag)} n={n}", b, ref, np.max(np.abs(ref)),
+                assert_close(f"trsv {uplo} trans={int(trans)} diag={int(diag)} n={n}", b, ref, np.max(np.abs(ref)),
                       SOLVE_TOL[dt])
+
+
+# Normwise backward error ||b − op(T)·x||∞ / (||op(T)||∞·||x||∞) a solve must stay within, per type: γ_n = n·u of
+# the work precision (FP32 for FP16 and FP32, FP64 for FP64), plus, for FP16, the rounding of x to FP16.
+def _backward_bound(dt, n):
+    if dt == np.float64:
+        return n * 2.0 ** -53
+    return n * 2.0 ** -24 + (2.0 ** -11 if dt == np.float16 else 0.0)
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("n", [1000, 1280, 1300])
+def test_trsv_not_dominant(g9, orc, dt, n):
+    """Triangles that are not diagonally dominant: off-diagonal entries uniform(−1, 1)/√n (row sums of |T| near
+    √n/2, far above the diagonal), unit or stored diagonal of magnitude 1..2. The solution stays bounded (its
+    variance grows by at most (1 + 1/n)^n ≈ e), but the solve is no longer well conditioned entry by entry, so the
+    check is the normwise backward error. n = 1000 takes the substitution, 1280 and 1300 the inverted 256-row blocks
+    (whose off-diagonal couplings are work-precision products): both meet the same bound."""
+    r = np.random.default_rng(n + 3 * DTYPES.index(dt))
+    A = (r.uniform(-1, 1, (n, n)) / np.sqrt(n))
+    d = r.uniform(-1, 1, n)
+    np.fill_diagonal(A, np.where(d < 0, -1.0, 1.0) * (1 + np.abs(d)))
+    A = A.astype(dt)
+    worst = 0.0
+    for uplo in "LU":
+        for trans in (False, True):
+            for diag in (False, True):
+                Op = orc.triangle(f64(A), uplo, diag)
+                Op = Op.T if trans else Op
+                b = r.uniform(-1, 1, n).astype(dt)
+                B = np.array(b, np.float64)   # a copy: the solve overwrites b
+                g9.trsv(A, b, uplo=uplo, trans=trans, diag=diag)
+                x = f64(b)
+                assert np.isfinite(x).all()
+                res = np.max(np.abs(B - Op @ x))
+                err = res / (np.max(np.abs(Op).sum(axis=1)) * np.max(np.abs(x)))
+                worst = max(worst, err)
+                assert err <= _backward_bound(dt, n), (
+                    f"trsv {uplo} trans={int(trans)} diag={int(diag)} n={n}: backward error {err:.2e}")
+    print(f"trsv not dominant {np.dtype(dt).name} n={n}: worst normwise backward error {worst:.2e}")
 
 
 @pytest.mark.parametrize("dt", DTYPES)
@@ -179,14 +184,14 @@ def test_trsv_blocked_inverse(g9, orc, dt, n):
                                        (100, 100, 99, 99), (1200, 1100, 2, 300)])
 def test_gbmv(g9, orc, dt, M, N, KL, KU):
     tol = TOL[dt]
-    D = f64(rng.uniform(-1, 1, (M, N)).astype(dt)) * band_mask(M, N, KL, KU)
-    P = to_band(D, KL, KU).astype(dt)
+    D = f64(rng.uniform(-1, 1, (M, N)).astype(dt)) * in_band(M, N, KL, KU)
+    P = band_store(D, KL, KU).astype(dt)
     assert np.array_equal(orc.band_dense(P, M, N, KL, KU), D)
     for tr in (False, True):
-        x, y0 = vector(M if tr else N, dt, -2), vector(N if tr else M, dt, 3)
+        x, y0 = strided(rng, M if tr else N, dt, -2), strided(rng, N if tr else M, dt, 3)
         ref, scale = orc.mv(D.T if tr else D, x, 0.5, 2.0, y0)
         g9.gbmv(P, x, M, N, KL, KU, alpha=0.5, beta=2.0, y=y0, trans=tr)
-        check(f"gbmv {M}x{N} KL={KL} KU={KU} tr={tr}", y0, ref, scale, tol)
+        assert_close(f"gbmv {M}x{N} KL={KL} KU={KU} tr={tr}", y0, ref, scale, tol)
 
 
 @pytest.mark.parametrize("dt", DTYPES)
@@ -197,58 +202,58 @@ def test_band_packed(g9, orc, dt, n, K):
     for uplo in "UL":
         g = uplo == "U"
         KL, KU = (0, K) if g else (K, 0)
-        T = Dp * band_mask(n, n, KL, KU)
-        P = to_band(T, KL, KU).astype(dt)
-        x = vector(n, dt, 2)
+        T = Dp * in_band(n, n, KL, KU)
+        P = band_store(T, KL, KU).astype(dt)
+        x = strided(rng, n, dt, 2)
         ref, scale = orc.mv(orc.symmetric(T, uplo), x, 1.5)
-        check(f"sbmv n={n} K={K} {uplo}", g9.sbmv(P, x, K, uplo=uplo, alpha=1.5), ref, scale, tol)
+        assert_close(f"sbmv n={n} K={K} {uplo}", g9.sbmv(P, x, K, uplo=uplo, alpha=1.5), ref, scale, tol)
         Tp = orc.triangle(Dp, uplo)
-        Ap = pack(Tp, uplo).astype(dt)
+        Ap = packed_store(Tp, uplo).astype(dt)
         assert np.array_equal(orc.packed_dense(Ap, n, uplo), Tp)
-        y0 = vector(n, dt, -1)
+        y0 = strided(rng, n, dt, -1)
         ref, scale = orc.mv(orc.symmetric(Tp, uplo), x, 0.5, -1.0, y0)
         g9.spmv(Ap, x, uplo=uplo, alpha=0.5, beta=-1.0, y=y0)
-        check(f"spmv n={n} {uplo}", y0, ref, scale, tol)
+        assert_close(f"spmv n={n} {uplo}", y0, ref, scale, tol)
         for tr in (False, True):
             for dg in (False, True):
                 label = f"n={n} K={K} {uplo} tr={tr} diag={dg}"
                 Ob, Op = orc.triangle(T, uplo, dg), orc.triangle(Tp, uplo, dg)
                 Ob, Op = (Ob.T, Op.T) if tr else (Ob, Op)
-                x = vector(n, dt, -3)
+                x = strided(rng, n, dt, -3)
                 ref, scale = orc.mv(Ob, x)
                 g9.tbmv(P, x, K, uplo=uplo, trans=tr, diag=dg)
-                check("tbmv " + label, x, ref, scale, tol)
-                x = vector(n, dt, 1)
+                assert_close("tbmv " + label, x, ref, scale, tol)
+                x = strided(rng, n, dt, 1)
                 ref, scale = orc.mv(Op, x)
                 g9.tpmv(Ap, x, uplo=uplo, trans=tr, diag=dg)
-                check("tpmv " + label, x, ref, scale, tol)
+                assert_close("tpmv " + label, x, ref, scale, tol)
                 # solves: well conditioned (small off-diagonal entries, diagonal 1..2)
                 Ts = T / max(K, 1) / 4
                 np.fill_diagonal(Ts, 1 + np.abs(np.diag(T)))
-                Ps = to_band(Ts, KL, KU).astype(dt)
+                Ps = band_store(Ts, KL, KU).astype(dt)
                 Os = orc.triangle(orc.band_dense(Ps, n, n, KL, KU), uplo, dg)
-                b = vector(n, dt, 2)
+                b = strided(rng, n, dt, 2)
                 ref = orc.solve(Os.T if tr else Os, f64(b))
                 g9.tbsv(Ps, b, K, uplo=uplo, trans=tr, diag=dg)
-                check("tbsv " + label, b, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+                assert_close("tbsv " + label, b, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
                 Tq = Tp / n
                 np.fill_diagonal(Tq, 1 + np.abs(np.diag(Tp)))
-                Aq = pack(Tq, uplo).astype(dt)
+                Aq = packed_store(Tq, uplo).astype(dt)
                 Oq = orc.triangle(orc.packed_dense(Aq, n, uplo), uplo, dg)
-                b = vector(n, dt, -1)
+                b = strided(rng, n, dt, -1)
                 ref = orc.solve(Oq.T if tr else Oq, f64(b))
                 g9.tpsv(Aq, b, uplo=uplo, trans=tr, diag=dg)
-                check("tpsv " + label, b, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
-        xs, ys = vector(n, dt, 1), vector(n, dt, -2)
+                assert_close("tpsv " + label, b, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+        xs, ys = strided(rng, n, dt, 1), strided(rng, n, dt, -2)
         X, Y = f64(xs), f64(ys)
         Ap1 = Ap.copy()
         g9.spr(-0.5, xs, Ap1, uplo=uplo)
-        check(f"spr n={n} {uplo}", Ap1, pack(orc.triangle(Tp - 0.5 * np.outer(X, X), uplo), uplo),
-              pack(np.abs(Tp) + 0.5 * np.outer(np.abs(X), np.abs(X)), uplo), tol)
+        assert_close(f"spr n={n} {uplo}", Ap1, packed_store(orc.triangle(Tp - 0.5 * np.outer(X, X), uplo), uplo),
+              packed_store(np.abs(Tp) + 0.5 * np.outer(np.abs(X), np.abs(X)), uplo), tol)
         Ap2 = Ap.copy()
         g9.spr2(0.25, xs, ys, Ap2, uplo=uplo)
-        check(f"spr2 n={n} {uplo}", Ap2, pack(orc.triangle(Tp + 0.25 * (np.outer(X, Y) + np.outer(Y, X)), uplo), uplo),
-              pack(np.abs(Tp) + 0.25 * (np.outer(np.abs(X), np.abs(Y)) + np.outer(np.abs(Y), np.abs(X))), uplo), tol)
+        assert_close(f"spr2 n={n} {uplo}", Ap2, packed_store(orc.triangle(Tp + 0.25 * (np.outer(X, Y) + np.outer(Y, X)), uplo), uplo),
+              packed_store(np.abs(Tp) + 0.25 * (np.outer(np.abs(X), np.abs(Y)) + np.outer(np.abs(Y), np.abs(X))), uplo), tol)
 
 
 @pytest.mark.parametrize("dt", [np.float32, np.float64])
@@ -267,16 +272,16 @@ def test_level2_device_n4096(g9, orc, torch_dev, dt, odd_ld):
     xd = torch.from_numpy(x).cuda()
     for uplo in "LU":
         ref, scale = orc.mv(orc.symmetric(Ad, uplo), x, 1.25)
-        check(f"symv {uplo}", g9.symv(Adev, xd, uplo=uplo, alpha=1.25).cpu().numpy(), ref, scale, TOL[dt])
+        assert_close(f"symv {uplo}", g9.symv(Adev, xd, uplo=uplo, alpha=1.25).cpu().numpy(), ref, scale, TOL[dt])
         for trans in (False, True):
             Op = orc.triangle(Ad, uplo)
             Op = Op.T if trans else Op
             v = xd.clone()
             g9.trmv(Adev, v, uplo=uplo, trans=trans)
             ref, scale = orc.mv(Op, x)
-            check(f"trmv {uplo} trans={trans}", v.cpu().numpy(), ref, scale, TOL[dt])
+            assert_close(f"trmv {uplo} trans={trans}", v.cpu().numpy(), ref, scale, TOL[dt])
         Ab = base.copy()
-        np.fill_diagonal(Ab[:, :n], np.where(np.diag(Ad) < 0, -1, 1) * n / 4 + np.diag(Ad))
+        Ab[:, :n] = dominant_triangle(A, False)
         Abd = torch.from_numpy(Ab).cuda()[:, :n]
         for trans in (False, True):
             Ob = orc.triangle(f64(Ab[:, :n]), uplo)
@@ -284,10 +289,10 @@ def test_level2_device_n4096(g9, orc, torch_dev, dt, odd_ld):
             v = xd.clone()
             g9.trsv(Abd, v, uplo=uplo, trans=trans)
             ref = orc.solve(Ob, f64(x))
-            check(f"trsv {uplo} trans={trans}", v.cpu().numpy(), ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
-        Ap = pack(orc.triangle(Ad, uplo), uplo).astype(dt)
+            assert_close(f"trsv {uplo} trans={trans}", v.cpu().numpy(), ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+        Ap = packed_store(orc.triangle(Ad, uplo), uplo).astype(dt)
         ref, scale = orc.mv(orc.symmetric(Ad, uplo), x)
-        check(f"spmv {uplo}", g9.spmv(torch.from_numpy(Ap).cuda(), xd, uplo=uplo).cpu().numpy(), ref, scale, TOL[dt])
+        assert_close(f"spmv {uplo}", g9.spmv(torch.from_numpy(Ap).cuda(), xd, uplo=uplo).cpu().numpy(), ref, scale, TOL[dt])
 
 
 @pytest.mark.parametrize("dt", [np.float32, np.float64])
@@ -298,23 +303,23 @@ def test_packed_products_unaligned_device(g9, orc, torch_dev, dt):
     torch = torch_dev
     n = 1500
     Dp = f64(rng.uniform(-1, 1, (n, n)).astype(dt))
-    x = vector(n, dt, 1)
+    x = strided(rng, n, dt, 1)
     xd = torch.from_numpy(np.ascontiguousarray(x)).cuda()
     for uplo in "LU":
         Tp = orc.triangle(Dp, uplo)
-        Ap = pack(Tp, uplo).astype(dt)
+        Ap = packed_store(Tp, uplo).astype(dt)
         buf = torch.zeros(Ap.size + 1, dtype=torch.float32 if dt == np.float32 else torch.float64, device="cuda")
         buf[1:] = torch.from_numpy(Ap).cuda()
         Apd = buf[1:]
         assert Apd.data_ptr() % 16 != 0
         ref, scale = orc.mv(orc.symmetric(Tp, uplo), x)
-        check(f"spmv unaligned {uplo}", g9.spmv(Apd, xd, uplo=uplo).cpu().numpy(), ref, scale, TOL[dt])
+        assert_close(f"spmv unaligned {uplo}", g9.spmv(Apd, xd, uplo=uplo).cpu().numpy(), ref, scale, TOL[dt])
         for tr in (False, True):
             Op = Tp.T if tr else Tp
             v = xd.clone()
             g9.tpmv(Apd, v, uplo=uplo, trans=tr)
             ref, scale = orc.mv(Op, x)
-            check(f"tpmv unaligned {uplo} trans={tr}", v.cpu().numpy(), ref, scale, TOL[dt])
+            assert_close(f"tpmv unaligned {uplo} trans={tr}", v.cpu().numpy(), ref, scale, TOL[dt])
 
 
 def test_level2_errors(g9):
@@ -381,42 +386,42 @@ def test_level2_random(g9, orc, case):
         T = orc.triangle(D, uplo, dg)
         if op == "symv":
             ref, scale = orc.mv(orc.symmetric(D, uplo), x, 1.5)
-            check(tag, g9.symv(A, x, uplo=uplo, alpha=1.5), ref, scale, tol)
+            assert_close(tag, g9.symv(A, x, uplo=uplo, alpha=1.5), ref, scale, tol)
         elif op == "trmv":
             ref, scale = orc.mv(T.T if tr else T, x)
             g9.trmv(A, x, uplo=uplo, trans=tr, diag=dg)
-            check(tag, x, ref, scale, tol)
+            assert_close(tag, x, ref, scale, tol)
         else:
             ref = orc.solve(T.T if tr else T, X)
             g9.trsv(A, x, uplo=uplo, trans=tr, diag=dg)
-            check(tag, x, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+            assert_close(tag, x, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
     elif op in ("sbmv", "tbmv", "tbsv"):
-        Tb = D * band_mask(n, n, KL, KU)
-        P = to_band(Tb, KL, KU).astype(dt)
+        Tb = D * in_band(n, n, KL, KU)
+        P = band_store(Tb, KL, KU).astype(dt)
         T = orc.triangle(orc.band_dense(P, n, n, KL, KU), uplo, dg)
         if op == "sbmv":
             ref, scale = orc.mv(orc.symmetric(Tb, uplo), x, -0.5)
-            check(tag, g9.sbmv(P, x, K, uplo=uplo, alpha=-0.5), ref, scale, tol)
+            assert_close(tag, g9.sbmv(P, x, K, uplo=uplo, alpha=-0.5), ref, scale, tol)
         elif op == "tbmv":
             ref, scale = orc.mv(T.T if tr else T, x)
             g9.tbmv(P, x, K, uplo=uplo, trans=tr, diag=dg)
-            check(tag, x, ref, scale, tol)
+            assert_close(tag, x, ref, scale, tol)
         else:
             ref = orc.solve(T.T if tr else T, X)
             g9.tbsv(P, x, K, uplo=uplo, trans=tr, diag=dg)
-            check(tag, x, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+            assert_close(tag, x, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
     else:
         Tp = orc.triangle(D, uplo)
-        Ap = pack(Tp, uplo).astype(dt)
+        Ap = packed_store(Tp, uplo).astype(dt)
         T = orc.triangle(orc.packed_dense(Ap, n, uplo), uplo, dg)
         if op == "spmv":
             ref, scale = orc.mv(orc.symmetric(Tp, uplo), x, 0.25)
-            check(tag, g9.spmv(Ap, x, uplo=uplo, alpha=0.25), ref, scale, tol)
+            assert_close(tag, g9.spmv(Ap, x, uplo=uplo, alpha=0.25), ref, scale, tol)
         elif op == "tpmv":
             ref, scale = orc.mv(T.T if tr else T, x)
             g9.tpmv(Ap, x, uplo=uplo, trans=tr, diag=dg)
-            check(tag, x, ref, scale, tol)
+            assert_close(tag, x, ref, scale, tol)
         else:
             ref = orc.solve(T.T if tr else T, X)
             g9.tpsv(Ap, x, uplo=uplo, trans=tr, diag=dg)
-            check(tag, x, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+            assert_close(tag, x, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])

@@ -102,7 +102,7 @@ def test_skinny_matrix_core_kernel(g9, torch_dev, M, N, K):
     rng = np.random.default_rng(31)
     a = rng.integers(-3, 4, (M, K)).astype(np.float16)
     w = rng.integers(-3, 4, (N, K)).astype(np.float16)
-    ref = a.astype(np.int64) @ w.astype(np.int64).T
+    ref = (a.astype(np.float64) @ w.astype(np.float64).T).astype(np.int64)
     assert np.abs(ref).max() <= 2048
     assert np.array_equal(g9.hgemm(a, w.T).astype(np.int64), ref), "host"
     Wd = g9.hgemm(_dev(torch_dev, a), _dev(torch_dev, w).t())
@@ -121,6 +121,74 @@ def test_skinny_matrix_core_kernel(g9, torch_dev, M, N, K):
     mask = np.ones(big.shape, bool)
     mask[2:M + 2, 1:N + 1] = False
     assert np.array_equal(big[mask], D0[mask]), "write outside the C slice"
+
+
+# (M, N, K): weights stored K×N (N-contiguous), shapes for the FP16 matrix-core form (K a multiple of 256, N a
+# multiple of 8: whole 16-column strips and a last strip shifted back when N % 16 = 8) and for the vector form
+# (K or N off those multiples, N below 16)
+KN_SHAPES = [(1, 4096, 512), (2, 264, 256), (3, 77 * 8, 768), (4, 2056, 1024), (7, 16, 256), (8, 520, 2048),
+             (12, 1000, 512), (16, 4096, 256), (16, 24, 4096), (1, 1000, 777), (5, 333, 300), (16, 9, 513),
+             (2, 4100, 1000)]
+
+
+@pytest.mark.parametrize("M,N,K", KN_SHAPES)
+def test_skinny_weights_n_contiguous(g9, torch_dev, M, N, K):
+    """C = a·W with W stored K×N (row-major x·W), the layout the reference sends to skinny_n4 / skinny_n2
+    (reference: lib/src/gemm.c:246-261). Small integers make every product and sum exact, so FP16 (matrix-core form
+    where the shape allows it, the vector form elsewhere) and FP32 (vector form) must be bit-exact; also the role swap
+    (C = Wᵀ·aᵀ with op(A) = Wᵀ: the weights become the transposed A), a transposed a (gathered first), and alpha/beta
+    into a slice of a larger C with nothing outside it written."""
+    rng = np.random.default_rng(M * 131 + N + K)
+    for dt in (np.float16, np.float32):
+        fn = g9.hgemm if dt == np.float16 else g9.sgemm
+        a = rng.integers(-3, 4, (M, K)).astype(dt)
+        w = rng.integers(-3, 4, (K, N)).astype(dt)
+        ref = (a.astype(np.float64) @ w.astype(np.float64)).astype(np.int64)
+        assert np.abs(ref).max() <= 2048 or dt == np.float32
+        tag = f"{np.dtype(dt).name} M={M} N={N} K={K}"
+        assert np.array_equal(fn(a, w).astype(np.int64), ref), tag + " host"
+        got = fn(_dev(torch_dev, a), _dev(torch_dev, w)).cpu().numpy()
+        assert np.array_equal(got.astype(np.int64), ref), tag + " device"
+        assert np.array_equal(fn(w.T, a.T).astype(np.int64), ref.T), tag + " small N (weights as transposed A)"
+        at = np.ascontiguousarray(a.T)   # a stored K×M: op(A) = atᵀ has a k stride
+        assert np.array_equal(fn(at.T, w).astype(np.int64), ref), tag + " transposed a"
+        big = rng.uniform(-1, 1, (M + 2, N + 3)).astype(dt)
+        D0 = big.copy()
+        C = big[1:M + 1, 3:N + 3]
+        C0 = C.astype(np.float64)
+        fn(a, w, alpha=0.5, beta=-2.0, C=C)
+        r64 = 0.5 * ref - 2.0 * C0
+        scale = 0.5 * (np.abs(a.astype(np.float64)) @ np.abs(w.astype(np.float64))) + 2.0 * np.abs(C0)
+        assert float(np.max(np.abs(C.astype(np.float64) - r64) / scale)) <= (2e-3 if dt == np.float16 else 1e-6), tag
+        mask = np.ones(big.shape, bool)
+        mask[1:M + 1, 3:N + 3] = False
+        assert np.array_equal(big[mask], D0[mask]), tag + ": write outside the C slice"
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
+def test_skinny_decode_4096_weights_k_by_n(g9, orc, torch_dev, M):
+    """The decode shape with W stored K×N (4096², ~N(0, 0.02)) on device memory, as the benchmark runs it: against
+    float64 with the skinny bound and the reference metric, and equal to the same product with the weights stored
+    N×K to within FP16 rounding and the FP32 summation bound (both sum the same exact products, in different
+    orders)."""
+    torch = torch_dev
+    K = N = 4096
+    A = orc.normal((M, K), np.float16, orc.SEED_A)
+    Ad = _dev(torch, A)
+    for i in range(2):
+        Wt = orc.normal((N, K), np.float16, orc.SEED_W0 + i, 0.02)   # N×K as in the K-contiguous case
+        W = np.ascontiguousarray(Wt.T)                                 # stored K×N
+        C = g9.hgemm(Ad, _dev(torch, W)).cpu().numpy()
+        ref = A.astype(np.float64) @ W.astype(np.float64)
+        assert _err(C, ref) <= TOL[np.float16], f"M={M} copy {i}"
+        scale = np.abs(A.astype(np.float64)) @ np.abs(W.astype(np.float64))
+        assert float(np.max(np.abs(C - ref) / scale)) <= 1e-3, f"M={M} copy {i}: reference metric"
+        Ck = g9.hgemm(Ad, _dev(torch, Wt).t()).cpu().numpy()
+        # each result is an FP32 sum of the same exact products, rounded once to FP16: they differ by at most one FP16
+        # ulp plus the two summation orders' error bounds, 2·K·2^-24·Σ|a·w|
+        c64, k64 = C.astype(np.float64), Ck.astype(np.float64)
+        bound = 2.0 ** -10 * np.maximum(np.abs(c64), np.abs(k64)) + 2 * K * 2.0 ** -24 * scale + 2.0 ** -24
+        assert (np.abs(c64 - k64) <= bound).all(), f"M={M}: layouts differ"
 
 
 def test_skinny_forced_threshold(g9):

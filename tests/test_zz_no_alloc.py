@@ -3,9 +3,13 @@
 Same kernels and dispatch as gen9blas_gemm, so on the same device operands the results must be identical, bit for
 bit: products that take split-K (whose slices then live in the entry point's static work space), the two-k-group
 tiles and the whole-tile FP16 kernel, in every type, two calls in a row with the second smaller (the work space
-keeps the last call's contents; a split-K slice writes every element it is later read at). Both are also held to the
-GEMM bounds against float64. Host operands and a work space beyond the fixed maximum give INVALID_ARG before any
-launch (the latter needs a split forced with GEN9BLAS_SPLITK, read once per process: a child process)."""
+keeps the last call's contents; a split-K slice writes every element it is later read at). The largest default
+splits are included: DGEMM 2048³ (128 tiles of 256×128 split two ways: the whole 64 MiB), FP64 640×640×1024 and FP16
+1280×1280×1000 on the general kernel. Both are also held to the GEMM bounds against float64. Host operands (checked
+before any dispatch, so the staging paths never run) and a work space beyond the fixed maximum give INVALID_ARG
+before any launch (the latter needs a split forced with GEN9BLAS_SPLITK, read once per process: a child process).
+A fresh child process checks the property itself: the free device memory does not move across no-alloc calls,
+while one gen9blas_gemm of the same product grows the library's buffers."""
 import ctypes
 import os
 import subprocess
@@ -53,15 +57,17 @@ def _err(W, opA, opB, alpha, beta, c0):
 CASES = [((200, 136, 1000, 0, 0), (100, 72, 500, 1, 1)),
          ((130, 260, 4096, 1, 0), (64, 64, 777, 0, 1)),
          ((1024, 1024, 512, 0, 0), (512, 384, 256, 0, 1))]
+# the largest default work spaces: 64 MiB (FP64 2048³), then 12.5 MiB (FP64 640×640×1024, FP16 1280×1280×1000)
+LARGE = {"D": ((2048, 2048, 2048, 0, 0), (640, 640, 1024, 1, 0)),
+         "H": ((1280, 1280, 1000, 0, 0), (640, 640, 1024, 0, 1)),
+         "HS": ((1280, 1280, 1000, 1, 1), (1000, 600, 1000, 0, 0))}
 
 
-@pytest.mark.parametrize("kind", ["S", "D", "H", "HS"])
-@pytest.mark.parametrize("pair", range(len(CASES)))
-def test_noalloc_matches_gemm(g9, torch_dev, kind, pair):
+def _compare(g9, torch_dev, kind, shapes, seed):
     L = _sig(g9._lib)
-    rng = np.random.default_rng(40 + pair)
+    rng = np.random.default_rng(seed)
     dt = DT[kind]
-    for (M, N, K, tA, tB) in CASES[pair]:
+    for (M, N, K, tA, tB) in shapes:
         a = rng.uniform(-1, 1, (K, M) if tA else (M, K)).astype(dt)
         b = rng.uniform(-1, 1, (N, K) if tB else (K, N)).astype(dt)
         c0 = rng.uniform(-1, 1, (M, N)).astype(dt)
@@ -71,6 +77,17 @@ def test_noalloc_matches_gemm(g9, torch_dev, kind, pair):
         assert np.array_equal(W0, W1), tag + ": no-alloc result differs from gen9blas_gemm"
         opA, opB = (a.T if tA else a), (b.T if tB else b)
         assert _err(W1, opA, opB, 1.5, 0.5, c0) <= BOUND[kind], tag
+
+
+@pytest.mark.parametrize("kind", ["S", "D", "H", "HS"])
+@pytest.mark.parametrize("pair", range(len(CASES)))
+def test_noalloc_matches_gemm(g9, torch_dev, kind, pair):
+    _compare(g9, torch_dev, kind, CASES[pair], 40 + pair)
+
+
+@pytest.mark.parametrize("kind", sorted(LARGE))
+def test_noalloc_largest_work_space(g9, torch_dev, kind):
+    _compare(g9, torch_dev, kind, LARGE[kind], 50)
 
 
 def test_noalloc_rejects_host_operands(g9):
@@ -104,7 +121,7 @@ print(rc, untouched, rc2, bool((c == K).all()), msg)
 
 
 def test_noalloc_rejects_work_space_beyond_maximum(g9, tmp_path):
-    """GEN9BLAS_SPLITK=64 on 1024² × 4096 FP32 needs 64 slices × 4 MiB of work space, beyond the 8 MiB maximum: the
+    """GEN9BLAS_SPLITK=64 on 1024² × 4096 FP32 needs 64 slices × 4 MiB of work space, beyond the 64 MiB maximum: the
     no-alloc call fails with INVALID_ARG and writes nothing; gen9blas_gemm (growing buffers) computes it."""
     script = tmp_path / "child.py"
     script.write_text(CHILD)
@@ -116,3 +133,69 @@ def test_noalloc_rejects_work_space_beyond_maximum(g9, tmp_path):
     assert int(rc) == INVALID and untouched == "True", r.stdout
     assert "fixed maximum" in r.stdout
     assert int(rc2) == 0 and right == "True", r.stdout
+
+
+FRESH = r"""
+import ctypes, sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1])
+import gen9blas as g
+L = g._lib
+i, d, p = ctypes.c_int, ctypes.c_double, ctypes.c_void_p
+for name in ("gen9blas_gemm", "gen9blas_gemm_noalloc"):
+    getattr(L, name).argtypes = [i, i, i, i, i, i, d, p, i, p, i, d, p, i]
+assert L.gen9blas_init() == 0
+dt = {0: torch.float16, 2: torch.float16, 3: torch.float64, 1: torch.float32}
+cases = [(3, 2048, 2048, 2048), (0, 1280, 1280, 1000), (2, 1280, 1280, 1000), (3, 640, 640, 1024), (1, 200, 136, 1000)]
+bufs = [[torch.randn(s, dtype=dt[t], device="cuda") for s in ((M, K), (K, N), (M, N))] for (t, M, N, K) in cases]
+small = [torch.ones((64, 64), dtype=torch.float32, device="cuda") for _ in range(3)]
+def call(name, t, M, N, K, a, b, c):
+    rc = getattr(L, name)(t, 0, 0, M, N, K, 1.0, a.data_ptr(), K, b.data_ptr(), N, 0.0, c.data_ptr(), N)
+    assert rc == 0, (name, t, M, N, K, L.gen9blas_error())
+call("gen9blas_gemm_noalloc", 1, 64, 64, 64, *small)   # warm-up: a product without split-K
+torch.cuda.synchronize()
+free0 = torch.cuda.mem_get_info()[0]
+for k in range(2):
+    for (t, M, N, K), (a, b, c) in zip(cases, bufs):
+        call("gen9blas_gemm_noalloc", t, M, N, K, a, b, c)
+torch.cuda.synchronize()
+free1 = torch.cuda.mem_get_info()[0]
+t, M, N, K = cases[0]
+call("gen9blas_gemm", t, M, N, K, *bufs[0])
+torch.cuda.synchronize()
+free2 = torch.cuda.mem_get_info()[0]
+# a pageable C of 32 MiB (the size that takes the row-panel staging in gen9blas_gemm) next to device A and B
+a = torch.randn((4096, 4096), dtype=torch.float16, device="cuda")
+ch = np.zeros((4096, 4096), np.float16)
+rc = L.gen9blas_gemm_noalloc(0, 0, 0, 4096, 4096, 4096, 1.0, a.data_ptr(), 4096, a.data_ptr(), 4096, 0.0,
+                             ch.ctypes.data, 4096)
+msg = L.gen9blas_error().decode()
+untouched = bool((ch == 0).all())
+# afterwards gen9blas_gemm on host buffers (row panels through the pinned ring) still computes correctly
+rng = np.random.default_rng(5)
+ah = rng.integers(-2, 3, (4096, 256)).astype(np.float16)
+bh = rng.integers(-2, 3, (256, 2048)).astype(np.float16)
+ch2 = np.zeros((4096, 2048), np.float16)
+rc2 = L.gen9blas_gemm(0, 0, 0, 4096, 2048, 256, 1.0, ah.ctypes.data, 256, bh.ctypes.data, 2048, 0.0,
+                      ch2.ctypes.data, 2048)
+exact = bool(np.array_equal(ch2.astype(np.float64), ah.astype(np.float64) @ bh.astype(np.float64)))
+print(free0 - free1, free1 - free2, rc, untouched, rc2, exact, "|", msg)
+"""
+
+
+def test_noalloc_allocates_nothing(g9, tmp_path):
+    """In a fresh process: after one warm-up call, no-alloc calls that use the whole 64 MiB work space (and smaller
+    ones) leave the free device memory where it was, while one gen9blas_gemm of the largest product takes at least
+    64 MiB for its split-K buffer. A pageable 32 MiB C next to device A and B gives INVALID_ARG, writes nothing, and
+    leaves the host staging paths working for the next gen9blas_gemm (exact on small integers)."""
+    script = tmp_path / "fresh.py"
+    script.write_text(FRESH)
+    pkg = os.path.join(os.path.dirname(os.path.dirname(os.path.realpath(__file__))), "gen9-gpu-blas_amd")
+    env = {k: v for k, v in os.environ.items() if not k.startswith("GEN9BLAS_")}
+    r = subprocess.run([sys.executable, str(script), pkg], env=env, capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0, r.stderr[-2000:]
+    fields = r.stdout.split("|")[0].split()
+    d_noalloc, d_gemm, rc, untouched, rc2, exact = fields[:6]
+    assert int(d_noalloc) < (2 << 20), f"free device memory fell by {d_noalloc} bytes across no-alloc calls"
+    assert int(d_gemm) >= (64 << 20), f"gen9blas_gemm's split-K buffer not seen ({d_gemm} bytes)"
+    assert int(rc) == INVALID and untouched == "True" and "device operands only" in r.stdout, r.stdout
+    assert int(rc2) == 0 and exact == "True", r.stdout
