@@ -86,6 +86,7 @@ def main():
     cal.g9cal_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     cal.g9cal_mfma.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
                                ctypes.c_int, ctypes.c_void_p]
+    cal.g9cal_touch.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     cal.g9cal_round_trip_us.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     cal.g9cal_round_trip_us.restype = ctypes.c_double
     lib_stream = ctypes.c_void_p(g9.hip_stream())
@@ -316,6 +317,40 @@ def main():
             floor["note"] = "a pure read of one 4096x4096 fp16 copy per call, 32 copies rotated (1 GiB)"
             res["skinny_read_floor_32MiB"] = floor
             log("skinny_read_floor", floor)
+            # Decomposition of the one-pass floor into a fixed part per call and a streaming part: the calibration
+            # read (1024 blocks) over S MiB per call, each call a new region of the same 1 GiB (beyond the 256 MB
+            # MALL), S = 4 .. 128; t(S) = t0 + S / bw fitted over S = 16 .. 128. Beside it: the same 32 MiB region read
+            # by every call (served from the MALL), and the one-word kernel back to back (the launch-to-launch floor
+            # of dependent kernels on one stream).
+            flat = Wd.view(-1)
+            total = flat.numel() * 2
+            dec = {}
+            for mib in (4, 8, 16, 32, 64, 128):
+                size = mib << 20
+                nreg = total // size
+                state = {"j": 0}
+
+                def fn():
+                    j = state["j"]
+                    state["j"] = (j + 1) % nreg
+                    check(cal.g9cal_stream_read(flat.data_ptr() + j * size, size, sink.data_ptr(), 1024, lib_stream))
+                ms = timed(fn, k=kshort, w=max(warm, 32))
+                dec[f"{mib}MiB"] = {"us_per_call": round(ms * 1e3, 2), "GBs": round(size / (ms * 1e-3) / 1e9, 1)}
+
+            def fn():
+                check(cal.g9cal_stream_read(flat.data_ptr(), 32 << 20, sink.data_ptr(), 1024, lib_stream))
+            ms = timed(fn, k=kshort, w=max(warm, 32))
+            dec["32MiB_same_region_MALL"] = {"us_per_call": round(ms * 1e3, 2),
+                                             "GBs": round((32 << 20) / (ms * 1e-3) / 1e9, 1)}
+            ms = timed(lambda: check(cal.g9cal_touch(sink.data_ptr(), lib_stream)), k=kshort, w=max(warm, 32))
+            dec["empty_kernel_us"] = round(ms * 1e3, 2)
+            xs = np.array([16.0, 32.0, 64.0, 128.0]) * (1 << 20)
+            ys = np.array([dec[f"{int(x) >> 20}MiB"]["us_per_call"] for x in xs])
+            slope, t0 = np.polyfit(xs, ys, 1)
+            dec["fit_16_128MiB"] = {"t0_us": round(float(t0), 2), "streaming_GBs": round(1e-3 / float(slope), 1),
+                                    "model_32MiB_us": round(float(t0 + slope * (32 << 20)), 2)}
+            res["skinny_floor_decomposition"] = dec
+            log("skinny_floor_decomposition", dec)
             del sink
         del Wd
 

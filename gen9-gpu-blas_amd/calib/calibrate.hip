@@ -3,6 +3,7 @@
 // - g9cal_stream_read: a pure streaming read (the HBM read rate, and the floor of a one-pass 32 MiB call such as the
 //   skinny product's weight stream). Each block reads 32 KiB contiguous per step with all 8 of a lane's 16-byte
 //   nontemporal loads issued before they are consumed; one float per block is written so the loads stay.
+// - g9cal_touch: the one-word kernel, back to back: the launch-to-launch floor of dependent kernels on one stream.
 // - g9cal_mfma: sustained matrix-core loops on random FP16 operands, v_mfma_f32_32x32x16_f16 or
 //   v_mfma_f32_16x16x32_f16 at the same flops per iteration. Operands rotate through 8 register fragments per lane, so
 //   their bits toggle as in a GEMM; FP16 GEMMs on random data run at the board's power limit, and this loop is the
@@ -124,6 +125,14 @@ __attribute__((visibility("default"))) double g9cal_round_trip_us(float *out, in
     }
     std::sort(t.begin(), t.end());
     return t[(size_t)reps / 2];
+}
+
+// The one-word kernel launched on `stream` without waiting: back to back, the launch-to-launch floor of dependent
+// kernels on one stream. 0 or a HIP error.
+__attribute__((visibility("default"))) int g9cal_touch(float *out, void *stream) {
+    if (!out) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(touch, dim3(1), dim3(64), 0, (hipStream_t)stream, out);
+    return (int)hipGetLastError();
 }
 
 }  // extern "C"
