@@ -132,22 +132,30 @@ __global__ void __launch_bounds__(SPW * 64) skinny_pb_kernel(int M, int N, int K
     }
 }
 
-// The same product with the weight and activation tiles streamed through LDS (K % 128 == 0, 16-byte aligned
-// activation rows): a workgroup of SKS waves owns 16 weight rows; its waves take groups of 128 k round robin, and
-// each wave streams its groups through a private NSP-stage LDS ring with global_load_lds_dwordx4: per group 4 copies
-// of 1 KiB bring 16 weight rows × 256 bytes (4 rows per copy, contiguous in memory) and MT/2 copies bring MT
-// activation rows × 512 bytes (2 rows per copy). Chunk c (16 bytes) of row r sits at position c ^ (r % 16) of the
-// row, so the 16 lanes that read one chunk of 16 rows hit distinct banks. Per 32 k, lane (i = l%16, q = l/16) reads
-// 8 FP16 weights of row n0 + i and 8 FP32 activations of row i at k = 8·q .. 8·q+7, and 8 v_mfma_f32_16x16x4_f32
-// add them (MFMA e takes k = 8·q + e from lane group q) into chain e % 4 of four independent chains. A wave reads only
-// what it copied itself, so no barrier is needed until the waves' 16×16 sums are added in LDS in wave order.
-template <int MT, int SKS, int NSP>
+// The same product with the weight and activation tiles streamed through LDS (K % GK == 0, 16-byte aligned
+// activation rows): a workgroup of SKS waves owns 16 weight rows; its waves take groups of GK = 64 or 128 k round
+// robin, and each wave streams its groups through a private NSP-stage LDS ring with global_load_lds_dwordx4: per group
+// 16·GK·2 / 1024 copies of 1 KiB bring 16 weight rows × 2·GK bytes (1024 / (2·GK) rows per copy, contiguous in
+// memory) and ⌈MT / rows per copy⌉ copies bring MT activation rows × 4·GK bytes. Chunk c (16 bytes) of weight row r
+// sits at position c ^ wsw(r), wsw(r) = (r / rows per 256 bytes) mod chunks per row, and of activation row r at
+// c ^ (r % 16), so the 16 lanes that read one chunk of 16 rows hit distinct banks. Per 32 k, lane (i = l%16, q = l/16)
+// reads 8 FP16 weights of row n0 + i and 8 FP32 activations of row i at k = 8·q .. 8·q+7, and 8
+// v_mfma_f32_16x16x4_f32 add them (MFMA e takes k = 8·q + e from lane group q) into chain e % 4 of four independent
+// chains. A wave reads only what it copied itself, so no barrier is needed until the waves' 16×16 sums are added in
+// LDS in wave order. The 64-k groups halve a stage, so 8 waves (two per SIMD, hiding each other's ring and LDS waits)
+// with three stages fit beside 16 activation rows.
+template <int MT, int SKS, int NSP, int GK = 128>
 __global__ void __launch_bounds__(SKS * 64) skinny_pb_lds_kernel(int M, int N, int K, const float *__restrict__ A,
                                                                  long long lda, const _Float16 *__restrict__ W,
                                                                  long long ldw, float *__restrict__ C, long long ldc,
                                                                  int *flag) {
-    constexpr int GK = 128, WROW = GK * 2, AROW = GK * 4;   // bytes of a weight / activation row per group
-    constexpr int NWC = 16 * WROW / 1024, NAC = (MT + 1) / 2;   // copies per group
+    static_assert(GK == 64 || GK == 128, "groups of 64 or 128 k");
+    constexpr int WROW = GK * 2, AROW = GK * 4;               // bytes of a weight / activation row per group
+    constexpr int CPR = WROW / 16, RPC = 1024 / WROW, RPB = 256 / WROW;   // weight chunks per row, rows per copy,
+                                                                          // rows per 256 bytes
+    constexpr int CPRA = AROW / 16, RPCA = 1024 / AROW;
+    constexpr int NWC = 16 / RPC, NAC = (MT + RPCA - 1) / RPCA;   // copies per group
+    constexpr int NSUB = GK / 32;
     constexpr int WB = 16 * WROW, SB = WB + NAC * 1024, LPG = NWC + NAC;
     static_assert((NSP - 1) * LPG < 64, "copies in flight must fit vmcnt");
     __shared__ __attribute__((aligned(1024))) unsigned char smem[SKS * NSP * SB];
@@ -157,18 +165,19 @@ __global__ void __launch_bounds__(SKS * 64) skinny_pb_lds_kernel(int M, int N, i
     const unsigned lbase = (unsigned)(uintptr_t)smem + wv * NSP * SB;
     const G9_LDS unsigned char *lds = (const G9_LDS unsigned char *)smem + wv * NSP * SB;
     const int G = K / GK, ng = G > wv ? (G - wv + SKS - 1) / SKS : 0;
-    // weight copy c: rows 4c + L/16, position L % 16; activation copy c: rows 2c + L/32, position L % 32. Rows past N
-    // (M) load the last valid row: their results are not stored (activations: zeroed before use).
+    auto wsw = [](int r) { return (r / RPB) % CPR; };
+    // weight copy c: row RPC·c + L / CPR, position L % CPR; activation copy c: row RPCA·c + L / CPRA, position
+    // L % CPRA. Rows past N (M) load the last valid row: their results are not stored (activations: zeroed before use).
     unsigned woff[NWC], aoff[NAC];
 #pragma unroll
     for (int c = 0; c < NWC; c++) {
-        const int r = 4 * c + (lane >> 4), rr = min(n0 + r, N - 1) - n0;
-        woff[c] = (unsigned)((long long)rr * ldw * 2 + (((lane & 15) ^ r) << 4));
+        const int r = RPC * c + lane / CPR, rr = min(n0 + r, N - 1) - n0;
+        woff[c] = (unsigned)((long long)rr * ldw * 2 + (((lane % CPR) ^ wsw(r)) << 4));
     }
 #pragma unroll
     for (int c = 0; c < NAC; c++) {
-        const int r = 2 * c + (lane >> 5), rr = min(r, M - 1);
-        aoff[c] = (unsigned)((long long)rr * lda * 4 + (((lane & 31) ^ (r & 15)) << 4));
+        const int r = RPCA * c + lane / CPRA, rr = min(r, M - 1);
+        aoff[c] = (unsigned)((long long)rr * lda * 4 + (((lane % CPRA) ^ (r & 15)) << 4));
     }
     const char *wb = reinterpret_cast<const char *>(W + (long long)n0 * ldw);
     const char *ab = reinterpret_cast<const char *>(A);
@@ -195,17 +204,17 @@ __global__ void __launch_bounds__(SKS * 64) skinny_pb_lds_kernel(int M, int N, i
     for (int j = 0; j < ng; j++) {
         wait_vm_stages<NSP - 1, LPG>(min(NSP - 1, ng - 1 - j));   // group j has landed
         const G9_LDS unsigned char *sg = lds + st * SB;
-        u32x4p wf[4], af0[4], af1[4];
+        u32x4p wf[NSUB], af0[NSUB], af1[NSUB];
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
+        for (int t = 0; t < NSUB; t++) {
             const int c = 4 * t + q;   // 16-byte weight chunk of the row; activation chunks 2c, 2c + 1
-            wf[t] = *reinterpret_cast<const G9_LDS u32x4p *>(sg + i * WROW + ((c ^ i) << 4));
-            af0[t] = *reinterpret_cast<const G9_LDS u32x4p *>(sg + WB + arow * AROW + (((2 * c) ^ arow) << 4));
-            af1[t] = *reinterpret_cast<const G9_LDS u32x4p *>(sg + WB + arow * AROW + (((2 * c + 1) ^ arow) << 4));
+            wf[t] = *reinterpret_cast<const G9_LDS u32x4p *>(sg + i * WROW + ((c ^ wsw(i)) << 4));
+            af0[t] = *reinterpret_cast<const G9_LDS u32x4p *>(sg + WB + arow * AROW + (((2 * c) ^ (arow & 15)) << 4));
+            af1[t] = *reinterpret_cast<const G9_LDS u32x4p *>(sg + WB + arow * AROW + (((2 * c + 1) ^ (arow & 15)) << 4));
         }
         __builtin_amdgcn_sched_barrier(0);   // all fragment reads are issued before the first MFMA
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
+        for (int t = 0; t < NSUB; t++) {
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 const unsigned h2 = wf[t][e / 2];
@@ -444,15 +453,17 @@ int gen9blas_gemm_pb_skinny(int M, const float *A, int lda, const gen9blas_packe
         if (M <= 1) launch_pb_valu<1, 2, 4, 1>(M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
         else if (M <= 2) launch_pb_valu<2, 4, 8, 1>(M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
         else launch_pb_valu<4, 8, 8, 1>(M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
-    } else if (K % 128 == 0 && avec && 16LL * (Bp->ld * 2 + o[0].ld * 4) < (1LL << 32)) {
-        // the LDS-streaming kernel: whole 128-k groups, 16-byte activation rows, 32-bit per-lane offsets
-        // MI355X, 32 packed 4096² copies rotated, µs per synchronous call (a trivial kernel's launch-and-wait round trip
-        // is 11.3 µs of it): M = 1 and 4, 8 waves with two stages 21.7-21.9 (8 waves, three: 22.4-22.9; 4 waves with
-        // three, five: 23.1-24.3; 2 waves with four, eight: 29-31); M = 16, 4 waves with two stages 23.7 (three:
-        // 24.4; 2 waves with four, six: 30.7-31.5). Two waves per SIMD hide each other's ring and LDS waits.
-        if (M <= 4) hipLaunchKernelGGL((skinny_pb_lds_kernel<4, 8, 2>), grid, dim3(8 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
-        else if (M <= 8) hipLaunchKernelGGL((skinny_pb_lds_kernel<8, 8, 2>), grid, dim3(8 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
-        else hipLaunchKernelGGL((skinny_pb_lds_kernel<16, 4, 2>), grid, dim3(4 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
+    } else if (K % 64 == 0 && avec && 16LL * (Bp->ld * 2 + o[0].ld * 4) < (1LL << 32)) {
+        // the LDS-streaming kernel: whole 64-k groups, 16-byte activation rows, 32-bit per-lane offsets
+        // MI355X, 32 packed 4096² copies rotated, µs per synchronous call (the wait for the call is about 6-8 µs of
+        // it): 8 waves on 64-k groups, three stages at M ≤ 8 and two at M > 8: M = 8 18.2, M = 12 17.7-19.1, M = 16
+        // 18.4-19.7 against 18.9, 19.8 and 20.0-20.5 for 128-k groups (8 waves with two stages at M ≤ 8, 4 waves with
+        // two above, the largest that fit); 4 waves with four 64-k stages 19.9-21.0. Before that: M = 1 and 4 on
+        // 128-k groups, 8 waves with two stages 21.7-21.9 (three: 22.4-22.9; 4 waves with three, five: 23.1-24.3;
+        // 2 waves with four, eight: 29-31). Two waves per SIMD hide each other's ring and LDS waits.
+        if (M <= 4) hipLaunchKernelGGL((skinny_pb_lds_kernel<4, 8, 3, 64>), grid, dim3(8 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
+        else if (M <= 8) hipLaunchKernelGGL((skinny_pb_lds_kernel<8, 8, 3, 64>), grid, dim3(8 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
+        else hipLaunchKernelGGL((skinny_pb_lds_kernel<16, 8, 2, 64>), grid, dim3(8 * 64), 0, stream, M, N, K, ad, o[0].ld, wd, Bp->ld, cd, o[1].ld, (int *)flag);
     } else {
         hipLaunchKernelGGL(skinny_pb_kernel, grid, dim3(SPW * 64), 0, stream, M, N, K, ad, o[0].ld, (int)avec, wd, Bp->ld,
                            spw, cd, o[1].ld, (int *)flag);
