@@ -126,7 +126,8 @@ __global__ void __launch_bounds__(256) trsm_store_kernel(const T *Y, T *B, ll ld
 
 constexpr int TRSM_NB = 128;
 // Inverse of the diagonal block bi of L (rows and columns r0 .. r0+b-1, b ≤ TRSM_NB, in the leaf p = r0 / lb of lb
-// rows whose element (i, j) is at L[p·bstride + i·ld + j]; the block's entries above the diagonal are zeros in L),
+// rows whose element (i, j) is at L[p·bstride + i·ld + j]; the block's entries above the diagonal are read as zeros,
+// and its diagonal as ones when unit),
 // in FP64, stored in the element type into the inverted diagonal block of lb rows (lb = TRSM_NB or 2·TRSM_NB) that
 // holds it: leaf p = r0 / lb at Inv + p·lb², row stride lb, at row and column offset o = r0 − p·lb. The first
 // 128-block of a leaf also writes zeros right of itself (columns b .. lb−1 of its rows), the leaf's upper-right
@@ -139,7 +140,7 @@ constexpr int TRSM_NB = 128;
 // 8128 FMAs long); the sums differ from plain column substitution in FP64 rounding only. X and the sums live in LDS
 // (154 KiB).
 template <class T>
-__global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, ll ld, ll bstride, int n, T *Inv, int lb) {
+__global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, ll ld, ll bstride, int n, T *Inv, int lb, int unit) {
     constexpr int S = 32, NSB = TRSM_NB / S;
     static_assert(NSB == 4, "four diagonal sub-blocks, staged in the lower regions (1,0), (2,0), (3,0), (3,1)");
     __shared__ double X[TRSM_NB][TRSM_NB + 1];
@@ -163,7 +164,10 @@ __global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, ll ld, ll bst
         for (int u = 0; u < PER; u++) {
             const int e = u * 256 + t, sb = e / (S * S), ii = (e / S) % S, kk = e % S;
             const int i = sb * S + ii, k = sb * S + kk;
-            X[stage_row(sb) + ii][stage_col(sb) + kk] = i < b && k < b ? (double)v[u] : 0.0;
+            // entries above the diagonal read as zero and, with a unit diagonal, the diagonal as one, so L may be the
+            // caller's matrix itself (whose other triangle and diagonal are not referenced)
+            const double lv = kk > ii ? 0.0 : (kk == ii && unit) ? 1.0 : (double)v[u];
+            X[stage_row(sb) + ii][stage_col(sb) + kk] = i < b && k < b ? lv : 0.0;
         }
     }
     __syncthreads();
@@ -279,7 +283,8 @@ static int dgemm_dev(int type, int tA, int tB, int M, int N, int K, double alpha
     return dgemm_dev_batched(type, tA, tB, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1);
 }
 
-// Blocked forward substitution L·X = Y (L n×n lower, Y and X n×m, row strides n and m) over diagonal blocks of lb
+// Blocked forward substitution L·X = alpha·Y (L n×n lower, Y and X n×m, row strides ldl, ldy and m; alpha is applied
+// by the first product that touches each block of rows of Y, or is 1 when Y already holds alpha·R) over diagonal blocks of lb
 // rows (256 for FP32 / FP64, 128 for FP16), by recursive halving: the first half of a block range is solved, one GEMM
 // then subtracts its contribution from the right-hand side of the second half, Y[i1..i2) -= L[i1..i2, i0..i1)·X[i0..i1),
 // and the second half is solved. A single block is X_i = inv(L_ii)·Y_i with the block's inverse (128-row inverses
@@ -290,17 +295,22 @@ struct TrsmSolve {
     int type, n, m, es, lb;   // lb: rows of an inverted diagonal block (leaf)
     const char *L, *Iv;
     char *Y, *X;
+    ll ldl, ldy;              // row strides of L and Y (X: m)
+    double alpha;             // applied by the first product that touches a row block of Y (1 when Y holds alpha·R)
     int solve(int b0, int nb) const {   // leaves [b0, b0 + nb)
         if (nb == 1) {
             const int i0 = b0 * lb, b = n - i0 < lb ? n - i0 : lb;
-            return dgemm_dev(type, 0, 0, b, m, b, 1.0, Iv + (ll)b0 * lb * lb * es, lb, Y + (ll)i0 * m * es, m, 0.0,
-                             X + (ll)i0 * m * es, m);
+            // only leaf 0's rows of Y are still unscaled when it is solved
+            return dgemm_dev(type, 0, 0, b, m, b, b0 == 0 ? alpha : 1.0, Iv + (ll)b0 * lb * lb * es, lb,
+                             Y + (ll)i0 * ldy * es, ldy, 0.0, X + (ll)i0 * m * es, m);
         }
         const int h = nb / 2;
         G9_TRY(solve(b0, h));
         const int i0 = b0 * lb, i1 = (b0 + h) * lb, i2 = n < (b0 + nb) * lb ? n : (b0 + nb) * lb;
-        G9_TRY(dgemm_dev(type, 0, 0, i2 - i1, m, i1 - i0, -1.0, L + ((ll)i1 * n + i0) * es, n, X + (ll)i0 * m * es, m, 1.0,
-                         Y + (ll)i1 * m * es, m));
+        // rows i1 .. i2 are first touched here when the range starts at row 0 (an enclosing range updates its second
+        // half only after solving its first): Y = alpha·Y − L·X then, Y −= L·X after
+        G9_TRY(dgemm_dev(type, 0, 0, i2 - i1, m, i1 - i0, -1.0, L + ((ll)i1 * ldl + i0) * es, ldl, X + (ll)i0 * m * es, m,
+                         b0 == 0 ? alpha : 1.0, Y + (ll)i1 * ldy * es, ldy));
         return solve(b0 + h, nb - h);
     }
 };
@@ -347,10 +357,10 @@ int launch_tri_inverse(int es, const void *L, long long ld, long long bstride, i
     const int n = count * TRSM_NB;
     if (es == 8)
         hipLaunchKernelGGL((trsm_inv_kernel<double>), dim3(count), dim3(256), 0, stream, (const double *)L, (ll)ld,
-                           (ll)bstride, n, (double *)Inv, lb);
+                           (ll)bstride, n, (double *)Inv, lb, 0);
     else
         hipLaunchKernelGGL((trsm_inv_kernel<float>), dim3(count), dim3(256), 0, stream, (const float *)L, (ll)ld,
-                           (ll)bstride, n, (float *)Inv, lb);
+                           (ll)bstride, n, (float *)Inv, lb, 0);
     G9_HIP(hipGetLastError());
     return 0;
 }
@@ -508,9 +518,23 @@ int gen9blas_trsm(int type, int side, int uplo, int transA, int diag, int M, int
     // Leaves of 256 rows for FP32 / FP64: each leaf inverse is composed from two 128-row FP64 inverses (below); FP16
     // keeps 128-row leaves (the composition would round once more in FP16)
     const int nbl = (n + TRSM_NB - 1) / TRSM_NB, lb = es >= 4 ? 2 * TRSM_NB : TRSM_NB, nleaf = (n + lb - 1) / lb;
+    // A left solve with A lower and not transposed reads both operands where they lie: every product below reads L
+    // strictly below its diagonal blocks, the block inversion masks the rest of A itself, B is the right-hand side
+    // updated in place (alpha applied by the first product that touches each block of rows), and only the solution
+    // is copied back. Every other case first writes L and alpha·R out in the solve's order (reversed for an upper
+    // triangle, transposed for the right side).
+    const bool direct = left && !tr && !rev;
     void *Ld, *Yd, *Iv, *Zd;
-    G9_TRY(scratch(SLOT_T, (size_t)n * n * es, &Ld));
-    G9_TRY(scratch(SLOT_X, (size_t)n * m * es, &Yd));
+    ll ldl = n, ldy = m;
+    if (direct) {
+        Ld = ops[0].dev;
+        ldl = ops[0].ld;
+        Yd = ops[1].dev;
+        ldy = ops[1].ld;
+    } else {
+        G9_TRY(scratch(SLOT_T, (size_t)n * n * es, &Ld));
+        G9_TRY(scratch(SLOT_X, (size_t)n * m * es, &Yd));
+    }
     // the leaf inverses, then (lb > TRSM_NB) the products C·I1 of the composition, TRSM_NB² per leaf
     const size_t inv_bytes = (size_t)nleaf * lb * lb * es;
     G9_TRY(scratch(SLOT_Y, inv_bytes + (lb > TRSM_NB ? (size_t)nleaf * TRSM_NB * TRSM_NB * es : 0), &Iv));
@@ -518,37 +542,41 @@ int gen9blas_trsm(int type, int side, int uplo, int transA, int diag, int M, int
     G9_TRY(by_es(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
         using S = typename Acc<T>::S;
-        hipLaunchKernelGGL((trsm_l_kernel<T>), dim3(grid_for((ll)n * n)), dim3(256), 0, stream, (const T *)ops[0].dev,
-                           ops[0].ld, (T *)Ld, n, uplo == GEN9BLAS_LOWER, tr, diag != 0, rev);
-        hipLaunchKernelGGL((trsm_y_kernel<T>), dim3(grid_for((ll)n * m)), dim3(256), 0, stream, (const T *)ops[1].dev,
-                           ops[1].ld, (T *)Yd, n, m, left, rev, (S)alpha);
-        hipLaunchKernelGGL((trsm_inv_kernel<T>), dim3(nbl), dim3(256), 0, stream, (const T *)Ld, (ll)n, (ll)lb * (n + 1),
-                           n, (T *)Iv, lb);
+        if (!direct) {
+            hipLaunchKernelGGL((trsm_l_kernel<T>), dim3(grid_for((ll)n * n)), dim3(256), 0, stream, (const T *)ops[0].dev,
+                               ops[0].ld, (T *)Ld, n, uplo == GEN9BLAS_LOWER, tr, diag != 0, rev);
+            hipLaunchKernelGGL((trsm_y_kernel<T>), dim3(grid_for((ll)n * m)), dim3(256), 0, stream, (const T *)ops[1].dev,
+                               ops[1].ld, (T *)Yd, n, m, left, rev, (S)alpha);
+        }
+        hipLaunchKernelGGL((trsm_inv_kernel<T>), dim3(nbl), dim3(256), 0, stream, (const T *)Ld, ldl, (ll)lb * (ldl + 1),
+                           n, (T *)Iv, lb, diag != 0);
         G9_HIP(hipGetLastError());
         return 0;
     }));
     if (lb > TRSM_NB) {
         // A leaf [I1 0; C I2]⁻¹ = [inv(I1) 0; −inv(I2)·C·inv(I1) inv(I2)]: the kernel above left inv(I1), inv(I2) and
         // the zero quadrant; two GEMMs form the lower-left quadrant, batched over the leaves with two whole halves
-        // (leaf p: C at L + p·lb·(n+1) + TRSM_NB·n, inv(I1) at Inv_p, inv(I2) at Inv_p + TRSM_NB·(lb+1)), then once
+        // (leaf p: C at L + p·lb·(ldl+1) + TRSM_NB·ldl, inv(I1) at Inv_p, inv(I2) at Inv_p + TRSM_NB·(lb+1)), then once
         // for a last leaf whose second half has b2 < TRSM_NB rows.
         const ll NB = TRSM_NB;
         const char *L0 = (const char *)Ld;
         char *I0 = (char *)Iv, *Tm = I0 + inv_bytes;
         const int full = n / lb;
-        G9_TRY(dgemm_dev_batched(type, 0, 0, TRSM_NB, TRSM_NB, TRSM_NB, 1.0, L0 + NB * n * es, n, (ll)lb * (n + 1), I0, lb,
-                                 (ll)lb * lb, 0.0, Tm, NB, NB * NB, full));
+        G9_TRY(dgemm_dev_batched(type, 0, 0, TRSM_NB, TRSM_NB, TRSM_NB, 1.0, L0 + NB * ldl * es, ldl, (ll)lb * (ldl + 1), I0,
+                                 lb, (ll)lb * lb, 0.0, Tm, NB, NB * NB, full));
         G9_TRY(dgemm_dev_batched(type, 0, 0, TRSM_NB, TRSM_NB, TRSM_NB, -1.0, I0 + NB * (lb + 1) * es, lb, (ll)lb * lb, Tm,
                                  NB, NB * NB, 0.0, I0 + NB * lb * es, lb, (ll)lb * lb, full));
         const ll i0 = (ll)full * lb;
         const int b2 = n - (int)i0 - TRSM_NB;
         if (b2 > 0) {
             char *Ip = I0 + i0 * lb * es;
-            G9_TRY(dgemm_dev(type, 0, 0, b2, TRSM_NB, TRSM_NB, 1.0, L0 + ((i0 + NB) * n + i0) * es, n, Ip, lb, 0.0, Tm, NB));
+            G9_TRY(dgemm_dev(type, 0, 0, b2, TRSM_NB, TRSM_NB, 1.0, L0 + ((i0 + NB) * ldl + i0) * es, ldl, Ip, lb, 0.0, Tm,
+                             NB));
             G9_TRY(dgemm_dev(type, 0, 0, b2, TRSM_NB, b2, -1.0, Ip + NB * (lb + 1) * es, lb, Tm, NB, 0.0, Ip + NB * lb * es, lb));
         }
     }
-    TrsmSolve rec{type, n, m, es, lb, (const char *)Ld, (const char *)Iv, (char *)Yd, (char *)Zd};
+    TrsmSolve rec{type, n, m, es, lb, (const char *)Ld, (const char *)Iv, (char *)Yd, (char *)Zd, ldl, ldy,
+                  direct ? alpha : 1.0};
     G9_TRY(rec.solve(0, nleaf));
     G9_TRY(by_es(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
