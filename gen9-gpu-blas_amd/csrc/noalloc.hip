@@ -1,14 +1,17 @@
 // gen9blas_gemm_noalloc: gen9blas_gemm for callers that cannot allocate device memory (tight serving loops, harnesses
 // that forbid hipMalloc). It runs the same kernels with the same dispatch as gen9blas_gemm; the only work buffer a
-// GEMM on device operands uses, the split-K partial slices, comes from a static device array instead of the library's
-// growing buffers, so the call itself allocates nothing.
+// GEMM on device operands uses comes from a static device array instead of the library's growing buffers, so the
+// call itself allocates nothing. That buffer holds the split-K partial slices of the tile kernels, or, for a skinny
+// product (min(M, N) ≤ 16), a transposed small operand gathered K-contiguous (M·K elements) and the K-split partial
+// sums of weights stored K×N (parts · M · N FP32 values, with parts · N ≤ 4 · 64 · CUs: 4 MiB at M = 16 on 256 CUs).
 //
 // Size of that array: without a split forced by GEN9BLAS_SPLITK, a product splits K into s > 1 slices only while
 // tiles · s ≤ CUs, and the slices hold ns ≤ s partial copies of C, M · N ≤ tiles · BM · BN elements each. So one
 // call needs at most CUs × (largest split tile: 256 × 256 FP32 sums = 256 × 128 FP64 sums = 256 KiB) bytes,
 // 64 MiB on MI355X's 256 CUs: DGEMM 2048³ on 128 tiles of 256×128 split two ways uses all of it. A forced split can
-// need more and is then rejected with INVALID_ARG before anything is launched (as is every product on a device
-// with more CUs than the bound assumes, should one need more).
+// need more, as can a skinny product whose gathered operand alone passes about 60 MiB (M · K · element size); both
+// are rejected with INVALID_ARG before anything is launched (as is every product on a device with more CUs than the
+// bound assumes, should one need more).
 #include "internal.h"
 #include <stdio.h>
 

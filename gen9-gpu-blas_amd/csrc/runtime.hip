@@ -146,8 +146,8 @@ int scratch(int slot, size_t bytes, void **p) {
             G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "%s takes device operands only: an operand in host memory would need a "
                     "staging buffer", fixed_who);
         if (bytes > fixed_bytes)
-            G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "%s: this product needs %zu bytes of split-K work space, more than its "
-                    "fixed maximum of %zu", fixed_who, bytes, fixed_bytes);
+            G9_FAIL(GEN9BLAS_ERR_INVALID_ARG, "%s: this product needs %zu bytes of work space (split-K slices, or a "
+                    "skinny product's gathered operand and partial sums), more than its fixed maximum of %zu", fixed_who, bytes, fixed_bytes);
         *p = fixed_base;
         return 0;
     }

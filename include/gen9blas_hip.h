@@ -32,9 +32,11 @@ GEN9BLAS_API int gen9blas_flush(void);
 // gen9blas_gemm that allocates nothing. No counterpart in the reference: it is for callers that cannot allocate
 // device memory (tight serving loops, harnesses that forbid hipMalloc). Same arguments, kernels and results as
 // gen9blas_gemm, but A, B and C must be device memory (an operand in host memory would need staging buffers:
-// INVALID_ARG before anything runs), and the split-K work space is a static 64 MiB device array per GPU, enough for
-// every default dispatch on MI355X (CUs × the largest split tile); a product that would need more (only with a split
-// forced by GEN9BLAS_SPLITK) gives INVALID_ARG before any launch. It runs on the library stream like every call and
+// INVALID_ARG before anything runs), and the work space is a static 64 MiB device array per GPU: enough for the
+// split-K slices of every default dispatch on MI355X (CUs × the largest split tile) and for the skinny products
+// (min(M, N) ≤ 16: a transposed small operand gathered, M·K elements; the K-split partial sums of weights stored
+// K×N, at most 4 MiB). A product that would need more (a split forced by GEN9BLAS_SPLITK, or a skinny product whose
+// M·K·element size passes about 60 MiB) gives INVALID_ARG before any launch. It runs on the library stream like every call and
 // is not meant for HIP graph capture. Call gen9blas_init first: the first call of the library opens the device. All
 // calls on one GPU share the array, so calls that overlap on one GPU (from several threads) race.
 GEN9BLAS_API int gen9blas_gemm_noalloc(int type, int transA, int transB, int M, int N, int K, double alpha,

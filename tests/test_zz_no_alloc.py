@@ -5,7 +5,8 @@ bit: products that take split-K (whose slices then live in the entry point's sta
 tiles and the whole-tile FP16 kernel, in every type, two calls in a row with the second smaller (the work space
 keeps the last call's contents; a split-K slice writes every element it is later read at). The largest default
 splits are included: DGEMM 2048³ (128 tiles of 256×128 split two ways: the whole 64 MiB), FP64 640×640×1024 and FP16
-1280×1280×1000 on the general kernel. Both are also held to the GEMM bounds against float64. Host operands (checked
+1280×1280×1000 on the general kernel. Skinny products whose gathered operand and partial sums live in that work
+space are included too. Both are also held to the GEMM bounds against float64. Host operands (checked
 before any dispatch, so the staging paths never run) and a work space beyond the fixed maximum give INVALID_ARG
 before any launch (the latter needs a split forced with GEN9BLAS_SPLITK, read once per process: a child process).
 A fresh child process checks the property itself: the free device memory does not move across no-alloc calls,
@@ -57,6 +58,10 @@ def _err(W, opA, opB, alpha, beta, c0):
 CASES = [((200, 136, 1000, 0, 0), (100, 72, 500, 1, 1)),
          ((130, 260, 4096, 1, 0), (64, 64, 777, 0, 1)),
          ((1024, 1024, 512, 0, 0), (512, 384, 256, 0, 1))]
+# skinny products (min(M, N) ≤ 16) that use the work space: weights stored K×N (FP16: K split in 4 parts, partial
+# sums in the work space) and a transposed small operand (gathered into the work space), the second call smaller
+SKINNY = [((4, 4096, 4096, 0, 0), (16, 2048, 1024, 1, 0)),
+          ((4096, 8, 2048, 0, 0), (1000, 3, 512, 1, 1))]
 # the largest default work spaces: 64 MiB (FP64 2048³), then 12.5 MiB (FP64 640×640×1024, FP16 1280×1280×1000)
 LARGE = {"D": ((2048, 2048, 2048, 0, 0), (640, 640, 1024, 1, 0)),
          "H": ((1280, 1280, 1000, 0, 0), (640, 640, 1024, 0, 1)),
@@ -83,6 +88,12 @@ def _compare(g9, torch_dev, kind, shapes, seed):
 @pytest.mark.parametrize("pair", range(len(CASES)))
 def test_noalloc_matches_gemm(g9, torch_dev, kind, pair):
     _compare(g9, torch_dev, kind, CASES[pair], 40 + pair)
+
+
+@pytest.mark.parametrize("kind", ["S", "H", "HS"])
+@pytest.mark.parametrize("pair", range(len(SKINNY)))
+def test_noalloc_skinny(g9, torch_dev, kind, pair):
+    _compare(g9, torch_dev, kind, SKINNY[pair], 60 + pair)
 
 
 @pytest.mark.parametrize("kind", sorted(LARGE))
