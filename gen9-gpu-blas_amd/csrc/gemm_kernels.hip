@@ -124,6 +124,16 @@ static int launch_layout(const GemmParams<typename Mma<T>::Sum> &p, int count) {
         }
         return launch_t<T, CF::small, AK, BKC, VEC>(p, count);
     }
+    // FP64 whose big tiles are exactly half the CUs (K would be split in two, with a reduction pass after): the small
+    // tiles instead, when they fill the CUs. MI355X, µs (TFLOP/s): 1024×4096×1024 with beta = 1 (the triangular
+    // solve's update of 1024 rows) 152.9 → 141.5 (56.2 → 60.7), 2048³ 268.4 → 258.3 (64.0 → 66.5); DTRSM n = 4096
+    // 1.613 → 1.565 ms. 64×64 tiles with two k groups there: 142.8 and 265.9.
+    if constexpr (sizeof(T) == 8) {
+        const long long ts = (long long)((p.M + CF::small.BM - 1) / CF::small.BM) *
+                             ((p.N + CF::small.BN - 1) / CF::small.BN) * count;
+        if (splitk_forced() < 0 && count == 1 && big_tiles * 2 == num_cus && ts >= num_cus)
+            return launch_t<T, CF::small, AK, BKC, VEC>(p, count);
+    }
     // FP32 with B k-contiguous has 64×64 big tiles, so a product of exactly num_cus of them lands here: the same
     // two-k-group tiles (NT n = 1024)
     if constexpr (sizeof(T) == 4) {

@@ -8,7 +8,8 @@
 // Size of that array: without a split forced by GEN9BLAS_SPLITK, a product splits K into s > 1 slices only while
 // tiles · s ≤ CUs, and the slices hold ns ≤ s partial copies of C, M · N ≤ tiles · BM · BN elements each. So one
 // call needs at most CUs × (largest split tile: 256 × 256 FP32 sums = 256 × 128 FP64 sums = 256 KiB) bytes,
-// 64 MiB on MI355X's 256 CUs: DGEMM 2048³ on 128 tiles of 256×128 split two ways uses all of it. A forced split can
+// 64 MiB on MI355X's 256 CUs: an FP16 product on the general kernel with 128 tiles of 256×256 split two ways
+// (2048×4096×1000, say) uses all of it. A forced split can
 // need more, as can a skinny product whose gathered operand alone passes about 60 MiB (M · K · element size); both
 // are rejected with INVALID_ARG before anything is launched (as is every product on a device with more CUs than the
 // bound assumes, should one need more).

@@ -47,7 +47,8 @@ GEMMS = [
     ("sgemm n=1024", "f32", 1024, 1024, 1024, False, 1.0, 0.0, False),
     ("sgemm split-K 130x260x4096", "f32", 130, 260, 4096, False, 1.0, 0.0, False),
     ("dgemm n=1024", "f64", 1024, 1024, 1024, False, 1.0, 0.0, False),
-    ("dgemm 2048 split-K", "f64", 2048, 2048, 2048, False, 1.0, 0.0, False),
+    ("dgemm 2048 small tiles", "f64", 2048, 2048, 2048, False, 1.0, 0.0, False),
+    ("hgemm general split-K 2048x4096x1000", "f16", 2048, 4096, 1000, False, 1.0, 0.0, False),
     ("dgemm 640x640x1024 tB beta", "f64", 640, 640, 1024, True, -1.0, 0.25, False),
 ]
 

@@ -4,7 +4,8 @@ Same kernels and dispatch as gen9blas_gemm, so on the same device operands the r
 bit: products that take split-K (whose slices then live in the entry point's static work space), the two-k-group
 tiles and the whole-tile FP16 kernel, in every type, two calls in a row with the second smaller (the work space
 keeps the last call's contents; a split-K slice writes every element it is later read at). The largest default
-splits are included: DGEMM 2048³ (128 tiles of 256×128 split two ways: the whole 64 MiB), FP64 640×640×1024 and FP16
+splits are included: FP16 2048×4096×1000 (128 general-kernel tiles of 256×256 split two ways: the whole 64 MiB),
+FP64 640×640×1024 (split four ways) and FP16
 1280×1280×1000 on the general kernel. Skinny products whose gathered operand and partial sums live in that work
 space are included too. Both are also held to the GEMM bounds against float64. Host operands (checked
 before any dispatch, so the staging paths never run) and a work space beyond the fixed maximum give INVALID_ARG
@@ -62,9 +63,10 @@ CASES = [((200, 136, 1000, 0, 0), (100, 72, 500, 1, 1)),
 # sums in the work space) and a transposed small operand (gathered into the work space), the second call smaller
 SKINNY = [((4, 4096, 4096, 0, 0), (16, 2048, 1024, 1, 0)),
           ((4096, 8, 2048, 0, 0), (1000, 3, 512, 1, 1))]
-# the largest default work spaces: 64 MiB (FP64 2048³), then 12.5 MiB (FP64 640×640×1024, FP16 1280×1280×1000)
+# the largest default work spaces: 64 MiB (FP16 2048×4096×1000), then 12.5 MiB (FP64 640×640×1024, FP16
+# 1280×1280×1000); FP64 2048³, whose big tiles are half the CUs, takes the small tiles instead of a split
 LARGE = {"D": ((2048, 2048, 2048, 0, 0), (640, 640, 1024, 1, 0)),
-         "H": ((1280, 1280, 1000, 0, 0), (640, 640, 1024, 0, 1)),
+         "H": ((2048, 4096, 1000, 0, 0), (1280, 1280, 1000, 0, 1)),
          "HS": ((1280, 1280, 1000, 1, 1), (1000, 600, 1000, 0, 0))}
 
 
@@ -156,7 +158,7 @@ for name in ("gen9blas_gemm", "gen9blas_gemm_noalloc"):
     getattr(L, name).argtypes = [i, i, i, i, i, i, d, p, i, p, i, d, p, i]
 assert L.gen9blas_init() == 0
 dt = {0: torch.float16, 2: torch.float16, 3: torch.float64, 1: torch.float32}
-cases = [(3, 2048, 2048, 2048), (0, 1280, 1280, 1000), (2, 1280, 1280, 1000), (3, 640, 640, 1024), (1, 200, 136, 1000)]
+cases = [(0, 2048, 4096, 1000), (3, 2048, 2048, 2048), (0, 1280, 1280, 1000), (2, 1280, 1280, 1000), (3, 640, 640, 1024), (1, 200, 136, 1000)]
 bufs = [[torch.randn(s, dtype=dt[t], device="cuda") for s in ((M, K), (K, N), (M, N))] for (t, M, N, K) in cases]
 small = [torch.ones((64, 64), dtype=torch.float32, device="cuda") for _ in range(3)]
 def call(name, t, M, N, K, a, b, c):
