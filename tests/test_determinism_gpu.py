@@ -6,7 +6,8 @@ work between the two runs (a different product, so the work buffers and caches h
 bytes must be identical: GEMM in every type on the whole-tile kernels, the general kernel, split-K and the
 two-k-group tiles (BASELINE's shapes included: FP16 n = 1024/2048/4096 in both modes, FP32 n = 4096 and the odd
 3000×11008×4096 product with beta, FP64 n = 1024), the skinny kernels at M = 1..16, SDOT at 2^26 and SGEMV N/T at
-16384², plus the level-3 calls on the GEMM kernels. Sums are in fixed order everywhere (split-K slices added in index
+16384², the skinny products with weights stored K×N, SYMV / TRMV / TRSV at n = 16384, plus the level-3 calls on
+the GEMM kernels. Sums are in fixed order everywhere (split-K slices added in index
 order, FP64 reduction partials summed by one block), so nothing may depend on timing.
 """
 import numpy as np
@@ -87,6 +88,45 @@ def test_skinny_twice(g9, torch_dev, M):
         torch.cuda.synchronize()
     for a, b in zip(first, second):
         assert _same(a, b), f"skinny M={M}: two runs differ"
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_skinny_weights_k_by_n_twice(g9, torch_dev, M):
+    """C = A·W with W stored K×N (4096² FP16, the split-K matrix-core form and its fixed-order sum), and with a
+    transposed small operand (gathered first): same bytes twice."""
+    torch = torch_dev
+    W = _data(torch, 101, (4096, 4096), torch.float16) * 0.02
+    A = _data(torch, 8, (M, 4096), torch.float16)
+    At = _data(torch, 9, (4096, M), torch.float16)
+    first, second = [], []
+    for out in (first, second):
+        out.append(g9.gemm(A, W))
+        out.append(g9.gemm(At.t(), W))
+        g9.gemm(W[:M].contiguous(), W)
+        torch.cuda.synchronize()
+    for a, b in zip(first, second):
+        assert _same(a, b), f"skinny K×N M={M}: two runs differ"
+
+
+def test_level2_partials_twice(g9, torch_dev):
+    """SYMV and TRMV (per-row and per-column partials summed in a fixed order by a second kernel) and TRSV on inverted
+    blocks at n = 16384 FP32: same bytes twice."""
+    torch = torch_dev
+    n = 16384
+    A = _data(torch, 30, (n, n), torch.float32) / 128
+    A.diagonal().add_(4.0)
+    v = _data(torch, 31, n, torch.float32)
+    calls = [("symv L", lambda: g9.symv(A, v, uplo="L")), ("symv U", lambda: g9.symv(A, v, uplo="U")),
+             ("trmv LT", lambda: g9.trmv(A, v.clone(), uplo="L", trans=True)),
+             ("trsv LN", lambda: g9.trsv(A, v.clone(), uplo="L")),
+             ("trsv UT", lambda: g9.trsv(A, v.clone(), uplo="U", trans=True))]
+    for name, fn in calls:
+        r1 = fn()
+        g9.symv(A[:300, :300], v[:300])
+        torch.cuda.synchronize()
+        r2 = fn()
+        torch.cuda.synchronize()
+        assert _same(r1, r2), f"{name}: two runs differ"
 
 
 def test_level12_twice(g9, torch_dev):
