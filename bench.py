@@ -591,7 +591,7 @@ def main():
 
 
 def config_summary(res):
-    """One short line per BASELINE configuration measured (GPU rate, fraction of its roofline, the CPU path's rate),
+    """One short line per benchmarked configuration (GPU rate, fraction of its roofline, the CPU path's rate),
     printed last so that a truncated log still holds every configuration."""
     cpu = res.get("cpu_path", {})
 
@@ -623,7 +623,7 @@ def config_summary(res):
 def cpu_baselines(budget_s=40.0):
     """The reference's CPU path (its BLAS layer forwards to OpenBLAS; HGEMM and skinny are NumPy FP32 math on the
     FP16 inputs, reference: lib/src/cblas.c:43-56, bench/gemm_cpu.py:33-37, bench/l12_cpu.py:13-16) on the host
-    cores, for every BASELINE configuration: best of up to 5 timed runs after one warm-up, on the same inputs as the
+    cores, for every benchmarked configuration: best of up to 5 timed runs after one warm-up, on the same inputs as the
     GPU cases. Returns (the HGEMM n = 4096 entry, which is `cpu_baseline`, {config: entry}). Bounded: each config stops
     after ~3 s of runs and the whole set after `budget_s`."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))

@@ -4,7 +4,7 @@ The reference's golden tool runs every seeded call twice and flags a call whose 
 (reference: tools/golden/blas_golden.py:29-61). Here each call below runs twice on the same inputs, with other
 work between the two runs (a different product, so the work buffers and caches hold other data), and the result
 bytes must be identical: GEMM in every type on the whole-tile kernels, the general kernel, split-K and the
-two-k-group tiles (BASELINE's shapes included: FP16 n = 1024/2048/4096 in both modes, FP32 n = 4096 and the odd
+two-k-group tiles (the benchmarked shapes included: FP16 n = 1024/2048/4096 in both modes, FP32 n = 4096 and the odd
 3000×11008×4096 product with beta, FP64 n = 1024), the skinny kernels at M = 1..16, SDOT at 2^26 and SGEMV N/T at
 16384², the skinny products with weights stored K×N, SYMV / TRMV / TRSV at n = 16384, plus the level-3 calls on
 the GEMM kernels. Sums are in fixed order everywhere (split-K slices added in index
@@ -76,7 +76,7 @@ def test_gemm_twice(g9, torch_dev, case):
 
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
 def test_skinny_twice(g9, torch_dev, M):
-    """C = A·Wᵀ at W 4096² FP16 (BASELINE's skinny config), both roles (M×4096 and 4096×M)."""
+    """C = A·Wᵀ at W 4096² FP16 (the benchmarked skinny configuration), both roles (M×4096 and 4096×M)."""
     torch = torch_dev
     W = _data(torch, 100, (4096, 4096), torch.float16) * 0.02
     A = _data(torch, 7, (M, 4096), torch.float16)

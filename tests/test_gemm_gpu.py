@@ -176,7 +176,7 @@ def _sampled_rows_error(W, A, B, rows, alpha=1.0, beta=0.0, C0=None, tB=False):
 @pytest.mark.parametrize("kind,n", [("H", 1024), ("H", 2048), ("H", 4096), ("HS", 1024), ("HS", 2048), ("HS", 4096),
                                     ("S", 1024), ("S", 4096), ("D", 1024), ("D", 4096)])
 def test_gemm_config_sizes(g9, orc, torch_dev, kind, n):
-    """square n, NN, alpha = 1, beta = 0; FP16 inputs N(0, 1), FP32/FP64 U[-1, 1] (device buffers)."""
+    """The benchmarked configurations: square n, NN, alpha = 1, beta = 0; FP16 inputs N(0, 1), FP32/FP64 U[-1, 1] (device buffers)."""
     torch = torch_dev
     dt = KIND_DT[kind]
     if dt == np.float16:
@@ -245,7 +245,7 @@ def test_sgemm_generic_two_group_fast_loop(tmp_path):
 
 
 def test_sgemm_odd_shape(g9, orc, torch_dev):
-    """BASELINE odd shape: M = 3000, N = 11008, K = 4096, transB (B stored N×K), beta = 0.5, C pre-filled U[-1, 1]."""
+    """The benchmarked odd shape: M = 3000, N = 11008, K = 4096, transB (B stored N×K), beta = 0.5, C pre-filled U[-1, 1]."""
     torch = torch_dev
     M, N, K = 3000, 11008, 4096
     A = orc.uniform((M, K), np.float32, orc.SEED_A)

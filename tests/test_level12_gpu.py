@@ -119,7 +119,7 @@ def test_gemv_submatrix(g9, orc, dt):
 
 
 def test_level2_config_device(g9, orc, torch_dev):
-    """BASELINE level 1/2 config at full size on device buffers: SAXPY, SDOT (2^26), SGEMV N/T (16384²)."""
+    """The benchmarked level 1/2 configuration at full size on device buffers: SAXPY, SDOT (2^26), SGEMV N/T (16384²)."""
     torch = torch_dev
     n = 1 << 26
     x = orc.uniform(n, np.float32, orc.SEED_X)
