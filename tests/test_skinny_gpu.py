@@ -123,9 +123,9 @@ def test_skinny_matrix_core_kernel(g9, torch_dev, M, N, K):
     assert np.array_equal(big[mask], D0[mask]), "write outside the C slice"
 
 
-# (M, N, K): weights stored K×N (N-contiguous), shapes for the FP16 matrix-core form (K a multiple of 256, N a
-# multiple of 8: whole 16-column strips and a last strip shifted back when N % 16 = 8) and for the vector form
-# (K or N off those multiples, N below 16)
+# (M, N, K): weights stored K×N (N-contiguous), shapes for the FP16 matrix-core form (K a multiple of 64, N ≥ 64 and
+# a multiple of 8: 64-column strips, the last one shifted back to end at N, K split in 1, 2 or 4 parts) and for the
+# vector form (K or N off those multiples, N below 64, and FP32)
 KN_SHAPES = [(1, 4096, 512), (2, 264, 256), (3, 77 * 8, 768), (4, 2056, 1024), (7, 16, 256), (8, 520, 2048),
              (12, 1000, 512), (16, 4096, 256), (16, 24, 4096), (1, 1000, 777), (5, 333, 300), (16, 9, 513),
              (2, 4100, 1000)]
