@@ -86,6 +86,7 @@ template <class S> struct GemmParams {
     // to P + z·M·N (row stride N, accumulator type S); a reduction kernel then forms alpha·Σ + beta·C
     S *P;
     int kper, vec_p;
+    int kpair = 0;   // KLIM: the second half of the dispatch order reversed (see the tile mapping)
 };
 
 // 16 bytes (V elements) of row r, columns c .. c+V-1 of a row-major matrix X (R valid rows, Cc valid columns, row
@@ -240,8 +241,13 @@ __global__ void __launch_bounds__(WM *WN * 64 * KG) gemm_kernel(GemmParams<typen
     } else if constexpr (KLIM != 0) {
         // Tiles in dispatch order, longest k range first, without the XCD remap: consecutive workgroups go to
         // different XCDs, so every XCD gets long and short tiles alike (a contiguous range per XCD would give one XCD
-        // all the longest tiles)
-        const int b = blockIdx.x;
+        // all the longest tiles). kpair (all tiles resident at once, two per CU): workgroups i and i + T/2 share a
+        // CU, and the second half takes the ranks in reverse, so that each CU pairs a long range with a short one
+        int b = blockIdx.x;
+        if (p.kpair) {
+            const int nt = p.tiles_m * p.tiles_n, h = nt / 2;
+            if (b >= h) b = nt - 1 - (b - h);
+        }
         if constexpr (KLIM <= 2) {   // the range depends on the tile row
             const int tr = b / p.tiles_n;
             m0 = (KLIM == 1 ? p.tiles_m - 1 - tr : tr) * BM;

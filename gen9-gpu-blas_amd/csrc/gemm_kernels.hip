@@ -278,15 +278,29 @@ static bool sgemm_tiles_ok(const GemmCall &c) {
            (c.ldb * es) % 16 == 0 && (c.ldc * es) % 16 == 0 &&
            (c.count == 1 || ((c.sA * es) % 16 == 0 && (c.sB * es) % 16 == 0 && (c.sC * es) % 16 == 0));
 }
+// Workgroups of KERN (threads each) that one CU holds at once, from the runtime's occupancy query (1 if it fails).
+template <auto KERN> static int wgs_per_cu(int threads) {
+    static const int occ = [threads] {
+        int o = 0;
+        return hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, KERN, threads, 0) == hipSuccess && o > 0 ? o : 1;
+    }();
+    return occ;
+}
+// k-limited tiles in the paired order: more tiles than CUs, all of them resident at once with two per CU (so that
+// workgroups i and i + tiles / 2 run side by side on one CU, each long range beside a short one). With fewer per CU
+// the later half starts as CUs free up, and the longest-first order balances better.
+static int klim_pair(long long tiles, int per_cu) { return tiles > num_cus && tiles <= 2LL * num_cus && per_cu >= 2; }
+
 // Triangle (TRI) and k-limited (KLIM) modes of the FP32 whole-tile kernel for SYRK / SYR2K / TRMM: one product,
 // whole tiles (the callers check), `tiles` workgroups.
 template <int BM, int BN, int WM, int WN, int NS, int BLK, bool AK, bool BKC, int TRI, int KLIM>
 static int launch_sg_mode(const sg::Params &p0, long long tiles) {
+    constexpr auto kern = sg::sgemm_kernel<BM, BN, WM, WN, NS, AK, BKC, BLK, TRI, KLIM>;
     sg::Params p = p0;
     p.tiles_m = p.M / BM;
     p.tiles_n = p.N / BN;
-    hipLaunchKernelGGL((sg::sgemm_kernel<BM, BN, WM, WN, NS, AK, BKC, BLK, TRI, KLIM>), dim3((unsigned)tiles),
-                       dim3(WM * WN * 64), 0, stream, p);
+    if constexpr (KLIM != 0) p.kpair = klim_pair(tiles, wgs_per_cu<kern>(WM * WN * 64));
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(WM * WN * 64), 0, stream, p);
     G9_HIP(hipGetLastError());
     return 0;
 }
@@ -502,18 +516,19 @@ int launch_gemm_tri(const GemmCall &c, bool lower) {
     G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "type %d unavailable", c.type);
 }
 
-// Product with a triangular operand (TRMM on the explicit triangular matrix): each tile's k range is cut to where the
-// triangle is non-zero (klim as gemm_kernel's KLIM), one launch over every tile of C, longest ranges dispatched first.
-// Layout NN only (both operands as stored), one product.
-template <class T, int KLIM, bool VEC>
+// Product with a triangular operand (TRMM on the explicit triangular matrix, TRSM's leaf products): each tile's k
+// range is cut to where the triangle is non-zero (klim as gemm_kernel's KLIM), one launch over every tile of C,
+// longest ranges dispatched first; the small tiles when the big ones are fewer than the CUs. Layout NN only (both
+// operands as stored), one product.
+template <class T, TileCfg C, int KLIM, bool VEC>
 static int launch_klim_t(GemmParams<typename Mma<T>::Sum> p) {
-    constexpr TileCfg C = Cfg<T, true, false, VEC>::big;
     p.tiles_m = (p.M + C.BM - 1) / C.BM;
     p.tiles_n = (p.N + C.BN - 1) / C.BN;
     const long long tiles = (long long)p.tiles_m * p.tiles_n;
     if (tiles > 0x7fffffffLL) G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "gemm grid too large (%d × %d tiles)", p.tiles_m, p.tiles_n);
-    hipLaunchKernelGGL((gemm_kernel<T, C.BM, C.BN, C.WM, C.WN, true, false, VEC, true, false, 0, KLIM>), dim3((unsigned)tiles),
-                       dim3(C.WM * C.WN * 64), 0, stream, p);
+    constexpr auto kern = gemm_kernel<T, C.BM, C.BN, C.WM, C.WN, true, false, VEC, true, false, 0, KLIM>;
+    p.kpair = klim_pair(tiles, wgs_per_cu<kern>(C.WM * C.WN * 64));
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(C.WM * C.WN * 64), 0, stream, p);
     G9_HIP(hipGetLastError());
     return 0;
 }
@@ -534,17 +549,35 @@ static int launch_klim_typed(const GemmCall &c, int klim) {
     const long long cal = es * 4 < 16 ? es * 4 : 16;
     p.vec_c = ((uintptr_t)c.C % cal == 0) && (c.ldc * es) % cal == 0;
     const bool vec = ((uintptr_t)c.A % 16 == 0) && ((uintptr_t)c.B % 16 == 0) && (c.lda * es) % 16 == 0 && (c.ldb * es) % 16 == 0;
-    switch (klim * 2 + (vec ? 1 : 0)) {
-    case 2: return launch_klim_t<T, 1, false>(p);
-    case 3: return launch_klim_t<T, 1, true>(p);
-    case 4: return launch_klim_t<T, 2, false>(p);
-    case 5: return launch_klim_t<T, 2, true>(p);
-    case 6: return launch_klim_t<T, 3, false>(p);
-    case 7: return launch_klim_t<T, 3, true>(p);
-    case 8: return launch_klim_t<T, 4, false>(p);
-    case 9: return launch_klim_t<T, 4, true>(p);
-    }
-    G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "k-limited product: mode %d", klim);
+    // tile class: FP16 the big tiles when they are at least the CUs; FP32 / FP64 the first of big, small and (FP64)
+    // 64×64 that makes two workgroups per CU or more, so that long and short k ranges can share the CUs
+    const auto by_cfg = [&](auto vc) -> int {
+        constexpr bool V = decltype(vc)::value;
+        using CF = Cfg<T, true, false, V>;
+        constexpr TileCfg tiny{64, 64, 2, 2};
+        const auto ntiles = [&](TileCfg t) {
+            return (long long)((c.M + t.BM - 1) / t.BM) * ((c.N + t.BN - 1) / t.BN);
+        };
+        constexpr bool half = sizeof(T) == 2, dbl = sizeof(T) == 8;
+        const long long want = half ? num_cus : 2LL * num_cus;
+        const int cls = ntiles(CF::big) >= want ? 0 : (!dbl || ntiles(CF::small) >= want) ? 1 : 2;
+        const auto go = [&](auto kc) -> int {
+            constexpr int K = decltype(kc)::value;
+            if (cls == 0) return launch_klim_t<T, CF::big, K, V>(p);
+            if constexpr (dbl) {
+                if (cls == 2) return launch_klim_t<T, tiny, K, V>(p);
+            }
+            return launch_klim_t<T, CF::small, K, V>(p);
+        };
+        switch (klim) {
+        case 1: return go(std::integral_constant<int, 1>());
+        case 2: return go(std::integral_constant<int, 2>());
+        case 3: return go(std::integral_constant<int, 3>());
+        case 4: return go(std::integral_constant<int, 4>());
+        }
+        G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "k-limited product: mode %d", klim);
+    };
+    return vec ? by_cfg(std::true_type()) : by_cfg(std::false_type());
 }
 int launch_gemm_klim(const GemmCall &c, int klim) {
     if (c.tA || c.tB || c.count != 1) G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "k-limited product: layout tA=%d tB=%d, batch %d", c.tA, c.tB, c.count);

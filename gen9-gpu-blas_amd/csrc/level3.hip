@@ -21,6 +21,7 @@
 // Products of the element type round as a GEMM does; the TRMM copy pass and SYMM's explicit matrix add no rounding
 // (they copy elements of the element type).
 #include "internal.h"
+#include <algorithm>
 #include <type_traits>
 
 namespace g9 {
@@ -113,6 +114,15 @@ __global__ void __launch_bounds__(256) trsm_y_kernel(const T *B, ll ldb, T *Y, i
         Y[e] = (T)(alpha * (S)b);
     }
 }
+// B rows (byte stride ldb_bytes) = the rows of Z (n rows of cpr 16-byte chunks, contiguous): the solution of a left
+// solve in its own order, 16 bytes per lane (both row strides and both pointers 16-byte aligned; the caller checks).
+__global__ void __launch_bounds__(256) trsm_store_rows16_kernel(const uint4 *Z, char *B, ll ldb_bytes, int n, int cpr) {
+    const ll tot = (ll)n * cpr;
+    for (ll e = blockIdx.x * 256ll + threadIdx.x; e < tot; e += (ll)gridDim.x * 256) {
+        const ll i = e / cpr, c = e - i * cpr;
+        *(uint4 *)(B + i * ldb_bytes + c * 16) = Z[e];
+    }
+}
 // B = X from Y (inverse of trsm_y_kernel's index map, without alpha).
 template <class T>
 __global__ void __launch_bounds__(256) trsm_store_kernel(const T *Y, T *B, ll ldb, int n, int m, int left, int rev) {
@@ -125,13 +135,15 @@ __global__ void __launch_bounds__(256) trsm_store_kernel(const T *Y, T *B, ll ld
 }
 
 constexpr int TRSM_NB = 128;
+// rows of a leaf (an inverted diagonal block applied by one product) of the FP32 / FP64 solve
+constexpr int TRSM_LEAF = 512;
 // Inverse of the diagonal block bi of L (rows and columns r0 .. r0+b-1, b ≤ TRSM_NB, in the leaf p = r0 / lb of lb
 // rows whose element (i, j) is at L[p·bstride + i·ld + j]; the block's entries above the diagonal are read as zeros,
 // and its diagonal as ones when unit),
-// in FP64, stored in the element type into the inverted diagonal block of lb rows (lb = TRSM_NB or 2·TRSM_NB) that
-// holds it: leaf p = r0 / lb at Inv + p·lb², row stride lb, at row and column offset o = r0 − p·lb. The first
-// 128-block of a leaf also writes zeros right of itself (columns b .. lb−1 of its rows), the leaf's upper-right
-// quadrant. The block is split into 32×32 sub-blocks: the four diagonal sub-blocks are inverted first, thread j
+// in FP64, stored in the element type into the inverted diagonal block of lb rows (lb a multiple of TRSM_NB) that
+// holds it: leaf p = r0 / lb at Inv + p·istride, row stride lb, at row and column offset o = r0 − p·lb. Each block
+// also writes zeros right of itself up to the end of its leaf (or column n), so that everything above the leaf's
+// diagonal is zero once the parts below its diagonal blocks are composed. The block is split into 32×32 sub-blocks: the four diagonal sub-blocks are inverted first, thread j
 // forming column j of its sub-block by substitution (X[j][j] = 1 / L[j][j], X[i][j] = −(Σ_{k=j}^{i-1}
 // L[i][k]·X[k][j]) / L[i][i]) from copies of those sub-blocks in LDS (placed, with one round of loads, in regions of
 // X that are filled only later); the off-diagonal sub-blocks then follow by distance d from the diagonal,
@@ -140,7 +152,8 @@ constexpr int TRSM_NB = 128;
 // 8128 FMAs long); the sums differ from plain column substitution in FP64 rounding only. X and the sums live in LDS
 // (154 KiB).
 template <class T>
-__global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, ll ld, ll bstride, int n, T *Inv, int lb, int unit) {
+__global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, ll ld, ll bstride, int n, T *Inv, int lb, ll istride,
+                                                        int unit) {
     constexpr int S = 32, NSB = TRSM_NB / S;
     static_assert(NSB == 4, "four diagonal sub-blocks, staged in the lower regions (1,0), (2,0), (3,0), (3,1)");
     __shared__ double X[TRSM_NB][TRSM_NB + 1];
@@ -247,18 +260,19 @@ __global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, ll ld, ll bst
     phase(std::integral_constant<int, 1>());
     phase(std::integral_constant<int, 2>());
     phase(std::integral_constant<int, 3>());
-    const int p = r0 / lb, o = r0 - p * lb, w = o == 0 ? lb : b;
-    T *out = Inv + (ll)p * lb * lb + (ll)o * lb + o;
-    // thread t writes column t (w ≤ 256) of the block's rows, 8 rows' LDS reads at a time
-    const int jc = min(t, TRSM_NB - 1);
-    if (t < w) {
+    // the block's rows from its diagonal to the end of its leaf: the inverse, then zeros (w ≤ lb columns)
+    const int p = r0 / lb, o = r0 - p * lb, w = min(lb, n - p * lb) - o;
+    T *out = Inv + (ll)p * istride + (ll)o * lb + o;
+    // thread t writes columns t, t + 256, ... of the block's rows, 8 rows' LDS reads at a time
+    for (int c = t; c < w; c += 256) {
+        const int jc = min(c, TRSM_NB - 1);
         for (int i0 = 0; i0 < b; i0 += 8) {
             double v[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) v[u] = X[min(i0 + u, TRSM_NB - 1)][jc];
 #pragma unroll
             for (int u = 0; u < 8; u++)
-                if (i0 + u < b) out[(ll)(i0 + u) * lb + t] = t < b ? (T)v[u] : T(0);
+                if (i0 + u < b) out[(ll)(i0 + u) * lb + c] = c < b ? (T)v[u] : T(0);
         }
     }
 }
@@ -285,10 +299,11 @@ static int dgemm_dev(int type, int tA, int tB, int M, int N, int K, double alpha
 
 // Blocked forward substitution L·X = alpha·Y (L n×n lower, Y and X n×m, row strides ldl, ldy and m; alpha is applied
 // by the first product that touches each block of rows of Y, or is 1 when Y already holds alpha·R) over diagonal blocks of lb
-// rows (256 for FP32 / FP64, 128 for FP16), by recursive halving: the first half of a block range is solved, one GEMM
-// then subtracts its contribution from the right-hand side of the second half, Y[i1..i2) -= L[i1..i2, i0..i1)·X[i0..i1),
-// and the second half is solved. A single block is X_i = inv(L_ii)·Y_i with the block's inverse (128-row inverses
-// computed in FP64; a 256-row inverse composed from two of them). The reference updates one block row at a time,
+// rows (TRSM_LEAF for FP32 / FP64, 128 for FP16), by recursive halving: the first half of a block range is solved, one
+// GEMM then subtracts its contribution from the right-hand side of the second half, Y[i1..i2) -= L[i1..i2, i0..i1)·
+// X[i0..i1), and the second half is solved. A single block is X_i = inv(L_ii)·Y_i with the block's inverse (128-row
+// inverses computed in FP64, larger ones composed from them; element (i, j) of the inverses at Iv[i·lb + j]), a product
+// whose tiles take only the k range where the lower-triangular inverse is non-zero. The reference updates one block row at a time,
 // Y_i -= L[i, <i]·X[<i] (level3.c:127-215): the same products, grouped so that most of the flops run in a few large
 // GEMMs instead of n/128 products of 128 rows; the sums differ only in rounding (each GEMM rounds once).
 struct TrsmSolve {
@@ -301,8 +316,16 @@ struct TrsmSolve {
         if (nb == 1) {
             const int i0 = b0 * lb, b = n - i0 < lb ? n - i0 : lb;
             // only leaf 0's rows of Y are still unscaled when it is solved
-            return dgemm_dev(type, 0, 0, b, m, b, b0 == 0 ? alpha : 1.0, Iv + (ll)b0 * lb * lb * es, lb,
-                             Y + (ll)i0 * ldy * es, ldy, 0.0, X + (ll)i0 * m * es, m);
+            GemmCall g;
+            g.type = type;
+            g.tA = g.tB = 0;
+            g.M = b; g.N = m; g.K = b;
+            g.count = 1;
+            g.alpha = b0 == 0 ? alpha : 1.0; g.beta = 0.0;
+            g.A = Iv + (ll)i0 * (lb + 1) * es; g.lda = lb; g.sA = 0;
+            g.B = Y + (ll)i0 * ldy * es; g.ldb = ldy; g.sB = 0;
+            g.C = X + (ll)i0 * m * es; g.ldc = m; g.sC = 0;
+            return lb > TRSM_NB ? launch_gemm_klim(g, 1) : launch_gemm(g);
         }
         const int h = nb / 2;
         G9_TRY(solve(b0, h));
@@ -351,16 +374,16 @@ static int tri_product(int type, int lower, int trans, int N, int K, double alph
 
 // The 128-row diagonal blocks of `count` / (lb / 128) lower-triangular leaves of lb rows for the level-2 solves: leaf
 // p's element (i, j) at L[p·bstride + i·ld + j] (es 4: float, 8: double); inverses into Inv as trsm_inv_kernel
-// places them (leaf p at Inv + p·lb², row stride lb, zeros above its first block's inverse).
+// places them (leaf p at Inv + p·lb², row stride lb, zeros right of each block's inverse to the end of its leaf).
 int launch_tri_inverse(int es, const void *L, long long ld, long long bstride, int count, void *Inv, int lb) {
     using namespace l3;
     const int n = count * TRSM_NB;
     if (es == 8)
         hipLaunchKernelGGL((trsm_inv_kernel<double>), dim3(count), dim3(256), 0, stream, (const double *)L, (ll)ld,
-                           (ll)bstride, n, (double *)Inv, lb, 0);
+                           (ll)bstride, n, (double *)Inv, lb, (ll)lb * lb, 0);
     else
         hipLaunchKernelGGL((trsm_inv_kernel<float>), dim3(count), dim3(256), 0, stream, (const float *)L, (ll)ld,
-                           (ll)bstride, n, (float *)Inv, lb, 0);
+                           (ll)bstride, n, (float *)Inv, lb, (ll)lb * lb, 0);
     G9_HIP(hipGetLastError());
     return 0;
 }
@@ -515,9 +538,9 @@ int gen9blas_trsm(int type, int side, int uplo, int transA, int diag, int M, int
     // L·Y = alpha·R: op'(A) = left ? op(A) : op(A)ᵀ; lower when the triangle of A, transposed or not, is lower
     const int tr = left ? transA != 0 : transA == 0;
     const int lower = (uplo == GEN9BLAS_LOWER) != (tr != 0), rev = !lower;
-    // Leaves of 256 rows for FP32 / FP64: each leaf inverse is composed from two 128-row FP64 inverses (below); FP16
-    // keeps 128-row leaves (the composition would round once more in FP16)
-    const int nbl = (n + TRSM_NB - 1) / TRSM_NB, lb = es >= 4 ? 2 * TRSM_NB : TRSM_NB, nleaf = (n + lb - 1) / lb;
+    // Leaves of TRSM_LEAF rows for FP32 / FP64: each leaf inverse is composed from the 128-row FP64 inverses (below);
+    // FP16 keeps 128-row leaves (the composition would round once more in FP16)
+    const int nbl = (n + TRSM_NB - 1) / TRSM_NB, lb = es >= 4 ? TRSM_LEAF : TRSM_NB, nleaf = (n + lb - 1) / lb;
     // A left solve with A lower and not transposed reads both operands where they lie: every product below reads L
     // strictly below its diagonal blocks, the block inversion masks the rest of A itself, B is the right-hand side
     // updated in place (alpha applied by the first product that touches each block of rows), and only the solution
@@ -535,9 +558,13 @@ int gen9blas_trsm(int type, int side, int uplo, int transA, int diag, int M, int
         G9_TRY(scratch(SLOT_T, (size_t)n * n * es, &Ld));
         G9_TRY(scratch(SLOT_X, (size_t)n * m * es, &Yd));
     }
-    // the leaf inverses, then (lb > TRSM_NB) the products C·I1 of the composition, TRSM_NB² per leaf
-    const size_t inv_bytes = (size_t)nleaf * lb * lb * es;
-    G9_TRY(scratch(SLOT_Y, inv_bytes + (lb > TRSM_NB ? (size_t)nleaf * TRSM_NB * TRSM_NB * es : 0), &Iv));
+    // the leaf inverses (leaf p at Iv + p·lb·(lb + 1), row stride lb: element (i, j) of a leaf's rows and columns at
+    // Iv[i·lb + j], and a sub-leaf at row s starts at Iv + s·(lb + 1) whatever leaf holds it), then (lb > TRSM_NB)
+    // the products C·inv(J1) of the compositions, at most (n / 2h)·h² for a level of h-row halves, h < lb
+    const size_t inv_bytes = ((size_t)n * (lb + 1) * es + 255) & ~(size_t)255;
+    size_t tm_elems = 0;
+    for (ll h = TRSM_NB; h < lb; h *= 2) tm_elems = std::max<size_t>(tm_elems, (size_t)(std::max<ll>(n / (2 * h), 1) * h * h));
+    G9_TRY(scratch(SLOT_Y, inv_bytes + tm_elems * es, &Iv));
     G9_TRY(scratch(SLOT_W, (size_t)n * m * es, &Zd));
     G9_TRY(by_es(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
@@ -549,35 +576,44 @@ int gen9blas_trsm(int type, int side, int uplo, int transA, int diag, int M, int
                                ops[1].ld, (T *)Yd, n, m, left, rev, (S)alpha);
         }
         hipLaunchKernelGGL((trsm_inv_kernel<T>), dim3(nbl), dim3(256), 0, stream, (const T *)Ld, ldl, (ll)lb * (ldl + 1),
-                           n, (T *)Iv, lb, diag != 0);
+                           n, (T *)Iv, lb, (ll)lb * (lb + 1), diag != 0);
         G9_HIP(hipGetLastError());
         return 0;
     }));
-    if (lb > TRSM_NB) {
-        // A leaf [I1 0; C I2]⁻¹ = [inv(I1) 0; −inv(I2)·C·inv(I1) inv(I2)]: the kernel above left inv(I1), inv(I2) and
-        // the zero quadrant; two GEMMs form the lower-left quadrant, batched over the leaves with two whole halves
-        // (leaf p: C at L + p·lb·(ldl+1) + TRSM_NB·ldl, inv(I1) at Inv_p, inv(I2) at Inv_p + TRSM_NB·(lb+1)), then once
-        // for a last leaf whose second half has b2 < TRSM_NB rows.
-        const ll NB = TRSM_NB;
+    // A block [J1 0; C J2]⁻¹ = [inv(J1) 0; −inv(J2)·C·inv(J1) inv(J2)], level by level from halves of h = 128 rows up
+    // to halves of lb / 2: the kernel above left the 128-row inverses and the zeros above the diagonal, each level's
+    // two GEMMs form the lower-left quadrants, batched over the whole blocks of 2h rows (block at row s: C at
+    // L + (s + h)·ldl + s, inv(J1) at Iv + s·(lb + 1), inv(J2) at Iv + (s + h)·(lb + 1), the quadrant at
+    // Iv + (s + h)·lb + s), then once for a last block whose second half has b2 < h rows.
+    for (ll h = TRSM_NB; h < lb; h *= 2) {
         const char *L0 = (const char *)Ld;
         char *I0 = (char *)Iv, *Tm = I0 + inv_bytes;
-        const int full = n / lb;
-        G9_TRY(dgemm_dev_batched(type, 0, 0, TRSM_NB, TRSM_NB, TRSM_NB, 1.0, L0 + NB * ldl * es, ldl, (ll)lb * (ldl + 1), I0,
-                                 lb, (ll)lb * lb, 0.0, Tm, NB, NB * NB, full));
-        G9_TRY(dgemm_dev_batched(type, 0, 0, TRSM_NB, TRSM_NB, TRSM_NB, -1.0, I0 + NB * (lb + 1) * es, lb, (ll)lb * lb, Tm,
-                                 NB, NB * NB, 0.0, I0 + NB * lb * es, lb, (ll)lb * lb, full));
-        const ll i0 = (ll)full * lb;
-        const int b2 = n - (int)i0 - TRSM_NB;
+        const ll st = 2 * h, ils = ldl + 1, iis = (ll)lb + 1;
+        const int full = (int)(n / st);
+        G9_TRY(dgemm_dev_batched(type, 0, 0, (int)h, (int)h, (int)h, 1.0, L0 + h * ldl * es, ldl, st * ils, I0, lb,
+                                 st * iis, 0.0, Tm, h, h * h, full));
+        G9_TRY(dgemm_dev_batched(type, 0, 0, (int)h, (int)h, (int)h, -1.0, I0 + h * iis * es, lb, st * iis, Tm, h, h * h,
+                                 0.0, I0 + h * lb * es, lb, st * iis, full));
+        const ll s0 = (ll)full * st;
+        const int b2 = n - (int)(s0 + h);
         if (b2 > 0) {
-            char *Ip = I0 + i0 * lb * es;
-            G9_TRY(dgemm_dev(type, 0, 0, b2, TRSM_NB, TRSM_NB, 1.0, L0 + ((i0 + NB) * ldl + i0) * es, ldl, Ip, lb, 0.0, Tm,
-                             NB));
-            G9_TRY(dgemm_dev(type, 0, 0, b2, TRSM_NB, b2, -1.0, Ip + NB * (lb + 1) * es, lb, Tm, NB, 0.0, Ip + NB * lb * es, lb));
+            G9_TRY(dgemm_dev(type, 0, 0, b2, (int)h, (int)h, 1.0, L0 + ((s0 + h) * ldl + s0) * es, ldl, I0 + s0 * iis * es,
+                             lb, 0.0, Tm, h));
+            G9_TRY(dgemm_dev(type, 0, 0, b2, (int)h, b2, -1.0, I0 + (s0 + h) * iis * es, lb, Tm, h, 0.0,
+                             I0 + ((s0 + h) * lb + s0) * es, lb));
         }
     }
     TrsmSolve rec{type, n, m, es, lb, (const char *)Ld, (const char *)Iv, (char *)Yd, (char *)Zd, ldl, ldy,
                   direct ? alpha : 1.0};
     G9_TRY(rec.solve(0, nleaf));
+    const ll row_bytes = (ll)m * es, ldb_bytes = ops[1].ld * es;
+    if (left && !rev && row_bytes % 16 == 0 && ldb_bytes % 16 == 0 && (uintptr_t)ops[1].dev % 16 == 0) {
+        const int cpr = (int)(row_bytes / 16);
+        hipLaunchKernelGGL(trsm_store_rows16_kernel, dim3(grid_for((ll)n * cpr)), dim3(256), 0, stream,
+                           (const uint4 *)Zd, (char *)ops[1].dev, ldb_bytes, n, cpr);
+        G9_HIP(hipGetLastError());
+        return finish(ops, 2);
+    }
     G9_TRY(by_es(es, [&](auto *tag) -> int {
         using T = std::remove_pointer_t<decltype(tag)>;
         hipLaunchKernelGGL((trsm_store_kernel<T>), dim3(grid_for((ll)n * m)), dim3(256), 0, stream, (const T *)Zd,

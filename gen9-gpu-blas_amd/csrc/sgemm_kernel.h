@@ -30,7 +30,7 @@
 // - KLIM: each tile's k range is cut to where a triangular operand is non-zero (NN, TRMM on the explicit triangular
 //   matrix): 1 op(A) lower, k < m0 + BM; 2 op(A) upper, k >= m0; 3 op(B) lower, k >= n0; 4 op(B) upper,
 //   k < n0 + BN. Tiles are dispatched longest range first, without the XCD remap (every XCD gets long and short
-//   tiles alike).
+//   tiles alike); when every tile is resident at once, two per CU, the second half of the order is reversed.
 // MSKIP: rows m < p.m_skip of C are computed but not stored (the edge strip of a product shifted up onto rows that
 // the interior tiles already wrote: every load stays inside A, and no C element is written twice).
 #pragma once
@@ -52,6 +52,7 @@ struct Params {
     int M, N, K, tiles_m, tiles_n;
     float alpha, beta;
     int m_skip = 0;   // MSKIP: leading rows of C not stored
+    int kpair = 0;    // KLIM: the second half of the dispatch order reversed (see the tile mapping)
 };
 
 // Fragment reads of one operand for a wave's TT tiles of 32 rows (m or n) from wave row w0 (a multiple of 32): per
@@ -117,6 +118,12 @@ __global__ void __launch_bounds__(WM *WN * 64) sgemm_kernel(Params p) {
 
     int bid = blockIdx.x, m0, n0;
     if constexpr (KLIM != 0) {
+        // kpair (all tiles resident at once, two per CU): workgroups i and i + T/2 share a CU, and the second half
+        // takes the ranks in reverse, so that each CU pairs a long range with a short one
+        if (p.kpair) {
+            const int nt = p.tiles_m * p.tiles_n, h = nt / 2;
+            if (bid >= h) bid = nt - 1 - (bid - h);
+        }
         if constexpr (KLIM <= 2) {   // the range depends on the tile row
             const int tr = bid / p.tiles_n;
             m0 = (KLIM == 1 ? p.tiles_m - 1 - tr : tr) * BM;

@@ -103,8 +103,8 @@ def test_trsm(g9, kind, dt, acc, tol):
         for uplo in "LU":
             for ta in (False, True):
                 for dg in (False, True):
-                    for (M, N) in [(40, 30), (300, 200), (70, 600), (400, 400)]:   # n = 400: a last 256-row
-                        # leaf whose second half has 16 rows
+                    for (M, N) in [(40, 30), (300, 200), (70, 600), (400, 400)]:   # n = 400: one partial leaf, its
+                        # 256-row inverse composed with a last 16 rows, then with a last 144
                         n = M if side == "L" else N
                         A = rng.uniform(-1, 1, (n, n)).astype(np.float32)
                         A[np.diag_indices(n)] = n if not dg else 0.5
@@ -124,13 +124,15 @@ def test_trsm(g9, kind, dt, acc, tol):
 
 
 @pytest.mark.parametrize("kind,dt,acc,tol", TRSM_TYPES, ids=[t[0] for t in TRSM_TYPES])
-@pytest.mark.parametrize("n", [1300, 2048])
+@pytest.mark.parametrize("n", [1300, 1450, 2048])
 def test_trsm_left_lower_in_place(g9, torch_dev, kind, dt, acc, tol, n):
     """The left, lower, non-transposed solve reads A and B where they lie: B is updated in place as the right-hand
     side, alpha is applied by the first product touching each block of rows, the FP64 block inversion masks A's other
     triangle and (unit) diagonal itself. A's upper triangle (and a unit diagonal) hold huge values that must not be
     read; B is a column slice of a wider array (row stride above N) whose other columns must survive; alpha 0.5 and
-    0 (X = 0), on host and device operands. n = 1300: 6 leaves (a partial one), n = 2048: 8 whole ones."""
+    0 (X = 0), on host and device operands. FP32 / FP64 leaves of 512 rows: n = 1300 ends in a partial leaf of 276 rows
+    (its inverse composed from 256 and 20 rows), n = 1450 in one of 426 (a 128 + 42-row block composed first), n = 2048
+    has 4 whole leaves; FP16 leaves have 128 rows."""
     torch = torch_dev
     rng = np.random.default_rng(n)
     big = {np.float16: 6e4, np.float32: 1e30, np.float64: 1e300}[dt]
@@ -145,35 +147,37 @@ def test_trsm_left_lower_in_place(g9, torch_dev, kind, dt, acc, tol, n):
         Ag[np.triu_indices(n, 1)] = big
         if dg:
             Ag[np.diag_indices(n)] = big
-        wide = rng.uniform(-1, 1, (n, m + 7)).astype(dt)
-        code = {"H": 0, "S": 1, "HS": 2, "D": 3}[kind]
-        es = np.dtype(dt).itemsize
-        d, p = ctypes.c_double, ctypes.c_void_p
-        for alpha in (0.5, 0.0):
-            for where in ("host", "device"):
-                # the C ABI on B = columns 3 .. 3 + m of the wide array (row stride m + 7)
-                if where == "host":
-                    W = wide.copy()
-                    rc = g9._lib.gen9blas_trsm(code, 0, 0, 0, int(dg), n, m, d(alpha), p(Ag.ctypes.data), n,
-                                               p(W.ctypes.data + 3 * es), m + 7)
-                else:
-                    Wd = torch.from_numpy(wide.copy()).cuda()
-                    Ad = torch.from_numpy(Ag).cuda()
-                    rc = g9._lib.gen9blas_trsm(code, 0, 0, 0, int(dg), n, m, d(alpha), p(Ad.data_ptr()), n,
-                                               p(Wd.data_ptr() + 3 * es), m + 7)
-                    torch.cuda.synchronize()
-                    W = Wd.cpu().numpy()
-                assert rc == 0, g9._lib.gen9blas_error()
-                tag = f"trsm LLN {kind} n={n} diag={dg} alpha={alpha} {where}"
-                assert np.array_equal(W[:, :3], wide[:, :3]) and np.array_equal(W[:, 3 + m:], wide[:, 3 + m:]), \
-                    tag + ": columns outside B changed"
-                X = f64(W[:, 3:3 + m])
-                if alpha == 0.0:
-                    assert np.array_equal(X, np.zeros_like(X)), tag
-                else:
-                    Xr = np.linalg.solve(T, alpha * f64(wide[:, 3:3 + m]))
-                    e = np.abs(X - Xr).max() / np.abs(Xr).max()
-                    assert e <= tol, f"{tag}: {e:.1e}"
+        for off, pad in ((3, 7), (4, 8)):
+            # B = columns off .. off + m of a wider array (row stride m + pad): off 3 misaligns B's rows, off 4 with
+            # pad 8 keeps FP32 / FP64 rows 16-byte aligned (the solution is then stored 16 bytes per lane)
+            wide = rng.uniform(-1, 1, (n, m + pad)).astype(dt)
+            code = {"H": 0, "S": 1, "HS": 2, "D": 3}[kind]
+            es = np.dtype(dt).itemsize
+            d, p = ctypes.c_double, ctypes.c_void_p
+            for alpha in (0.5, 0.0):
+                for where in ("host", "device"):
+                    if where == "host":
+                        W = wide.copy()
+                        rc = g9._lib.gen9blas_trsm(code, 0, 0, 0, int(dg), n, m, d(alpha), p(Ag.ctypes.data), n,
+                                                   p(W.ctypes.data + off * es), m + pad)
+                    else:
+                        Wd = torch.from_numpy(wide.copy()).cuda()
+                        Ad = torch.from_numpy(Ag).cuda()
+                        rc = g9._lib.gen9blas_trsm(code, 0, 0, 0, int(dg), n, m, d(alpha), p(Ad.data_ptr()), n,
+                                                   p(Wd.data_ptr() + off * es), m + pad)
+                        torch.cuda.synchronize()
+                        W = Wd.cpu().numpy()
+                    assert rc == 0, g9._lib.gen9blas_error()
+                    tag = f"trsm LLN {kind} n={n} diag={dg} alpha={alpha} {where} B at column {off}"
+                    assert np.array_equal(W[:, :off], wide[:, :off]) and \
+                        np.array_equal(W[:, off + m:], wide[:, off + m:]), tag + ": columns outside B changed"
+                    X = f64(W[:, off:off + m])
+                    if alpha == 0.0:
+                        assert np.array_equal(X, np.zeros_like(X)), tag
+                    else:
+                        Xr = np.linalg.solve(T, alpha * f64(wide[:, off:off + m]))
+                        e = np.abs(X - Xr).max() / np.abs(Xr).max()
+                        assert e <= tol, f"{tag}: {e:.1e}"
 
 
 def test_level3_device_operands(g9, torch_dev):
