@@ -257,6 +257,44 @@ def test_trmm_fp32_whole_tiles(g9, M, N, full):
                     assert np.array_equal(f64(W), 1.5 * P), f"trmm {side}{uplo} tA={ta} diag={dg}"
 
 
+@pytest.mark.parametrize("kind,M,N", [("S", 512, 4096), ("S", 500, 4000), ("D", 512, 4096)])
+def test_trmm_paired_k_limited_tiles(g9, kind, M, N):
+    """k-limited products with more tiles than CUs but at most two per CU, all resident at once, take the paired
+    dispatch order (the second half of the longest-first order reversed): FP32 512×4096 on the whole-tile kernel's
+    64×64 tiles (512), 500×4000 on the general kernel's (504), FP64 512×4096 on its 64×64 tiles (512); both sides
+    and triangles (the four k-limit modes), small integers, so every result is exact and a tile computed twice or
+    not at all shows up."""
+    dt = np.float32 if kind == "S" else np.float64
+    rng = np.random.default_rng(8)
+    for side in "LR":
+        for uplo in "LU":
+            m, n_ = (M, N) if side == "L" else (N, M)
+            n = m if side == "L" else n_
+            A = rng.integers(-2, 3, (n, n)).astype(dt)
+            B = rng.integers(-2, 3, (m, n_)).astype(dt)
+            T = np.tril(f64(A)) if uplo == "L" else np.triu(f64(A))
+            W = g9.trmm(A, B, side, uplo, False, False, 1.5)
+            P = T @ f64(B) if side == "L" else f64(B) @ T
+            assert np.array_equal(f64(W), 1.5 * P), f"trmm {kind} {side}{uplo} {m}x{n_}"
+
+
+@pytest.mark.parametrize("kind,dt,tol", [("S", np.float32, 1e-4), ("D", np.float64, 1e-12)])
+def test_trsm_paired_leaf_products(g9, kind, dt, tol):
+    """TRSM of order 1024 with 4096 right-hand sides: its two 512-row leaves are applied by k-limited products of
+    512×4096 (512 tiles of 64×64, the paired dispatch order), for every side and triangle against float64."""
+    rng = np.random.default_rng(9)
+    n, m = 1024, 4096
+    for uplo in "LU":
+        A = (rng.uniform(-1, 1, (n, n)) / n).astype(dt)
+        A[np.diag_indices(n)] = 1.0 + rng.uniform(0, 1, n)
+        B = rng.uniform(-1, 1, (n, m)).astype(dt)
+        T = np.tril(f64(A)) if uplo == "L" else np.triu(f64(A))
+        X = f64(g9.trsm(A, B, "L", uplo, False, False, 0.5))
+        Xr = np.linalg.solve(T, 0.5 * f64(B))
+        e = np.abs(X - Xr).max() / np.abs(Xr).max()
+        assert e <= tol, f"trsm {kind} L{uplo} {n}x{m}: {e:.1e}"
+
+
 def _l3_cases(seed, count):
     """Seeded random level-3 calls: operation, type, side / triangle / transpose / unit diagonal, and dimensions that
     are small (1-79), multiples of 64 (the whole-tile classes of the GEMMs underneath), within 3 of one, or 80-599."""
