@@ -117,9 +117,13 @@ static int launch_layout(const GemmParams<typename Mma<T>::Sum> &p, int count) {
         // triangular solve's block products) 8.6 → 15.8. FP32 above num_cus tiles loses (n = 1280: 74 → 70), FP64
         // does not. Other FP64 shapes measured at n = 1024 / 1536 against 53.6 / 48.1: four k groups of 2×2 waves
         // 54.0 / 45.1, four of one 64×64 wave 41.9 / 34.9, two of 1×2 waves 48.7, four of 2×1 waves 51.1.
+        // A batch (count > 1) cannot split K, so it takes these tiles from num_cus / 4 of them: FP64 128³ × 16 (the
+        // triangular solve's 256-row compositions) 12.7 → 8.2 µs on 64 workgroups of 8 waves instead of 32 of 64×128,
+        // DTRSM n = 4096 1.458 → 1.443 ms.
         if constexpr (sizeof(T) >= 4) {
             const long long t64 = (long long)((p.M + 63) / 64) * ((p.N + 63) / 64) * count;
-            if (splitk_forced() < 0 && t64 * 2 >= num_cus && (sizeof(T) == 8 || t64 <= num_cus))
+            const long long need = count > 1 ? (num_cus + 3) / 4 : (num_cus + 1) / 2;
+            if (splitk_forced() < 0 && t64 >= need && (sizeof(T) == 8 || t64 <= num_cus))
                 return launch_t<T, TileCfg{64, 64, 2, 2}, AK, BKC, VEC, 2>(p, count);
         }
         return launch_t<T, CF::small, AK, BKC, VEC>(p, count);
