@@ -147,17 +147,15 @@ constexpr int TRSM_LEAF = 512;
 // forming column j of its sub-block by substitution (X[j][j] = 1 / L[j][j], X[i][j] = −(Σ_{k=j}^{i-1}
 // L[i][k]·X[k][j]) / L[i][i]) from copies of those sub-blocks in LDS (placed, with one round of loads, in regions of
 // X that are filled only later); the off-diagonal sub-blocks then follow by distance d from the diagonal,
-// X_ij = −inv(L_ii)·Σ_{k=j}^{i-1} L_ik·X_kj (i − j = d): for the sum a thread takes one row of L_i,j..i−1 (all
-// d·32 loads in flight) and 4 columns of X; for the product with inv(L_ii) a 4×4 tile of the result. The work per thread is balanced (a single column chain of the whole block would be
-// 8128 FMAs long); the sums differ from plain column substitution in FP64 rounding only. X and the sums live in LDS
-// (154 KiB).
+// X_ij = −inv(L_ii)·Σ_{k=j}^{i-1} L_ik·X_kj (i − j = d), both products on the FP64 matrix cores (below). No thread runs
+// a column chain of the whole block (8128 FMAs); the sums differ from plain column substitution in FP64 rounding
+// only. X lives in LDS (132 KiB).
 template <class T>
 __global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, ll ld, ll bstride, int n, T *Inv, int lb, ll istride,
                                                         int unit) {
     constexpr int S = 32, NSB = TRSM_NB / S;
     static_assert(NSB == 4, "four diagonal sub-blocks, staged in the lower regions (1,0), (2,0), (3,0), (3,1)");
     __shared__ double X[TRSM_NB][TRSM_NB + 1];
-    __shared__ double Sb[NSB - 1][S][S + 1];
     const int bi = blockIdx.x, r0 = bi * TRSM_NB, b = min(TRSM_NB, n - r0), t = threadIdx.x;
     const T *Lb = L + (ll)(r0 / lb) * bstride + (ll)(r0 % lb) * (ld + 1);   // element (i, j) of the block at Lb[i·ld + j]
     // region of X holding the copy of diagonal sub-block s of L until phase d ≥ 1 overwrites it
@@ -203,63 +201,61 @@ __global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, ll ld, ll bst
         for (int i = 0; i < S; i++) X[sb * S + i][j] = x[i];
     }
     __syncthreads();
-    const auto phase = [&](auto dc) {
-        constexpr int d = decltype(dc)::value, nblk = NSB - d, KW = d * S;   // sub-blocks (j + d, j), j < nblk
-        // item it of this thread: sub-block j, row rr, columns cc0 .. cc0 + 3; all items' loads in flight first
-        // (rows and columns clamped into the block: a valid row's columns j·32 .. row − 1 are all below b)
-        T lv[nblk][KW];
+    // Off-diagonal sub-blocks by distance d from the diagonal, on the matrix cores (v_mfma_f64_16x16x4f64: lane l
+    // supplies A[l % 16][k = l / 16] and B[k = l / 16][l % 16]; accumulator r of lane l holds D[4r + l / 16][l % 16]).
+    // Task (j, J) of level d forms columns j·32 + 16J .. + 15 of X_(i, j), i = j + d, as two 16-row halves:
+    // S = Σ_k L_(i, k)·X_(k, j) over the d·32 columns k of blocks j .. i − 1 (d·8 steps; L from global memory, zero
+    // outside the block, X from LDS), then X_(i, j) = −inv(L_(i, i))·S with S taken straight from the accumulators:
+    // accumulator r of half kh holds rows 16kh + 4r + l / 16 of S, which is the second operand's k of that step. A
+    // level's tasks read only blocks of earlier levels and write distinct blocks; they go round robin over the waves.
+    typedef double f64x4 __attribute__((ext_vector_type(4)));
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6), lr = t & 15, lg = (t & 63) >> 4;
+    const auto level = [&](auto dc) {
+        constexpr int d = decltype(dc)::value, nblk = NSB - d, KS4 = d * S / 4, NTASK = 2 * nblk;
+        for (int task = wv; task < NTASK; task += 4) {
+            const int j = task >> 1, J = task & 1, i = j + d, c0 = j * S + 16 * J;
+            // every load of L in flight first, from addresses clamped into the block (values outside it are not used)
+            T lv[2][KS4];
 #pragma unroll
-        for (int it = 0; it < nblk; it++) {
-            const int q = it * 256 + t, j = q / (S * S / 4), rr = (q / (S / 4)) % S;
-            const T *li = Lb + (ll)min((j + d) * S + rr, b - 1) * ld;
+            for (int h = 0; h < 2; h++) {
+                const T *li = Lb + (ll)min(i * S + 16 * h + lr, b - 1) * ld;
 #pragma unroll
-            for (int u = 0; u < KW; u++) lv[it][u] = li[min(j * S + u, b - 1)];
-        }
-#pragma unroll
-        for (int it = 0; it < nblk; it++) {
-            const int q = it * 256 + t, j = q / (S * S / 4), rr = (q / (S / 4)) % S, cc0 = 4 * (q % (S / 4));
-            const int row = (j + d) * S + rr, col0 = j * S + cc0;
-            double sm[4] = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-            for (int u = 0; u < KW; u++)
-#pragma unroll
-                for (int m = 0; m < 4; m++) sm[m] = __builtin_fma((double)lv[it][u], X[j * S + u][col0 + m], sm[m]);
-#pragma unroll
-            for (int m = 0; m < 4; m++) Sb[j][rr][cc0 + m] = row < b && col0 + m < b ? sm[m] : 0.0;
-        }
-        __syncthreads();
-        // X_(j+d, j) = −inv(L_(j+d, j+d))·Sb_j: 64 threads per sub-block j, each a 4×4 tile (rows 4·tr.., columns
-        // 4·tc..), 8 LDS reads per 16 FMAs; each element's sum runs over m in ascending order
-        {
-            const int j = t / 64, tr = (t / 8) % 8, tc = t % 8, i = j + d;
-            if (j < nblk) {
-                double acc[4][4] = {};
-#pragma unroll 4
-                for (int m = 0; m < S; m++) {
-                    double av[4], bv[4];
-#pragma unroll
-                    for (int r = 0; r < 4; r++) av[r] = X[i * S + 4 * tr + r][i * S + m];
-#pragma unroll
-                    for (int c = 0; c < 4; c++) bv[c] = Sb[j][m][4 * tc + c];
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-#pragma unroll
-                        for (int c = 0; c < 4; c++) acc[r][c] = __builtin_fma(av[r], bv[c], acc[r][c]);
-                }
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-#pragma unroll
-                    for (int c = 0; c < 4; c++) {
-                        const int row = i * S + 4 * tr + r, col = j * S + 4 * tc + c;
-                        if (row < b && col < b) X[row][col] = -acc[r][c];
-                    }
+                for (int q = 0; q < KS4; q++) lv[h][q] = li[min(j * S + 4 * q + lg, b - 1)];
             }
+            f64x4 sacc[2] = {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}};
+#pragma unroll
+            for (int q = 0; q < KS4; q++) {
+                const int k = j * S + 4 * q + lg;
+                const double xb = X[k][c0 + lr];
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const double a = i * S + 16 * h + lr < b && k < b ? (double)lv[h][q] : 0.0;
+                    sacc[h] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, xb, sacc[h], 0, 0, 0);
+                }
+            }
+            f64x4 pacc[2] = {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}};
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const double a = X[i * S + 16 * h + lr][i * S + 16 * kh + 4 * r + lg];
+                        pacc[h] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, sacc[kh][r], pacc[h], 0, 0, 0);
+                    }
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = i * S + 16 * h + 4 * r + lg, col = c0 + lr;
+                    if (row < b && col < b) X[row][col] = -pacc[h][r];
+                }
         }
         __syncthreads();
     };
-    phase(std::integral_constant<int, 1>());
-    phase(std::integral_constant<int, 2>());
-    phase(std::integral_constant<int, 3>());
+    level(std::integral_constant<int, 1>());
+    level(std::integral_constant<int, 2>());
+    level(std::integral_constant<int, 3>());
     // the block's rows from its diagonal to the end of its leaf: the inverse, then zeros (w ≤ lb columns)
     const int p = r0 / lb, o = r0 - p * lb, w = min(lb, n - p * lb) - o;
     T *out = Inv + (ll)p * istride + (ll)o * lb + o;
