@@ -161,6 +161,28 @@ __global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, ll ld, ll bst
     // region of X holding the copy of diagonal sub-block s of L until phase d ≥ 1 overwrites it
     const auto stage_row = [](int s) { return S * (s < 3 ? s + 1 : 3); };
     const auto stage_col = [](int s) { return S * (s < 3 ? 0 : 1); };
+    // The off-diagonal levels below are tasks (j, J) of wave wv: task = wv + 4·round, j = task / 2, J = task % 2, and
+    // their operands from L are rows i·32 + 16h + lane % 16, columns j·32 + 4q + lane / 16 (i = j + d; addresses
+    // clamped into the block, values outside it not used). Level 1's are loaded here with the gather's, level d + 1's
+    // before level d runs, so that their latency is hidden (all three levels' at once need 256 registers and slow the
+    // diagonal inverses down).
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6), lr = t & 15, lg = (t & 63) >> 4;
+    const auto load_task = [&](auto dc, int task, auto &lv) {
+        constexpr int d = decltype(dc)::value, KS4 = d * S / 4;
+        const int j = task >> 1, i = j + d;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const T *li = Lb + (ll)min(i * S + 16 * h + lr, b - 1) * ld;
+#pragma unroll
+            for (int q = 0; q < KS4; q++) lv[h][q] = li[min(j * S + 4 * q + lg, b - 1)];
+        }
+    };
+    using D1 = std::integral_constant<int, 1>;
+    using D2 = std::integral_constant<int, 2>;
+    using D3 = std::integral_constant<int, 3>;
+    T l1[2][2][S / 4], l2[2][2 * S / 4], l3[2][3 * S / 4];   // level 1: a second task for waves 0, 1; level 3: waves 0, 1
+    load_task(D1(), wv, l1[0]);
+    if (wv + 4 < 2 * (NSB - 1)) load_task(D1(), wv + 4, l1[1]);
     {
         constexpr int PER = NSB * S * S / 256;
         T v[PER];   // every load in flight, from addresses clamped into the block
@@ -204,58 +226,52 @@ __global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, ll ld, ll bst
     // Off-diagonal sub-blocks by distance d from the diagonal, on the matrix cores (v_mfma_f64_16x16x4f64: lane l
     // supplies A[l % 16][k = l / 16] and B[k = l / 16][l % 16]; accumulator r of lane l holds D[4r + l / 16][l % 16]).
     // Task (j, J) of level d forms columns j·32 + 16J .. + 15 of X_(i, j), i = j + d, as two 16-row halves:
-    // S = Σ_k L_(i, k)·X_(k, j) over the d·32 columns k of blocks j .. i − 1 (d·8 steps; L from global memory, zero
-    // outside the block, X from LDS), then X_(i, j) = −inv(L_(i, i))·S with S taken straight from the accumulators:
+    // S = Σ_k L_(i, k)·X_(k, j) over the d·32 columns k of blocks j .. i − 1 (d·8 steps; L from the registers loaded
+    // above, zero outside the block, X from LDS), then X_(i, j) = −inv(L_(i, i))·S with S taken straight from the accumulators:
     // accumulator r of half kh holds rows 16kh + 4r + l / 16 of S, which is the second operand's k of that step. A
-    // level's tasks read only blocks of earlier levels and write distinct blocks; they go round robin over the waves.
+    // level's tasks read only blocks of earlier levels and write distinct blocks.
     typedef double f64x4 __attribute__((ext_vector_type(4)));
-    const int wv = __builtin_amdgcn_readfirstlane(t >> 6), lr = t & 15, lg = (t & 63) >> 4;
-    const auto level = [&](auto dc) {
-        constexpr int d = decltype(dc)::value, nblk = NSB - d, KS4 = d * S / 4, NTASK = 2 * nblk;
-        for (int task = wv; task < NTASK; task += 4) {
-            const int j = task >> 1, J = task & 1, i = j + d, c0 = j * S + 16 * J;
-            // every load of L in flight first, from addresses clamped into the block (values outside it are not used)
-            T lv[2][KS4];
+    const auto task_run = [&](auto dc, int task, const auto &lv) {
+        constexpr int d = decltype(dc)::value, KS4 = d * S / 4;
+        const int j = task >> 1, J = task & 1, i = j + d, c0 = j * S + 16 * J;
+        f64x4 sacc[2] = {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}};
+#pragma unroll
+        for (int q = 0; q < KS4; q++) {
+            const int k = j * S + 4 * q + lg;
+            const double xb = X[k][c0 + lr];
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                const T *li = Lb + (ll)min(i * S + 16 * h + lr, b - 1) * ld;
-#pragma unroll
-                for (int q = 0; q < KS4; q++) lv[h][q] = li[min(j * S + 4 * q + lg, b - 1)];
+                const double a = i * S + 16 * h + lr < b && k < b ? (double)lv[h][q] : 0.0;
+                sacc[h] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, xb, sacc[h], 0, 0, 0);
             }
-            f64x4 sacc[2] = {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}};
+        }
+        f64x4 pacc[2] = {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}};
 #pragma unroll
-            for (int q = 0; q < KS4; q++) {
-                const int k = j * S + 4 * q + lg;
-                const double xb = X[k][c0 + lr];
+        for (int h = 0; h < 2; h++)
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const double a = i * S + 16 * h + lr < b && k < b ? (double)lv[h][q] : 0.0;
-                    sacc[h] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, xb, sacc[h], 0, 0, 0);
-                }
-            }
-            f64x4 pacc[2] = {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}};
-#pragma unroll
-            for (int h = 0; h < 2; h++)
-#pragma unroll
-                for (int kh = 0; kh < 2; kh++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const double a = X[i * S + 16 * h + lr][i * S + 16 * kh + 4 * r + lg];
-                        pacc[h] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, sacc[kh][r], pacc[h], 0, 0, 0);
-                    }
-#pragma unroll
-            for (int h = 0; h < 2; h++)
+            for (int kh = 0; kh < 2; kh++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const int row = i * S + 16 * h + 4 * r + lg, col = c0 + lr;
-                    if (row < b && col < b) X[row][col] = -pacc[h][r];
+                    const double a = X[i * S + 16 * h + lr][i * S + 16 * kh + 4 * r + lg];
+                    pacc[h] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, sacc[kh][r], pacc[h], 0, 0, 0);
                 }
-        }
-        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int row = i * S + 16 * h + 4 * r + lg, col = c0 + lr;
+                if (row < b && col < b) X[row][col] = -pacc[h][r];
+            }
     };
-    level(std::integral_constant<int, 1>());
-    level(std::integral_constant<int, 2>());
-    level(std::integral_constant<int, 3>());
+    load_task(D2(), wv, l2);
+    task_run(D1(), wv, l1[0]);
+    if (wv + 4 < 2 * (NSB - 1)) task_run(D1(), wv + 4, l1[1]);
+    __syncthreads();
+    if (wv < 2 * (NSB - 3)) load_task(D3(), wv, l3);
+    task_run(D2(), wv, l2);
+    __syncthreads();
+    if (wv < 2 * (NSB - 3)) task_run(D3(), wv, l3);
+    __syncthreads();
     // the block's rows from its diagonal to the end of its leaf: the inverse, then zeros (w ≤ lb columns)
     const int p = r0 / lb, o = r0 - p * lb, w = min(lb, n - p * lb) - o;
     T *out = Inv + (ll)p * istride + (ll)o * lb + o;
