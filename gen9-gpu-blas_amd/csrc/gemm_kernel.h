@@ -286,6 +286,11 @@ __global__ void __launch_bounds__(WM *WN * 64 * KG) gemm_kernel(GemmParams<typen
         K = max(k1 - k0, 0);
         A += AK ? k0 : (long long)k0 * p.lda;
         B += BKC ? k0 : (long long)k0 * p.ldb;
+        if constexpr (!SPLIT) {   // k-limited tiles of a batch: product z
+            A += z * p.sA;
+            B += z * p.sB;
+            C += z * p.sC;
+        }
     } else {
         A += z * p.sA;
         B += z * p.sB;

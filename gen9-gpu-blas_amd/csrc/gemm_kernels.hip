@@ -298,13 +298,13 @@ static int klim_pair(long long tiles, int per_cu) { return tiles > num_cus && ti
 // Triangle (TRI) and k-limited (KLIM) modes of the FP32 whole-tile kernel for SYRK / SYR2K / TRMM: one product,
 // whole tiles (the callers check), `tiles` workgroups.
 template <int BM, int BN, int WM, int WN, int NS, int BLK, bool AK, bool BKC, int TRI, int KLIM>
-static int launch_sg_mode(const sg::Params &p0, long long tiles) {
+static int launch_sg_mode(const sg::Params &p0, long long tiles, int count = 1) {
     constexpr auto kern = sg::sgemm_kernel<BM, BN, WM, WN, NS, AK, BKC, BLK, TRI, KLIM>;
     sg::Params p = p0;
     p.tiles_m = p.M / BM;
     p.tiles_n = p.N / BN;
-    if constexpr (KLIM != 0) p.kpair = klim_pair(tiles, wgs_per_cu<kern>(WM * WN * 64));
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(WM * WN * 64), 0, stream, p);
+    if constexpr (KLIM != 0) p.kpair = count == 1 && klim_pair(tiles, wgs_per_cu<kern>(WM * WN * 64));
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)count), dim3(WM * WN * 64), 0, stream, p);
     G9_HIP(hipGetLastError());
     return 0;
 }
@@ -342,21 +342,25 @@ static bool sg_tri(const GemmCall &c, bool lower, int *rc) {
     if (c.tA && !c.tB) return lower ? sg_tri_layout<1, false, false>(c, rc) : sg_tri_layout<2, false, false>(c, rc);
     return false;
 }
-// k-limited FP32 NN product on the whole-tile kernel (TRMM): the plain products' classes, whole tiles only.
+// k-limited FP32 NN product (or strided batch of them) on the whole-tile kernel (TRMM, the triangular solves): the
+// plain products' classes, whole tiles only.
 template <int KLIM>
 static bool sg_klim_mode(const GemmCall &c, int *rc) {
     const sg::Params p = sg_params(c);
     const long long t0 = (long long)(c.M / 128) * (c.N / 256), t1 = (long long)(c.M / 128) * (c.N / 128),
-                    t2 = (long long)(c.M / 64) * (c.N / 64);
-    if (c.M % 128 == 0 && c.N % 256 == 0 && t0 >= num_cus) *rc = launch_sg_mode<128, 256, 2, 4, 2, 4, true, false, 0, KLIM>(p, t0);
-    else if (c.M % 128 == 0 && c.N % 128 == 0 && t1 >= num_cus) *rc = launch_sg_mode<128, 128, 2, 4, 3, 4, true, false, 0, KLIM>(p, t1);
-    else if (c.M % 64 == 0 && c.N % 64 == 0 && t2 >= num_cus) *rc = launch_sg_mode<64, 64, 2, 2, 4, 8, true, false, 0, KLIM>(p, t2);
+                    t2 = (long long)(c.M / 64) * (c.N / 64), nb = c.count;
+    if (c.M % 128 == 0 && c.N % 256 == 0 && t0 * nb >= num_cus)
+        *rc = launch_sg_mode<128, 256, 2, 4, 2, 4, true, false, 0, KLIM>(p, t0, c.count);
+    else if (c.M % 128 == 0 && c.N % 128 == 0 && t1 * nb >= num_cus)
+        *rc = launch_sg_mode<128, 128, 2, 4, 3, 4, true, false, 0, KLIM>(p, t1, c.count);
+    else if (c.M % 64 == 0 && c.N % 64 == 0 && t2 * nb >= num_cus)
+        *rc = launch_sg_mode<64, 64, 2, 2, 4, 8, true, false, 0, KLIM>(p, t2, c.count);
     else return false;
     return true;
 }
 static bool sg_klim(const GemmCall &c, int klim, int *rc) {
     // the k range of every tile is non-empty only when K spans the triangular operand's order
-    if (c.count != 1 || c.tA || c.tB || !sgemm_tiles_ok(c) || (klim <= 2 ? c.K != c.M : c.K != c.N)) return false;
+    if (c.count < 1 || c.tA || c.tB || !sgemm_tiles_ok(c) || (klim <= 2 ? c.K != c.M : c.K != c.N)) return false;
     switch (klim) {
     case 1: return sg_klim_mode<1>(c, rc);
     case 2: return sg_klim_mode<2>(c, rc);
@@ -491,7 +495,8 @@ static int launch_tri_typed(const GemmCall &c, bool lower) {
     GemmParams<S> p;
     p.A = c.A; p.B = c.B; p.C = c.C;
     p.lda = c.lda; p.ldb = c.ldb; p.ldc = c.ldc;
-    p.sA = p.sB = p.sC = 0;
+    const bool batch = c.count > 1;
+    p.sA = batch ? c.sA : 0; p.sB = batch ? c.sB : 0; p.sC = batch ? c.sC : 0;
     p.M = c.M; p.N = c.N; p.K = c.K;
     p.alpha = (S)c.alpha;
     p.beta = (S)c.beta;
@@ -500,8 +505,9 @@ static int launch_tri_typed(const GemmCall &c, bool lower) {
     p.kper = p.vec_p = 0;
     const long long es = sizeof(T);
     const long long cal = es * 4 < 16 ? es * 4 : 16;
-    p.vec_c = ((uintptr_t)c.C % cal == 0) && (c.ldc * es) % cal == 0;
-    const bool vec = ((uintptr_t)c.A % 16 == 0) && ((uintptr_t)c.B % 16 == 0) && (c.lda * es) % 16 == 0 && (c.ldb * es) % 16 == 0;
+    p.vec_c = ((uintptr_t)c.C % cal == 0) && (c.ldc * es) % cal == 0 && (p.sC * es) % cal == 0;
+    const bool vec = ((uintptr_t)c.A % 16 == 0) && ((uintptr_t)c.B % 16 == 0) && (c.lda * es) % 16 == 0 && (c.ldb * es) % 16 == 0 &&
+                     (p.sA * es) % 16 == 0 && (p.sB * es) % 16 == 0;
     if (!c.tA && c.tB) return launch_tri_layout<T, true, true>(p, vec, lower);
     if (c.tA && !c.tB) return launch_tri_layout<T, false, false>(p, vec, lower);
     G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "triangle product: layout tA=%d tB=%d", c.tA, c.tB);
@@ -525,14 +531,14 @@ int launch_gemm_tri(const GemmCall &c, bool lower) {
 // longest ranges dispatched first; the small tiles when the big ones are fewer than the CUs. Layout NN only (both
 // operands as stored), one product.
 template <class T, TileCfg C, int KLIM, bool VEC>
-static int launch_klim_t(GemmParams<typename Mma<T>::Sum> p) {
+static int launch_klim_t(GemmParams<typename Mma<T>::Sum> p, int count) {
     p.tiles_m = (p.M + C.BM - 1) / C.BM;
     p.tiles_n = (p.N + C.BN - 1) / C.BN;
     const long long tiles = (long long)p.tiles_m * p.tiles_n;
     if (tiles > 0x7fffffffLL) G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "gemm grid too large (%d × %d tiles)", p.tiles_m, p.tiles_n);
     constexpr auto kern = gemm_kernel<T, C.BM, C.BN, C.WM, C.WN, true, false, VEC, true, false, 0, KLIM>;
-    p.kpair = klim_pair(tiles, wgs_per_cu<kern>(C.WM * C.WN * 64));
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(C.WM * C.WN * 64), 0, stream, p);
+    p.kpair = count == 1 && klim_pair(tiles, wgs_per_cu<kern>(C.WM * C.WN * 64));
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)count), dim3(C.WM * C.WN * 64), 0, stream, p);
     G9_HIP(hipGetLastError());
     return 0;
 }
@@ -542,7 +548,8 @@ static int launch_klim_typed(const GemmCall &c, int klim) {
     GemmParams<S> p;
     p.A = c.A; p.B = c.B; p.C = c.C;
     p.lda = c.lda; p.ldb = c.ldb; p.ldc = c.ldc;
-    p.sA = p.sB = p.sC = 0;
+    const bool batch = c.count > 1;
+    p.sA = batch ? c.sA : 0; p.sB = batch ? c.sB : 0; p.sC = batch ? c.sC : 0;
     p.M = c.M; p.N = c.N; p.K = c.K;
     p.alpha = (S)c.alpha;
     p.beta = (S)c.beta;
@@ -551,8 +558,9 @@ static int launch_klim_typed(const GemmCall &c, int klim) {
     p.kper = p.vec_p = 0;
     const long long es = sizeof(T);
     const long long cal = es * 4 < 16 ? es * 4 : 16;
-    p.vec_c = ((uintptr_t)c.C % cal == 0) && (c.ldc * es) % cal == 0;
-    const bool vec = ((uintptr_t)c.A % 16 == 0) && ((uintptr_t)c.B % 16 == 0) && (c.lda * es) % 16 == 0 && (c.ldb * es) % 16 == 0;
+    p.vec_c = ((uintptr_t)c.C % cal == 0) && (c.ldc * es) % cal == 0 && (p.sC * es) % cal == 0;
+    const bool vec = ((uintptr_t)c.A % 16 == 0) && ((uintptr_t)c.B % 16 == 0) && (c.lda * es) % 16 == 0 && (c.ldb * es) % 16 == 0 &&
+                     (p.sA * es) % 16 == 0 && (p.sB * es) % 16 == 0;
     // tile class: FP16 the big tiles when they are at least the CUs; FP32 / FP64 the first of big, small and (FP64)
     // 64×64 that makes two workgroups per CU or more, so that long and short k ranges can share the CUs
     const auto by_cfg = [&](auto vc) -> int {
@@ -560,18 +568,18 @@ static int launch_klim_typed(const GemmCall &c, int klim) {
         using CF = Cfg<T, true, false, V>;
         constexpr TileCfg tiny{64, 64, 2, 2};
         const auto ntiles = [&](TileCfg t) {
-            return (long long)((c.M + t.BM - 1) / t.BM) * ((c.N + t.BN - 1) / t.BN);
+            return (long long)((c.M + t.BM - 1) / t.BM) * ((c.N + t.BN - 1) / t.BN) * c.count;
         };
         constexpr bool half = sizeof(T) == 2, dbl = sizeof(T) == 8;
         const long long want = half ? num_cus : 2LL * num_cus;
         const int cls = ntiles(CF::big) >= want ? 0 : (!dbl || ntiles(CF::small) >= want) ? 1 : 2;
         const auto go = [&](auto kc) -> int {
             constexpr int K = decltype(kc)::value;
-            if (cls == 0) return launch_klim_t<T, CF::big, K, V>(p);
+            if (cls == 0) return launch_klim_t<T, CF::big, K, V>(p, c.count);
             if constexpr (dbl) {
-                if (cls == 2) return launch_klim_t<T, tiny, K, V>(p);
+                if (cls == 2) return launch_klim_t<T, tiny, K, V>(p, c.count);
             }
-            return launch_klim_t<T, CF::small, K, V>(p);
+            return launch_klim_t<T, CF::small, K, V>(p, c.count);
         };
         switch (klim) {
         case 1: return go(std::integral_constant<int, 1>());
@@ -584,7 +592,7 @@ static int launch_klim_typed(const GemmCall &c, int klim) {
     return vec ? by_cfg(std::true_type()) : by_cfg(std::false_type());
 }
 int launch_gemm_klim(const GemmCall &c, int klim) {
-    if (c.tA || c.tB || c.count != 1) G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "k-limited product: layout tA=%d tB=%d, batch %d", c.tA, c.tB, c.count);
+    if (c.tA || c.tB || c.count < 1) G9_FAIL(GEN9BLAS_ERR_UNSUPPORTED, "k-limited product: layout tA=%d tB=%d, batch %d", c.tA, c.tB, c.count);
     switch (c.type) {
     case GEN9BLAS_H:
     case GEN9BLAS_HS: return launch_klim_typed<f16>(c, klim);

@@ -129,13 +129,15 @@ struct GemmCall {
 G9_HIDDEN int launch_gemm(const GemmCall &c);
 // Lower (upper) triangle only of a square product, C = alpha·op(A)·op(B) + beta·C there (tA != tB, count 1).
 G9_HIDDEN int launch_gemm_tri(const GemmCall &c, bool lower);
-// NN product whose tiles take only the k range where a triangular operand is non-zero: klim 1 op(A) lower, 2 op(A)
-// upper, 3 op(B) lower, 4 op(B) upper (count 1).
+// NN product (or strided batch of them) whose tiles take only the k range where a triangular operand is non-zero:
+// klim 1 op(A) lower, 2 op(A) upper, 3 op(B) lower, 4 op(B) upper.
 G9_HIDDEN int launch_gemm_klim(const GemmCall &c, int klim);
 // Inverses, computed in FP64 (level3.hip), of the `count` 128-row diagonal blocks of lower-triangular leaves of lb
-// rows (lb = 128 or 256): leaf p's element (i, j) at L[p·bstride + i·ld + j]; the inverses go to leaf p at
-// Inv + p·lb² (row stride lb), with zeros above the first block's inverse; es 4 (float) or 8 (double).
-G9_HIDDEN int launch_tri_inverse(int es, const void *L, long long ld, long long bstride, int count, void *Inv, int lb);
+// rows (lb a multiple of 128): leaf p's element (i, j) at L[p·bstride + i·ld + j]; the inverses go to leaf p at
+// Inv + p·istride (row stride lb), with zeros right of each block's inverse to the end of its leaf; es 4 (float) or
+// 8 (double).
+G9_HIDDEN int launch_tri_inverse(int es, const void *L, long long ld, long long bstride, int count, void *Inv, int lb,
+                                 long long istride);
 // The whole gen9blas_gemm_batched call: checks, operand resolution, skinny / MFMA dispatch, wait (gemm.hip).
 G9_HIDDEN int gemm_impl(int type, int tA, int tB, int M, int N, int K, double alpha, const void *A, int lda, long long sA,
                         const void *B, int ldb, long long sB, double beta, void *C, int ldc, long long sC, int count);

@@ -758,7 +758,8 @@ constexpr int INV_MIN = 1280;
 constexpr int INV_IB = 256;     // rows per block
 constexpr int INV_ROWS = 16;    // rows of x_q per solving workgroup
 
-// 128 × 128 tiles of D_q and C_q, in solve order, into Dg and Cg + q·IB² (row stride IB), zero padded: past the
+// 128 × 128 tiles of D_q and C_q, in solve order, into Dg + q·IB·(IB + 1) and Cg + q·IB² (row stride IB; D_q's
+// stride puts element (i, j) of the blocks' rows and columns, counted from block 0, at Dg[i·IB + j]), zero padded: past the
 // order, D_q holds the identity and C_q zeros, so inv(D_q) and E_q keep the block's rows apart from the padding.
 // Block q = blockIdx.x; blockIdx.y < Q² (Q = IB / 128) is quadrant (y / Q, y % Q) of D_q (diagonal quadrants: the
 // triangle with the diagonal, or ones for a unit diagonal, which is not read; below: dense; above: zeros), the
@@ -773,7 +774,7 @@ __global__ void __launch_bounds__(NT) inv_gather(Shape s, const T *__restrict__ 
     const int n = s.nrows, q = blockIdx.x, tid = threadIdx.x, w = tid % SB;
     const bool coup = blockIdx.y >= Q * Q;
     const int y = coup ? blockIdx.y - Q * Q : blockIdx.y, qr = y / Q, qc = y % Q;
-    R *out = (coup ? Cg : Dg) + (ll)q * IB * IB + (ll)qr * SB * IB + qc * SB;
+    R *out = (coup ? Cg + (ll)q * IB * IB : Dg + (ll)q * IB * (IB + 1)) + (ll)qr * SB * IB + qc * SB;
     // mode 0: zeros, 1: dense, 2: lower triangle with the diagonal
     const int mode = coup ? (q > 0 ? 1 : 0) : (qr == qc ? 2 : qr > qc ? 1 : 0);
     const int G0 = q * IB + qr * SB, H0 = (coup ? q - 1 : q) * IB + qc * SB;   // solve-order row and column
@@ -1043,12 +1044,12 @@ static int launch_rank(int es, int fmt, const Shape &s, double alpha, const void
     });
 }
 
-// Work space of the inverse-based solve for order n: the solution vector, then D (later E), C and the inverses,
-// nbI·IB² each, and the products of the IB = 256 composition, nbI·128².
+// Work space of the inverse-based solve for order n: the solution vector, then D (later E) and the inverses, nbI·IB·
+// (IB + 1) each, C, nbI·IB², and the products of the compositions, at most nbI·IB²/4.
 template <class R>
 static size_t inv_bytes(int n) {
-    const size_t nbI = (size_t)(n + INV_IB - 1) / INV_IB, m2 = (size_t)INV_IB * INV_IB;
-    return (((size_t)n * sizeof(R) + 255) & ~(size_t)255) + (3 * nbI * m2 + nbI * SB * SB) * sizeof(R);
+    const size_t nbI = (size_t)(n + INV_IB - 1) / INV_IB, m2 = (size_t)INV_IB * INV_IB, sd = m2 + INV_IB;
+    return (((size_t)n * sizeof(R) + 255) & ~(size_t)255) + (2 * nbI * sd + nbI * m2 + nbI * m2 / 4) * sizeof(R);
 }
 // The inverse-based solve of full storage (inv_gather, inv_step) in the work space w (inv_bytes).
 template <class T>
@@ -1056,17 +1057,20 @@ static int solve_inv(const Shape &s, const T *a, int trans, int fwd, typename Co
     using R = typename Comp<T>::R;
     constexpr int IB = INV_IB, QB = IB / SB;
     const int n = s.nrows, nbI = (n + IB - 1) / IB, type = sizeof(R) == 8 ? GEN9BLAS_D : GEN9BLAS_S;
-    const ll m2 = (ll)IB * IB;
+    // D_q and inv(D_q) at stride sd = IB·(IB + 1), so that the sub-blocks of 2h rows of every level of the composition
+    // below start at the uniform stride 2h·(IB + 1); C_q and E_q (which reuses D's space) at stride IB²
+    const ll m2 = (ll)IB * IB, sd = m2 + IB;
     R *xs = (R *)w;
     R *D = (R *)((char *)w + (((size_t)n * sizeof(R) + 255) & ~(size_t)255));
-    R *C = D + nbI * m2, *Di = C + nbI * m2, *Tm = Di + nbI * m2, *E = D;
+    R *Di = D + nbI * sd, *C = Di + nbI * sd, *Tm = C + nbI * m2, *E = D;
     hipLaunchKernelGGL((inv_gather<T, IB>), dim3(nbI, 2 * QB * QB), dim3(NT), 0, stream, s, a, trans, fwd, D, C);
     G9_HIP(hipGetLastError());
-    // the 128-row diagonal blocks of every D_q, in FP64, into their places in inv(D_q) (zeros above them)
-    G9_TRY(launch_tri_inverse((int)sizeof(R), D, IB, m2, nbI * QB, Di, IB));
-    // count products C_z = alpha·A_z·B_z of M × K by K × N, (row stride, batch stride) of each operand given
+    // the 128-row diagonal blocks of every D_q, in FP64, into their places in inv(D_q) (zeros right of them)
+    G9_TRY(launch_tri_inverse((int)sizeof(R), D, IB, sd, nbI * QB, Di, IB, sd));
+    // count products C_z = alpha·A_z·B_z of M × K by K × N, (row stride, batch stride) of each operand given; klim: A
+    // is lower triangular and each tile takes only the k range where it is non-zero
     const auto gemm = [&](int M, int N, int K, double alpha, const R *A, ll lda, ll sA, const R *B, ll ldb, ll sB, R *Cp,
-                          ll ldc, ll sC, int count) {
+                          ll ldc, ll sC, int count, bool klim = false) {
         GemmCall g;
         g.type = type;
         g.tA = g.tB = 0;
@@ -1077,14 +1081,18 @@ static int solve_inv(const Shape &s, const T *a, int trans, int fwd, typename Co
         g.A = A; g.lda = lda; g.sA = sA;
         g.B = B; g.ldb = ldb; g.sB = sB;
         g.C = Cp; g.ldc = ldc; g.sC = sC;
-        return launch_gemm(g);
+        return klim ? launch_gemm_klim(g, 1) : launch_gemm(g);
     };
-    if (QB == 2) {   // lower-left quadrant of inv(D_q) = [I1 0; K I2]⁻¹: −inv(I2)·K·inv(I1), K = D_q's lower-left
-        const ll h = SB, t2 = (ll)SB * SB;
-        G9_TRY(gemm(SB, SB, SB, 1.0, Di + h * (IB + 1), IB, m2, D + h * IB, IB, m2, Tm, SB, t2, nbI));
-        G9_TRY(gemm(SB, SB, SB, -1.0, Tm, SB, t2, Di, IB, m2, Di + h * IB, IB, m2, nbI));
+    // inv(D_q) by levels, h = 128 .. IB / 2: a sub-block [I1 0; K I2] of 2h rows (every one whole: D_q is padded) has the
+    // inverse [inv(I1) 0; −inv(I2)·K·inv(I1) inv(I2)]; two GEMMs batched over all of them form the lower-left quadrants
+    for (ll h = SB; h < IB; h *= 2) {
+        const int cnt = (int)(nbI * (IB / (2 * h)));
+        const ll st = 2 * h * (IB + 1), t2 = h * h;
+        G9_TRY(gemm((int)h, (int)h, (int)h, 1.0, Di + h * (IB + 1), IB, st, D + h * IB, IB, st, Tm, h, t2, cnt));
+        G9_TRY(gemm((int)h, (int)h, (int)h, -1.0, Tm, h, t2, Di, IB, st, Di + h * IB, IB, st, cnt));
     }
-    if (nbI > 1) G9_TRY(gemm(IB, IB, IB, 1.0, Di + m2, IB, m2, C + m2, IB, m2, E + m2, IB, m2, nbI - 1));   // E_q, q ≥ 1
+    // E_q = inv(D_q)·C_q, q ≥ 1, each tile over the k range where inv(D_q) is non-zero (256³ × 63 FP32: 27.9 → 24.8 µs)
+    if (nbI > 1) G9_TRY(gemm(IB, IB, IB, 1.0, Di + sd, IB, sd, C + m2, IB, m2, E + m2, IB, m2, nbI - 1, true));
     const int per = trans ? UPD_COLS : UPD_ROWS;
     for (int q = 0; q < nbI; q++) {
         const int g0 = q * IB, b = n - g0 < IB ? n - g0 : IB, p = fwd ? g0 : n - g0 - b;
@@ -1097,7 +1105,7 @@ static int solve_inv(const Shape &s, const T *a, int trans, int fwd, typename Co
         }
         const unsigned grid = IB / INV_ROWS + (o1 > o0 ? blocks(o1 - o0, per) : 0u);
         hipLaunchKernelGGL((inv_step<T, IB>), dim3(grid), dim3(NT), 0, stream, s, a, trans, fwd, pp, pb, p, b, o0, o1,
-                           Di + q * m2, E + q * m2, xf, xs);
+                           Di + q * sd, E + q * m2, xf, xs);
         G9_HIP(hipGetLastError());
     }
     return 0;
