@@ -234,13 +234,15 @@ static int launch_hgemm_tiles(const GemmCall &c) {
 }
 
 // ---------------- FP32 whole-tile kernel ----------------
-// Classes, largest tile first; a product takes the first class whose whole tiles fill the CUs and cover at least
-// 90 % of C. Measured on MI355X (TFLOP/s, sustained, against the general kernel of gemm_kernel.h in the same runs):
+// Classes, largest tile first; a product takes the first class whose whole tiles fill the CUs (128×128: twice over,
+// else the 64×64 tiles of several rounds finish sooner: 2048³ 129 → 125 µs, 2048×2048×1024 68 → 66, the triangular
+// solve's 1024×4096×1024 with beta = 1 70.3 → 67.1) and cover at least 90 % of C. Measured on MI355X (TFLOP/s,
+// sustained, against the general kernel of gemm_kernel.h in the same runs):
 // - 128×256 tiles, 8 waves of 64×64, two stages, sums blocked per 128 k: n = 4096 NN 144.9 (124.6), NT 144.3
 //   (130.8); 8192×8192×2048 144.1 (123.4); 2944×11008×4096 NT β = 0.5 140.0 (127.9). Three stages 142.6, blocks of
 //   32 k 134.3, of 64 k 140.3, of 256 k 142.6; 256×128 tiles 142.7;
 // - 128×128 tiles, 8 waves of 64×32, three stages, 128-k blocks: n = 2048 134.4 (121.4; 4 waves of 64×64: 129.7;
-//   64×64 tiles: 132.4);
+//   64×64 tiles: 132.4; a later build read 133.0 against 137.2 for the 64×64 tiles, which n = 2048 now takes);
 // - 64×64 tiles, 4 waves of 32×32, four stages, 256-k blocks: n = 1024 102.6 (87.7; 128-k blocks 101.9, 32-k blocks
 //   90.9; three stages 94.0, six 93.0, eight 92.2).
 // The rows and columns beyond the whole tiles (an M or N that is not a multiple of the tile) go to the general
@@ -387,7 +389,7 @@ static int launch_sgemm(const GemmCall &c) {
     for (int k = 0; k < 3 && cls < 0; k++) {
         const int mi = c.M / SG_CLASSES[k].BM * SG_CLASSES[k].BM, ni = c.N / SG_CLASSES[k].BN * SG_CLASSES[k].BN;
         const long long tiles = (long long)(mi / SG_CLASSES[k].BM) * (ni / SG_CLASSES[k].BN) * c.count;
-        if (tiles >= num_cus && tiles <= 0x7fffffffLL && (double)mi * ni >= 0.9 * (double)c.M * c.N) {
+        if (tiles >= (k == 1 ? 2LL : 1LL) * num_cus && tiles <= 0x7fffffffLL && (double)mi * ni >= 0.9 * (double)c.M * c.N) {
             cls = k;
             Mi = mi;
             Ni = ni;
