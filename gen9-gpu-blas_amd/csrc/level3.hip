@@ -158,7 +158,7 @@ __global__ void __launch_bounds__(256) trsm_inv_kernel(const T *L, ll ld, ll bst
     __shared__ double X[TRSM_NB][TRSM_NB + 1];
     const int bi = blockIdx.x, r0 = bi * TRSM_NB, b = min(TRSM_NB, n - r0), t = threadIdx.x;
     const T *Lb = L + (ll)(r0 / lb) * bstride + (ll)(r0 % lb) * (ld + 1);   // element (i, j) of the block at Lb[i·ld + j]
-    // region of X holding the copy of diagonal sub-block s of L until phase d ≥ 1 overwrites it
+    // region of X holding the copy of diagonal sub-block s of L until a level d ≥ 1 below overwrites it
     const auto stage_row = [](int s) { return S * (s < 3 ? s + 1 : 3); };
     const auto stage_col = [](int s) { return S * (s < 3 ? 0 : 1); };
     // The off-diagonal levels below are tasks (j, J) of wave wv: task = wv + 4·round, j = task / 2, J = task % 2, and
