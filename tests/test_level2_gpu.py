@@ -10,6 +10,8 @@ FP16 3e-3, FP64 1e-12. Device-resident cases at n = 4096 exercise the multi-bloc
 product kernel (16-byte rows and an odd row stride); orders below 1280 take the substituting solve, from 1280 up the
 solve on inverted diagonal blocks.
 """
+import itertools
+
 import numpy as np
 import pytest
 
@@ -214,36 +216,35 @@ def test_band_packed(g9, orc, dt, n, K):
         ref, scale = orc.mv(orc.symmetric(Tp, uplo), x, 0.5, -1.0, y0)
         g9.spmv(Ap, x, uplo=uplo, alpha=0.5, beta=-1.0, y=y0)
         assert_close(f"spmv n={n} {uplo}", y0, ref, scale, tol)
-        for tr in (False, True):
-            for dg in (False, True):
-                label = f"n={n} K={K} {uplo} tr={tr} diag={dg}"
-                Ob, Op = orc.triangle(T, uplo, dg), orc.triangle(Tp, uplo, dg)
-                Ob, Op = (Ob.T, Op.T) if tr else (Ob, Op)
-                x = strided(rng, n, dt, -3)
-                ref, scale = orc.mv(Ob, x)
-                g9.tbmv(P, x, K, uplo=uplo, trans=tr, diag=dg)
-                assert_close("tbmv " + label, x, ref, scale, tol)
-                x = strided(rng, n, dt, 1)
-                ref, scale = orc.mv(Op, x)
-                g9.tpmv(Ap, x, uplo=uplo, trans=tr, diag=dg)
-                assert_close("tpmv " + label, x, ref, scale, tol)
-                # solves: well conditioned (small off-diagonal entries, diagonal 1..2)
-                Ts = T / max(K, 1) / 4
-                np.fill_diagonal(Ts, 1 + np.abs(np.diag(T)))
-                Ps = band_store(Ts, KL, KU).astype(dt)
-                Os = orc.triangle(orc.band_dense(Ps, n, n, KL, KU), uplo, dg)
-                b = strided(rng, n, dt, 2)
-                ref = orc.solve(Os.T if tr else Os, f64(b))
-                g9.tbsv(Ps, b, K, uplo=uplo, trans=tr, diag=dg)
-                assert_close("tbsv " + label, b, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
-                Tq = Tp / n
-                np.fill_diagonal(Tq, 1 + np.abs(np.diag(Tp)))
-                Aq = packed_store(Tq, uplo).astype(dt)
-                Oq = orc.triangle(orc.packed_dense(Aq, n, uplo), uplo, dg)
-                b = strided(rng, n, dt, -1)
-                ref = orc.solve(Oq.T if tr else Oq, f64(b))
-                g9.tpsv(Aq, b, uplo=uplo, trans=tr, diag=dg)
-                assert_close("tpsv " + label, b, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+        for tr, dg in itertools.product((False, True), repeat=2):
+            label = f"{uplo} n={n} K={K} trans={tr} unit={dg}"
+            Ob, Op = orc.triangle(T, uplo, dg), orc.triangle(Tp, uplo, dg)
+            Ob, Op = (Ob.T, Op.T) if tr else (Ob, Op)
+            x = strided(rng, n, dt, -3)
+            ref, scale = orc.mv(Ob, x)
+            g9.tbmv(P, x, K, uplo=uplo, trans=tr, diag=dg)
+            assert_close("tbmv " + label, x, ref, scale, tol)
+            x = strided(rng, n, dt, 1)
+            ref, scale = orc.mv(Op, x)
+            g9.tpmv(Ap, x, uplo=uplo, trans=tr, diag=dg)
+            assert_close("tpmv " + label, x, ref, scale, tol)
+            # solves: well conditioned (small off-diagonal entries, diagonal 1..2)
+            Ts = T / max(K, 1) / 4
+            np.fill_diagonal(Ts, 1 + np.abs(np.diag(T)))
+            Ps = band_store(Ts, KL, KU).astype(dt)
+            Os = orc.triangle(orc.band_dense(Ps, n, n, KL, KU), uplo, dg)
+            b = strided(rng, n, dt, 2)
+            ref = orc.solve(Os.T if tr else Os, f64(b))
+            g9.tbsv(Ps, b, K, uplo=uplo, trans=tr, diag=dg)
+            assert_close("tbsv " + label, b, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+            Tq = Tp / n
+            np.fill_diagonal(Tq, 1 + np.abs(np.diag(Tp)))
+            Aq = packed_store(Tq, uplo).astype(dt)
+            Oq = orc.triangle(orc.packed_dense(Aq, n, uplo), uplo, dg)
+            b = strided(rng, n, dt, -1)
+            ref = orc.solve(Oq.T if tr else Oq, f64(b))
+            g9.tpsv(Aq, b, uplo=uplo, trans=tr, diag=dg)
+            assert_close("tpsv " + label, b, ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
         xs, ys = strided(rng, n, dt, 1), strided(rng, n, dt, -2)
         X, Y = f64(xs), f64(ys)
         Ap1 = Ap.copy()
