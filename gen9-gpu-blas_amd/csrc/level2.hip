@@ -715,15 +715,17 @@ __global__ void __launch_bounds__(NT) solve_step(Shape s, const T *__restrict__ 
 
 // ---------------- inverse-based solve (full storage) ----------------
 // In solve order (index g is row g of A forward, n − 1 − g backward, so op(A) becomes lower triangular) the order
-// is cut into blocks of IB rows, q = 0 .. nbI − 1, the last one partial. The diagonal blocks D_q are inverted up
-// front, all at once: their 128-row diagonal blocks in FP64 (one launch), and for IB = 256 the lower-left quadrant
-// −inv(D₂)·C·inv(D₁) by two batched GEMMs; one more batched GEMM forms E_q = inv(D_q)·C_q, C_q being the block of
-// op(A) that couples block q to block q − 1. Step q is x_q = inv(D_q)·r_q − E_q·x_{q−1}, r_q being block q's
-// right-hand side after the updates of blocks ≤ q − 2: two IB × IB matrix-vector products, split over IB / 16
-// workgroups of 16 rows with no synchronisation between them, while the launch's other workgroups apply x_{q−1}
-// to the rows beyond block q (the one-block look-ahead of solve_step). The chain per block is a launch, the loads of
-// 16 rows of inv(D_q) and E_q and a 16-lane sum, where solve_step has the diagonal block's loads, its right-hand
-// side and a 128-step substitution. The solution goes to a second vector xs, since the solving workgroups read r_q
+// is cut into blocks of IB rows (256 below order INV_BIG, 512 from there), q = 0 .. nbI − 1, the last one partial.
+// The diagonal blocks D_q are inverted up front, all at once: their 128-row diagonal blocks in FP64 (one launch),
+// then level by level the lower-left quadrants −inv(D₂)·C·inv(D₁) of the sub-blocks of 256 (and 512) rows by two
+// batched GEMMs per level; one more batched GEMM forms E_q = inv(D_q)·C_q, C_q being the block of op(A) that couples
+// block q to block q − 1. Step q is x_q = inv(D_q)·r_q − E_q·x_{q−1}, r_q being block q's right-hand side after the
+// updates of blocks ≤ q − 2: two IB × IB matrix-vector products, split over IB / INV_ROWS workgroups (16 rows of 16
+// lanes, or for IB = 512 4 rows of 64 lanes, so that each workgroup loads 32 KiB of FP32) with no synchronisation
+// between them, while the launch's other workgroups apply x_{q−1} to the rows beyond block q (the one-block
+// look-ahead of solve_step). The chain per block is a launch, the loads of the rows of inv(D_q) and E_q and a sum
+// across each row's lanes, where solve_step has the diagonal block's loads, its right-hand side and a 128-step
+// substitution. The solution goes to a second vector xs, since the solving workgroups read r_q
 // from xf while others write x_q. The reference substitutes (level12.c:303-347, level12.cl:493-548); the results
 // differ from substitution by rounding only.
 // Sum over each row of 16 lanes, left in every lane of the row, by DPP moves (quad_perm [1,0,3,2] and [2,3,0,1],
@@ -755,8 +757,14 @@ __device__ __forceinline__ double row16_sum(double v) {
 // 96 (op(A) = A / Aᵀ) against 99; n = 1280 101 / 120 against 103; n = 1536 120 / 144 against 108; n = 2048 160 / 193
 // against 118.
 constexpr int INV_MIN = 1280;
-constexpr int INV_IB = 256;     // rows per block
-constexpr int INV_ROWS = 16;    // rows of x_q per solving workgroup
+// From this order on, blocks of 512 rows: half the dependent launches for a larger set-up (E_q of 512², one more
+// composition level). MI355X, µs per call, op(A) = A / Aᵀ, 512 against 256 rows: FP32 n = 2048 115 / 117 against
+// 103 / 103, n = 4096 131 / 136 against 137 / 136, n = 8192 179 / 187 against 209 / 206, n = 16384 400 / 398 against
+// 427 / 396; FP64 n = 4096 131 / 133 against 138 / 138, n = 8192 176 / 174 against 207 / 203.
+constexpr int INV_BIG = 4096;
+// Rows of x_q per solving workgroup: each loads 32 KiB of FP32 (the IB = 512 step with 8 or 16 rows per workgroup
+// loads 64-128 KiB in each: FP32 n = 16384 op(A) = A 413 and 466 µs against 400 with 4)
+template <int IB> constexpr int INV_ROWS = IB == 256 ? 16 : 4;
 
 // 128 × 128 tiles of D_q and C_q, in solve order, into Dg + q·IB·(IB + 1) and Cg + q·IB² (row stride IB; D_q's
 // stride puts element (i, j) of the blocks' rows and columns, counted from block 0, at Dg[i·IB + j]), zero padded: past the
@@ -887,28 +895,29 @@ __device__ __forceinline__ void upd_cols_full(const Shape &s, const T *__restric
 }
 
 // Step q of the inverse-based solve: block q covers rows [p, p + b) of A, block q − 1 rows [pp, pp + pb) (pb = 0:
-// the first step). Workgroups 0 .. IB / 16 − 1 form 16 rows each of x_q = Di·r_q − Eq·x_{q−1} (16 lanes per row, IB /
-// 16 columns per lane, then a fixed-order butterfly over the 16 lanes) into xs; the others apply x_{q−1} (in xs) to
-// rows [o0, o1) of xf.
+// the first step). Workgroups 0 .. IB / ROWS − 1 form ROWS rows each of x_q = Di·r_q − Eq·x_{q−1} (L = 256 / ROWS
+// lanes per row, IB / L columns per lane, then a fixed-order sum over the row's lanes) into xs; the others apply
+// x_{q−1} (in xs) to rows [o0, o1) of xf.
 template <class T, int IB>
 __global__ void __launch_bounds__(NT) inv_step(Shape s, const T *__restrict__ a, int trans, int fwd, int pp, int pb, int p,
                                                int b, int o0, int o1, const typename Comp<T>::R *__restrict__ Di,
                                                const typename Comp<T>::R *__restrict__ Eq, typename Comp<T>::R *xf,
                                                typename Comp<T>::R *xs) {
     using R = typename Comp<T>::R;
-    constexpr int WGS = IB / INV_ROWS, L = NT / INV_ROWS, CPL = IB / L;   // solving workgroups, lanes per row, columns per lane
-    static_assert(L == 16 && CPL % 4 == 0, "16 lanes per row, whole 4-column chunks");
+    constexpr int ROWS = INV_ROWS<IB>;
+    constexpr int WGS = IB / ROWS, L = NT / ROWS, CPL = IB / L;   // solving workgroups, lanes per row, columns per lane
+    static_assert(L >= 16 && L <= 64 && CPL % 4 == 0, "16 to 64 lanes per row, whole 4-column chunks");
     __shared__ R red[NT / 64][64];
     if (blockIdx.x >= WGS) {
         if (trans) upd_cols_full<T, IB>(s, a, pp, o0, o1, xf, xs, blockIdx.x - WGS, red);
         else upd_rows_full<T, IB>(s, a, pp, o0, o1, xf, xs, blockIdx.x - WGS);
         return;
     }
-    // lane l of a row takes columns 64j + 4l .. 64j + 4l + 3: the 16 lanes of a row read 256 contiguous bytes of
+    // lane l of a row takes columns 4Lj + 4l .. 4Lj + 4l + 3: the L lanes of a row read 16·L contiguous bytes of
     // inv(D_q) and E_q per load
     typedef R R4 __attribute__((ext_vector_type(4)));
     constexpr int NJ = CPL / 4;
-    const int k = blockIdx.x * INV_ROWS + threadIdx.x / L, l = threadIdx.x % L;
+    const int k = blockIdx.x * ROWS + threadIdx.x / L, l = threadIdx.x % L;
     R4 dv[NJ], ev[NJ];
     R rv[NJ][4], xv[NJ][4];
 #pragma unroll
@@ -938,6 +947,8 @@ __global__ void __launch_bounds__(NT) inv_step(Shape s, const T *__restrict__ a,
             for (int i = 0; i < 4; i++) t = fma_r(-ev[j][i], xv[j][i], t);
     }
     t = row16_sum(t);
+#pragma unroll
+    for (int d = 16; d < L; d *= 2) t += __shfl_xor(t, d);   // rows of 32 or 64 lanes: the 16-lane sums, in lane order
     if (threadIdx.x % L == 0 && k < b) xs[fwd ? p + k : p + b - 1 - k] = t;
 }
 
@@ -1047,15 +1058,15 @@ static int launch_rank(int es, int fmt, const Shape &s, double alpha, const void
 // Work space of the inverse-based solve for order n: the solution vector, then D (later E) and the inverses, nbI·IB·
 // (IB + 1) each, C, nbI·IB², and the products of the compositions, at most nbI·IB²/4.
 template <class R>
-static size_t inv_bytes(int n) {
-    const size_t nbI = (size_t)(n + INV_IB - 1) / INV_IB, m2 = (size_t)INV_IB * INV_IB, sd = m2 + INV_IB;
+static size_t inv_bytes(int n, int ib) {
+    const size_t nbI = (size_t)(n + ib - 1) / ib, m2 = (size_t)ib * ib, sd = m2 + ib;
     return (((size_t)n * sizeof(R) + 255) & ~(size_t)255) + (2 * nbI * sd + nbI * m2 + nbI * m2 / 4) * sizeof(R);
 }
 // The inverse-based solve of full storage (inv_gather, inv_step) in the work space w (inv_bytes).
-template <class T>
+template <class T, int IB>
 static int solve_inv(const Shape &s, const T *a, int trans, int fwd, typename Comp<T>::R *xf, void *w) {
     using R = typename Comp<T>::R;
-    constexpr int IB = INV_IB, QB = IB / SB;
+    constexpr int QB = IB / SB;
     const int n = s.nrows, nbI = (n + IB - 1) / IB, type = sizeof(R) == 8 ? GEN9BLAS_D : GEN9BLAS_S;
     // D_q and inv(D_q) at stride sd = IB·(IB + 1), so that the sub-blocks of 2h rows of every level of the composition
     // below start at the uniform stride 2h·(IB + 1); C_q and E_q (which reuses D's space) at stride IB²
@@ -1103,7 +1114,7 @@ static int solve_inv(const Shape &s, const T *a, int trans, int fwd, typename Co
             o0 = fwd ? p + b : 0;
             o1 = fwd ? n : p;
         }
-        const unsigned grid = IB / INV_ROWS + (o1 > o0 ? blocks(o1 - o0, per) : 0u);
+        const unsigned grid = IB / INV_ROWS<IB> + (o1 > o0 ? blocks(o1 - o0, per) : 0u);
         hipLaunchKernelGGL((inv_step<T, IB>), dim3(grid), dim3(NT), 0, stream, s, a, trans, fwd, pp, pb, p, b, o0, o1,
                            Di + q * sd, E + q * m2, xf, xs);
         G9_HIP(hipGetLastError());
@@ -1118,15 +1129,16 @@ static int launch_solve(int es, int fmt, const Shape &s, const void *a, int tran
         using T = std::remove_pointer_t<decltype(tag)>;
         using R = typename Comp<T>::R;
         const int n = s.nrows, nb = (n + SB - 1) / SB;
-        const bool inv = fmt == F_FULL && n >= INV_MIN;
+        const bool inv = fmt == F_FULL && n >= INV_MIN, big = n >= INV_BIG;
         void *wp, *w2 = nullptr;
         G9_TRY(scratch(SLOT_T, (size_t)n * sizeof(R), &wp));
-        if (inv) G9_TRY(scratch(SLOT_X, inv_bytes<R>(n), &w2));
+        if (inv) G9_TRY(scratch(SLOT_X, inv_bytes<R>(n, big ? 512 : 256), &w2));
         R *xf = (R *)wp;
         hipLaunchKernelGGL((to_work<T, R>), dim3(blocks(n, NT)), dim3(NT), 0, stream, n, (const T *)x, ix, xf);
         G9_HIP(hipGetLastError());
         if (inv) {
-            G9_TRY(solve_inv<T>(s, (const T *)a, trans, lower, xf, w2));
+            G9_TRY((big ? solve_inv<T, 512>(s, (const T *)a, trans, lower, xf, w2)
+                        : solve_inv<T, 256>(s, (const T *)a, trans, lower, xf, w2)));
             hipLaunchKernelGGL((from_work<T, R>), dim3(blocks(n, NT)), dim3(NT), 0, stream, n, (const R *)w2, (T *)x, ix);
             G9_HIP(hipGetLastError());
             return 0;

@@ -113,11 +113,13 @@ def test_full_storage_unreferenced_nan(g9, orc, dt, n):
 
 
 @pytest.mark.parametrize("dt", DTYPES)
-@pytest.mark.parametrize("n", [1280, 1300, 4100])
+@pytest.mark.parametrize("n", [1280, 1300, 4095, 4096, 4100])
 def test_trsv_blocked_inverse(g9, orc, dt, n):
-    """TRSV from order 1280 up runs on inverted 256-row diagonal blocks (x_q = inv(D_q)·r_q − E_q·x_(q-1), inverses in
-    FP64): n = 1280 is the smallest such order (5 whole blocks), n = 1300 ends on a partial block of 20 rows (the
-    last in solve order, at the start of A for a backward solve), n = 4100 on one of 4 rows after 16 whole blocks. Both triangles, both transposes, unit and stored
+    """TRSV from order 1280 up runs on inverted diagonal blocks (x_q = inv(D_q)·r_q − E_q·x_(q-1), inverses in FP64),
+    of 256 rows below order 4096 and of 512 rows from there: n = 1280 is the smallest such order (5 whole blocks),
+    n = 1300 ends on a partial block of 20 rows (the last in solve order, at the start of A for a backward solve),
+    n = 4095 is the largest order on 256-row blocks (16, the last one row short), n = 4096 the smallest on 512-row
+    blocks (8 whole ones), n = 4100 ends on one of 4 rows after them. Both triangles, both transposes, unit and stored
     diagonals, a negative-stride x, and the unreferenced triangle (and a unit diagonal) filled with huge values, which
     must not be read into the result."""
     A = rng.uniform(-1, 1, (n, n)).astype(dt)
@@ -150,13 +152,14 @@ def _backward_bound(dt, n):
 
 
 @pytest.mark.parametrize("dt", DTYPES)
-@pytest.mark.parametrize("n", [1000, 1280, 1300])
+@pytest.mark.parametrize("n", [1000, 1280, 1300, 4500])
 def test_trsv_not_dominant(g9, orc, dt, n):
     """Triangles that are not diagonally dominant: off-diagonal entries uniform(−1, 1)/√n (row sums of |T| near
     √n/2, far above the diagonal), unit or stored diagonal of magnitude 1..2. The solution stays bounded (its
     variance grows by at most (1 + 1/n)^n ≈ e), but the solve is no longer well conditioned entry by entry, so the
-    check is the normwise backward error. n = 1000 takes the substitution, 1280 and 1300 the inverted 256-row blocks
-    (whose off-diagonal couplings are work-precision products): both meet the same bound."""
+    check is the normwise backward error. n = 1000 takes the substitution, 1280 and 1300 the inverted 256-row blocks,
+    4500 the 512-row blocks (8 whole ones and one of 404 rows), whose off-diagonal couplings are work-precision
+    products: all meet the same bound."""
     r = np.random.default_rng(n + 3 * DTYPES.index(dt))
     A = (r.uniform(-1, 1, (n, n)) / np.sqrt(n))
     d = r.uniform(-1, 1, n)
