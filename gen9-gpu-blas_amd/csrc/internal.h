@@ -135,9 +135,9 @@ G9_HIDDEN int launch_gemm_klim(const GemmCall &c, int klim);
 // Inverses, computed in FP64 (level3.hip), of the `count` 128-row diagonal blocks of lower-triangular leaves of lb
 // rows (lb a multiple of 128): leaf p's element (i, j) at L[p·bstride + i·ld + j]; the inverses go to leaf p at
 // Inv + p·istride (row stride lb), with zeros right of each block's inverse to the end of its leaf; es 4 (float) or
-// 8 (double).
+// 8 (double). Each block's entries above its diagonal are read as zeros, and with `unit` its diagonal as ones.
 G9_HIDDEN int launch_tri_inverse(int es, const void *L, long long ld, long long bstride, int count, void *Inv, int lb,
-                                 long long istride);
+                                 long long istride, int unit);
 // The whole gen9blas_gemm_batched call: checks, operand resolution, skinny / MFMA dispatch, wait (gemm.hip).
 G9_HIDDEN int gemm_impl(int type, int tA, int tB, int M, int N, int K, double alpha, const void *A, int lda, long long sA,
                         const void *B, int ldb, long long sB, double beta, void *C, int ldc, long long sC, int count);

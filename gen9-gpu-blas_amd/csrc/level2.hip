@@ -1078,10 +1078,20 @@ static int solve_inv(const Shape &s, const T *a, int trans, int fwd, typename Co
     R *xs = (R *)w;
     R *D = (R *)((char *)w + (((size_t)n * sizeof(R) + 255) & ~(size_t)255));
     R *Di = D + nbI * sd, *C = Di + nbI * sd, *Tm = C + nbI * m2, *E = D;
-    hipLaunchKernelGGL((inv_gather<T, IB>), dim3(nbI, 2 * QB * QB), dim3(NT), 0, stream, s, a, trans, fwd, D, C);
-    G9_HIP(hipGetLastError());
-    // the 128-row diagonal blocks of every D_q, in FP64, into their places in inv(D_q) (zeros right of them)
-    G9_TRY(launch_tri_inverse((int)sizeof(R), D, IB, sd, nbI * QB, Di, IB, sd));
+    // A forward solve on A itself (lower, not transposed) in the work precision, with whole blocks, reads D_q, the
+    // quadrants below its diagonal and C_q where they lie in A, at the uniform strides of its diagonal (no gather);
+    // every other case gathers them in solve order first (transposing, reversing, converting, padding)
+    const bool direct = std::is_same<T, R>::value && !trans && fwd && n % IB == 0;
+    const R *Ad = reinterpret_cast<const R *>(a);
+    const ll lda = s.ld;
+    if (direct) {
+        G9_TRY(launch_tri_inverse((int)sizeof(R), Ad, lda, IB * (lda + 1), nbI * QB, Di, IB, sd, s.unit));
+    } else {
+        hipLaunchKernelGGL((inv_gather<T, IB>), dim3(nbI, 2 * QB * QB), dim3(NT), 0, stream, s, a, trans, fwd, D, C);
+        G9_HIP(hipGetLastError());
+        // the 128-row diagonal blocks of every D_q, in FP64, into their places in inv(D_q) (zeros right of them)
+        G9_TRY(launch_tri_inverse((int)sizeof(R), D, IB, sd, nbI * QB, Di, IB, sd, 0));
+    }
     // count products C_z = alpha·A_z·B_z of M × K by K × N, (row stride, batch stride) of each operand given; klim: A
     // is lower triangular and each tile takes only the k range where it is non-zero
     const auto gemm = [&](int M, int N, int K, double alpha, const R *A, ll lda, ll sA, const R *B, ll ldb, ll sB, R *Cp,
@@ -1103,11 +1113,21 @@ static int solve_inv(const Shape &s, const T *a, int trans, int fwd, typename Co
     for (ll h = SB; h < IB; h *= 2) {
         const int cnt = (int)(nbI * (IB / (2 * h)));
         const ll st = 2 * h * (IB + 1), t2 = h * h;
-        G9_TRY(gemm((int)h, (int)h, (int)h, 1.0, Di + h * (IB + 1), IB, st, D + h * IB, IB, st, Tm, h, t2, cnt));
+        if (direct)   // the sub-blocks' lower-left quadrants at A + 2hk·(lda + 1) + h·lda
+            G9_TRY(gemm((int)h, (int)h, (int)h, 1.0, Di + h * (IB + 1), IB, st, Ad + h * lda, lda, 2 * h * (lda + 1), Tm,
+                        h, t2, cnt));
+        else
+            G9_TRY(gemm((int)h, (int)h, (int)h, 1.0, Di + h * (IB + 1), IB, st, D + h * IB, IB, st, Tm, h, t2, cnt));
         G9_TRY(gemm((int)h, (int)h, (int)h, -1.0, Tm, h, t2, Di, IB, st, Di + h * IB, IB, st, cnt));
     }
     // E_q = inv(D_q)·C_q, q ≥ 1, each tile over the k range where inv(D_q) is non-zero (256³ × 63 FP32: 27.9 → 24.8 µs)
-    if (nbI > 1) G9_TRY(gemm(IB, IB, IB, 1.0, Di + sd, IB, sd, C + m2, IB, m2, E + m2, IB, m2, nbI - 1, true));
+    if (nbI > 1) {
+        if (direct)   // C_q = A[q·IB .., (q − 1)·IB ..]: from A + IB·lda at the stride IB·(lda + 1)
+            G9_TRY(gemm(IB, IB, IB, 1.0, Di + sd, IB, sd, Ad + IB * lda, lda, IB * (lda + 1), E + m2, IB, m2, nbI - 1,
+                        true));
+        else
+            G9_TRY(gemm(IB, IB, IB, 1.0, Di + sd, IB, sd, C + m2, IB, m2, E + m2, IB, m2, nbI - 1, true));
+    }
     const int per = trans ? UPD_COLS : UPD_ROWS;
     for (int q = 0; q < nbI; q++) {
         const int g0 = q * IB, b = n - g0 < IB ? n - g0 : IB, p = fwd ? g0 : n - g0 - b;

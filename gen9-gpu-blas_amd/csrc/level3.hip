@@ -388,15 +388,15 @@ static int tri_product(int type, int lower, int trans, int N, int K, double alph
 // p's element (i, j) at L[p·bstride + i·ld + j] (es 4: float, 8: double); inverses into Inv as trsm_inv_kernel
 // places them (leaf p at Inv + p·istride, row stride lb, zeros right of each block's inverse to the end of its leaf).
 int launch_tri_inverse(int es, const void *L, long long ld, long long bstride, int count, void *Inv, int lb,
-                       long long istride) {
+                       long long istride, int unit) {
     using namespace l3;
     const int n = count * TRSM_NB;
     if (es == 8)
         hipLaunchKernelGGL((trsm_inv_kernel<double>), dim3(count), dim3(256), 0, stream, (const double *)L, (ll)ld,
-                           (ll)bstride, n, (double *)Inv, lb, (ll)istride, 0);
+                           (ll)bstride, n, (double *)Inv, lb, (ll)istride, unit);
     else
         hipLaunchKernelGGL((trsm_inv_kernel<float>), dim3(count), dim3(256), 0, stream, (const float *)L, (ll)ld,
-                           (ll)bstride, n, (float *)Inv, lb, (ll)istride, 0);
+                           (ll)bstride, n, (float *)Inv, lb, (ll)istride, unit);
     G9_HIP(hipGetLastError());
     return 0;
 }
