@@ -135,8 +135,10 @@ __global__ void __launch_bounds__(256) trsm_store_kernel(const T *Y, T *B, ll ld
 }
 
 constexpr int TRSM_NB = 128;
-// rows of a leaf (an inverted diagonal block applied by one product) of the FP32 / FP64 solve
-constexpr int TRSM_LEAF = 512;
+// rows of a leaf (an inverted diagonal block applied by one product) of the FP32 and the FP64 solve: one more
+// composition level and half the leaves for FP64 (n = 4096 left lower, MI355X: 1.427 -> 1.412 ms with 1024 rows
+// against 512; FP32 stays at 512: 0.729 against 0.823 ms when measured)
+constexpr int TRSM_LEAF_S = 512, TRSM_LEAF_D = 1024;
 // Inverse of the diagonal block bi of L (rows and columns r0 .. r0+b-1, b ≤ TRSM_NB, in the leaf p = r0 / lb of lb
 // rows whose element (i, j) is at L[p·bstride + i·ld + j]; the block's entries above the diagonal are read as zeros,
 // and its diagonal as ones when unit),
@@ -311,7 +313,7 @@ static int dgemm_dev(int type, int tA, int tB, int M, int N, int K, double alpha
 
 // Blocked forward substitution L·X = alpha·Y (L n×n lower, Y and X n×m, row strides ldl, ldy and m; alpha is applied
 // by the first product that touches each block of rows of Y, or is 1 when Y already holds alpha·R) over diagonal blocks of lb
-// rows (TRSM_LEAF for FP32 / FP64, 128 for FP16), by recursive halving: the first half of a block range is solved, one
+// rows (TRSM_LEAF_S / TRSM_LEAF_D for FP32 / FP64, 128 for FP16), by recursive halving: the first half of a block range is solved, one
 // GEMM then subtracts its contribution from the right-hand side of the second half, Y[i1..i2) -= L[i1..i2, i0..i1)·
 // X[i0..i1), and the second half is solved. A single block is X_i = inv(L_ii)·Y_i with the block's inverse (128-row
 // inverses computed in FP64, larger ones composed from them; element (i, j) of the inverses at Iv[i·lb + j]), a product
@@ -551,9 +553,9 @@ int gen9blas_trsm(int type, int side, int uplo, int transA, int diag, int M, int
     // L·Y = alpha·R: op'(A) = left ? op(A) : op(A)ᵀ; lower when the triangle of A, transposed or not, is lower
     const int tr = left ? transA != 0 : transA == 0;
     const int lower = (uplo == GEN9BLAS_LOWER) != (tr != 0), rev = !lower;
-    // Leaves of TRSM_LEAF rows for FP32 / FP64: each leaf inverse is composed from the 128-row FP64 inverses (below);
+    // Leaves of TRSM_LEAF_S / _D rows for FP32 / FP64: each leaf inverse is composed from the 128-row FP64 inverses (below);
     // FP16 keeps 128-row leaves (the composition would round once more in FP16)
-    const int nbl = (n + TRSM_NB - 1) / TRSM_NB, lb = es >= 4 ? TRSM_LEAF : TRSM_NB, nleaf = (n + lb - 1) / lb;
+    const int nbl = (n + TRSM_NB - 1) / TRSM_NB, lb = es == 8 ? TRSM_LEAF_D : es == 4 ? TRSM_LEAF_S : TRSM_NB, nleaf = (n + lb - 1) / lb;
     // A left solve with A lower and not transposed reads both operands where they lie: every product below reads L
     // strictly below its diagonal blocks, the block inversion masks the rest of A itself, B is the right-hand side
     // updated in place (alpha applied by the first product that touches each block of rows), and only the solution
