@@ -260,6 +260,40 @@ def test_band_packed(g9, orc, dt, n, K):
               packed_store(np.abs(Tp) + 0.25 * (np.outer(np.abs(X), np.abs(Y)) + np.outer(np.abs(Y), np.abs(X))), uplo), tol)
 
 
+def test_trsv_blocks_read_in_place(g9, orc, torch_dev):
+    """The forward solve on A itself (uplo L, not transposed, FP32 / FP64, whole blocks of 256 or 512 rows) reads the
+    diagonal blocks, their lower-left quadrants and the couplings where they lie in A: 16 seeded cases on device
+    views with a row stride of n + 0..8, unit and stored diagonals, and huge values in the unreferenced triangle (and
+    on a unit diagonal) that must not reach the result; every fourth case another triangle or transpose (gathered)."""
+    torch = torch_dev
+    r = np.random.default_rng(2024)
+    big = {np.float32: 1e30, np.float64: 1e300}
+    for c in range(16):
+        dt = (np.float32, np.float64)[c % 2]
+        n = int(r.choice([1280, 1536, 2048, 4096, 4608]))
+        pad = int(r.integers(0, 9))
+        other_case = c % 4 == 3
+        uplo = "LU"[int(r.integers(0, 2))] if other_case else "L"
+        trans = bool(r.integers(0, 2)) if other_case else False
+        diag = bool(r.integers(0, 2))
+        A = dominant_triangle(r.uniform(-1, 1, (n, n)), diag).astype(dt)
+        Ab = A.copy()
+        Ab[np.triu_indices(n, 1) if uplo == "L" else np.tril_indices(n, -1)] = big[dt]
+        if diag:
+            np.fill_diagonal(Ab, big[dt])
+        base = r.uniform(-1, 1, (n, n + pad)).astype(dt)
+        base[:, :n] = Ab
+        Ob = orc.triangle(f64(A), uplo, diag)
+        Ob = Ob.T if trans else Ob
+        b = r.uniform(-1, 1, n).astype(dt)
+        ref = orc.solve(Ob, f64(b))
+        Ad = torch.from_numpy(base).cuda()[:, :n]
+        bd = torch.from_numpy(b).cuda()
+        g9.trsv(Ad, bd, uplo=uplo, trans=trans, diag=diag)
+        assert_close(f"trsv case {c} {np.dtype(dt).name} n={n} ld={n + pad} {uplo} trans={int(trans)} diag={int(diag)}",
+                     bd.cpu().numpy(), ref, np.max(np.abs(ref)), SOLVE_TOL[dt])
+
+
 @pytest.mark.parametrize("dt", [np.float32, np.float64])
 @pytest.mark.parametrize("odd_ld", [False, True])
 def test_level2_device_n4096(g9, orc, torch_dev, dt, odd_ld):
